@@ -1,0 +1,437 @@
+// C ABI of the MoE engine (declared in include/aps_moe.h).
+//
+// Host-side replacement of the reference's launch layer for this path:
+// register_moe_weights_gpu / moe_forward_grouped_gpu (src/tensor.cu:2757-2928)
+// and the router call of PhiMoE::forward (src/layer.cu:113-121).  Differences
+// by design:
+//  * weights are packed once into kernel-native layouts owned by the library
+//    (the reference keeps pointers to the caller's fp32 tensors);
+//  * all scratch comes from a caller-provided workspace, so a forward call
+//    performs no allocation and no host synchronisation;
+//  * errors are status codes plus a thread-local message instead of C++
+//    exceptions crossing the ABI.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/aps_moe.h"
+#include "common.hpp"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t err, const char* what) {
+    return fail(APS_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+#define APS_HIP(call, what)                                 \
+    do {                                                    \
+        hipError_t err_ = (call);                           \
+        if (err_ != hipSuccess) return hip_fail(err_, what); \
+    } while (0)
+
+struct WeightSet {
+    int device = 0;
+    int E = 0, H = 0, F = 0;
+    int compute = APS_DTYPE_F32;
+    // bf16 path
+    aps::bf16_t* w13 = nullptr;  // [E][F/64][128][H]
+    aps::bf16_t* w2b = nullptr;  // [E][H][F]
+    // f32 path
+    float* w1 = nullptr;         // [E][F][H]
+    float* w3 = nullptr;         // [E][F][H]
+    float* w2 = nullptr;         // [E][H][F]
+    ~WeightSet() {
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        if (cur != device) (void)hipSetDevice(device);
+        for (void* p : {static_cast<void*>(w13), static_cast<void*>(w2b), static_cast<void*>(w1),
+                        static_cast<void*>(w3), static_cast<void*>(w2)})
+            if (p) (void)hipFree(p);
+        if (cur != device) (void)hipSetDevice(cur);
+    }
+};
+
+std::mutex g_mu;
+std::vector<std::unique_ptr<WeightSet>> g_sets;  // handle h -> g_sets[h-1]
+
+WeightSet* lookup(uint64_t handle) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (handle == 0 || handle > g_sets.size()) return nullptr;
+    return g_sets[handle - 1].get();
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+int dtype_size(int dt) {
+    switch (dt) {
+        case APS_DTYPE_F32: return 4;
+        case APS_DTYPE_BF16: return 2;
+        case APS_DTYPE_E4M3: return 1;
+        default: return 0;
+    }
+}
+
+void make_layout(const WeightSet& w, int64_t rows, aps_moe_ws_layout* L) {
+    std::memset(L, 0, sizeof(*L));
+    const size_t T = static_cast<size_t>(rows);
+    const size_t E = static_cast<size_t>(w.E);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off = align_up(off + bytes);
+        return at;
+    };
+    const size_t elt = w.compute == APS_DTYPE_F32 ? 4 : 2;
+    L->logits = take(T * E * 4);
+    L->routes = take(T * 2);
+    L->tile_counts = take(static_cast<size_t>(aps::ceil_div(rows, aps::kTileTokens)) * E * 4);
+    L->counts = take(E * 4);
+    L->offsets = take((E + 1) * 4);
+    L->assignment_rows = take(2 * T * 4);
+    L->route_positions = take(2 * T * 4);
+    L->act = take(2 * T * static_cast<size_t>(w.F) * elt);
+    L->act_scale = 0;
+    L->y = take(2 * T * static_cast<size_t>(w.H) * elt);
+    L->xq = 0;
+    L->xq_scale = 0;
+    L->total_bytes = off;
+}
+
+int check_device(const WeightSet& w) {
+    int cur = 0;
+    APS_HIP(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != w.device)
+        return fail(APS_ERR_ARG, "weight set lives on device %d but device %d is current", w.device, cur);
+    return APS_OK;
+}
+
+// The two grouped GEMMs of the expert FFN over a filled routing plan
+// (offsets, assignment_rows).  Shared by every entry point that runs them.
+int run_ffn_up(const WeightSet& w, const void* x, int64_t rows, const uint32_t* offsets,
+               const uint32_t* arows, void* act, hipStream_t s) {
+    if (w.compute == APS_DTYPE_F32)
+        APS_HIP(aps::launch_ffn_up_f32(static_cast<const float*>(x), offsets, arows, w.w1, w.w3,
+                                       static_cast<float*>(act), rows, w.H, w.F, w.E, s),
+                "ffn_up_f32 launch");
+    else
+        APS_HIP(aps::launch_ffn_up_bf16(static_cast<const aps::bf16_t*>(x), offsets, arows, w.w13,
+                                        static_cast<aps::bf16_t*>(act), rows, w.H, w.F, w.E, s),
+                "ffn_up_bf16 launch");
+    return APS_OK;
+}
+
+int run_ffn_down(const WeightSet& w, const void* act, int64_t rows, const uint32_t* offsets, void* y,
+                 hipStream_t s) {
+    if (w.compute == APS_DTYPE_F32)
+        APS_HIP(aps::launch_ffn_down_f32(static_cast<const float*>(act), offsets, w.w2,
+                                         static_cast<float*>(y), rows, w.H, w.F, w.E, s),
+                "ffn_down_f32 launch");
+    else
+        APS_HIP(aps::launch_ffn_down_bf16(static_cast<const aps::bf16_t*>(act), offsets, w.w2b,
+                                          static_cast<aps::bf16_t*>(y), rows, w.H, w.F, w.E, s),
+                "ffn_down_bf16 launch");
+    return APS_OK;
+}
+
+int run_ffn(const WeightSet& w, const void* x, int64_t rows, const uint32_t* offsets,
+            const uint32_t* arows, void* act, void* y, hipStream_t s) {
+    if (int rc = run_ffn_up(w, x, rows, offsets, arows, act, s)) return rc;
+    return run_ffn_down(w, act, rows, offsets, y, s);
+}
+
+int check_x_dtype(const WeightSet& w, int32_t x_dtype) {
+    const int want = w.compute == APS_DTYPE_F32 ? APS_DTYPE_F32 : APS_DTYPE_BF16;
+    if (x_dtype != want)
+        return fail(APS_ERR_DTYPE, "x dtype %d does not match the weight set (expects %d)", x_dtype, want);
+    return APS_OK;
+}
+
+int grouped_from_logits(const WeightSet& w, const void* x, const float* logits, int64_t rows,
+                        void* out, int32_t out_dtype, char* ws, const aps_moe_ws_layout& L,
+                        hipStream_t s) {
+    auto* routes = reinterpret_cast<uint8_t*>(ws + L.routes);
+    auto* tiles = reinterpret_cast<uint32_t*>(ws + L.tile_counts);
+    auto* counts = reinterpret_cast<uint32_t*>(ws + L.counts);
+    auto* offsets = reinterpret_cast<uint32_t*>(ws + L.offsets);
+    auto* arows = reinterpret_cast<uint32_t*>(ws + L.assignment_rows);
+    auto* rpos = reinterpret_cast<uint32_t*>(ws + L.route_positions);
+    APS_HIP(aps::launch_route_top2(logits, rows, w.E, routes, tiles, s), "route_top2 launch");
+    APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, w.E, counts, offsets, arows, rpos, s),
+            "dispatch launch");
+    int rc = run_ffn(w, x, rows, offsets, arows, ws + L.act, ws + L.y, s);
+    if (rc) return rc;
+    APS_HIP(aps::launch_combine(ws + L.y, w.compute != APS_DTYPE_F32, rpos, rows, w.H, out,
+                                out_dtype == APS_DTYPE_BF16, s),
+            "combine launch");
+    return APS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* aps_moe_last_error(void) { return g_error.c_str(); }
+int aps_moe_abi_version(void) { return APS_MOE_ABI_VERSION; }
+
+int aps_moe_weights_register(const aps_moe_weights_desc* d, void* stream, uint64_t* handle_out) {
+    if (!d || !handle_out) return fail(APS_ERR_ARG, "register: NULL descriptor or handle pointer");
+    *handle_out = 0;
+    // reference: "MoE weight table size" (src/tensor.cu:2761-2764)
+    if (d->num_experts < 2 || d->num_experts > aps::kMaxExperts)
+        return fail(APS_ERR_SHAPE, "MoE weight table size: %d experts (2..%d supported)",
+                    d->num_experts, aps::kMaxExperts);
+    if (d->hidden <= 0 || d->ffn <= 0 || d->hidden % 256 != 0 || d->ffn % 64 != 0)
+        return fail(APS_ERR_SHAPE, "hidden %d must be a multiple of 256 and ffn %d of 64",
+                    d->hidden, d->ffn);
+    if (!d->w1 || !d->w3 || !d->w2) return fail(APS_ERR_ARG, "register: NULL weight table");
+    for (int e = 0; e < d->num_experts; ++e)
+        if (!d->w1[e] || !d->w3[e] || !d->w2[e])
+            return fail(APS_ERR_ARG, "register: NULL weight pointer for expert %d", e);
+    if (d->compute_dtype == APS_DTYPE_F32) {
+        if (d->src_dtype != APS_DTYPE_F32)
+            return fail(APS_ERR_DTYPE, "fp32 compute needs fp32 source weights");
+    } else if (d->compute_dtype == APS_DTYPE_BF16) {
+        if (d->src_dtype != APS_DTYPE_F32 && d->src_dtype != APS_DTYPE_BF16)
+            return fail(APS_ERR_DTYPE, "bf16 compute needs fp32 or bf16 source weights");
+    } else {
+        return fail(APS_ERR_DTYPE, "compute dtype %d not supported", d->compute_dtype);
+    }
+
+    auto w = std::make_unique<WeightSet>();
+    APS_HIP(hipGetDevice(&w->device), "hipGetDevice");
+    w->E = d->num_experts;
+    w->H = d->hidden;
+    w->F = d->ffn;
+    w->compute = d->compute_dtype;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t fh = static_cast<size_t>(w->F) * w->H;
+    const size_t n = fh * w->E;
+    if (w->compute == APS_DTYPE_F32) {
+        APS_HIP(hipMalloc(&w->w1, n * 4), "hipMalloc w1");
+        APS_HIP(hipMalloc(&w->w3, n * 4), "hipMalloc w3");
+        APS_HIP(hipMalloc(&w->w2, n * 4), "hipMalloc w2");
+        for (int e = 0; e < w->E; ++e) {
+            APS_HIP(hipMemcpyAsync(w->w1 + e * fh, d->w1[e], fh * 4, hipMemcpyDeviceToDevice, s), "copy w1");
+            APS_HIP(hipMemcpyAsync(w->w3 + e * fh, d->w3[e], fh * 4, hipMemcpyDeviceToDevice, s), "copy w3");
+            APS_HIP(hipMemcpyAsync(w->w2 + e * fh, d->w2[e], fh * 4, hipMemcpyDeviceToDevice, s), "copy w2");
+        }
+    } else {
+        const bool src_bf16 = d->src_dtype == APS_DTYPE_BF16;
+        APS_HIP(hipMalloc(&w->w13, 2 * n * 2), "hipMalloc w13");
+        APS_HIP(hipMalloc(&w->w2b, n * 2), "hipMalloc w2");
+        APS_HIP(aps::launch_pack_w13_bf16(d->w1, d->w3, src_bf16, w->w13, w->E, w->F, w->H, s),
+                "pack w1/w3");
+        for (int e = 0; e < w->E; ++e) {
+            if (src_bf16)
+                APS_HIP(hipMemcpyAsync(w->w2b + e * fh, d->w2[e], fh * 2, hipMemcpyDeviceToDevice, s),
+                        "copy w2");
+            else
+                APS_HIP(aps::launch_convert_to_bf16(static_cast<const float*>(d->w2[e]), w->w2b + e * fh,
+                                                    static_cast<int64_t>(fh), s),
+                        "convert w2");
+        }
+    }
+    APS_HIP(hipStreamSynchronize(s), "register: synchronize");
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_sets.push_back(std::move(w));
+    *handle_out = g_sets.size();
+    return APS_OK;
+}
+
+int aps_moe_weights_release(uint64_t handle) {
+    std::unique_ptr<WeightSet> victim;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (handle == 0 || handle > g_sets.size() || !g_sets[handle - 1])
+            return fail(APS_ERR_HANDLE, "release: invalid handle %llu", (unsigned long long)handle);
+        victim = std::move(g_sets[handle - 1]);
+    }
+    (void)hipDeviceSynchronize();  // the set may still be in use by queued work
+    return APS_OK;
+}
+
+int aps_moe_workspace_layout(uint64_t handle, int64_t rows, aps_moe_ws_layout* out) {
+    const WeightSet* w = lookup(handle);
+    if (!w) return fail(APS_ERR_HANDLE, "grouped MoE shape or handle: invalid handle %llu",
+                        (unsigned long long)handle);
+    if (!out) return fail(APS_ERR_ARG, "workspace_layout: NULL output");
+    if (rows < 0 || rows > (int64_t(1) << 30)) return fail(APS_ERR_SHAPE, "rows %lld out of range", (long long)rows);
+    make_layout(*w, rows, out);
+    return APS_OK;
+}
+
+size_t aps_moe_dispatch_workspace_size(int64_t rows, int32_t num_experts) {
+    if (rows <= 0 || num_experts <= 0) return 0;
+    return static_cast<size_t>(aps::ceil_div(rows, aps::kTileTokens)) * num_experts * 4;
+}
+
+int aps_router_logits(const void* x, int32_t x_dtype, const float* gate, int64_t rows,
+                      int32_t hidden, int32_t num_experts, float* logits, void* stream) {
+    if (rows < 0 || hidden <= 0 || hidden % 256 != 0 || num_experts <= 0 || num_experts > aps::kMaxExperts)
+        return fail(APS_ERR_SHAPE, "matmul_transposed_gpu shape: rows %lld hidden %d experts %d",
+                    (long long)rows, hidden, num_experts);
+    if (x_dtype != APS_DTYPE_F32 && x_dtype != APS_DTYPE_BF16)
+        return fail(APS_ERR_DTYPE, "router x dtype %d not supported", x_dtype);
+    if (rows > 0 && (!x || !gate || !logits)) return fail(APS_ERR_ARG, "router: NULL pointer");
+    APS_HIP(aps::launch_router_logits(x, x_dtype == APS_DTYPE_BF16, gate, rows, hidden, num_experts,
+                                      logits, static_cast<hipStream_t>(stream)),
+            "router_logits launch");
+    return APS_OK;
+}
+
+int aps_moe_route_top2(const float* logits, int64_t rows, int32_t num_experts, uint8_t* routes,
+                       void* stream) {
+    if (rows < 0 || num_experts < 2 || num_experts > aps::kMaxExperts)
+        return fail(APS_ERR_SHAPE, "route_top2: rows %lld experts %d", (long long)rows, num_experts);
+    if (rows > 0 && (!logits || !routes)) return fail(APS_ERR_ARG, "route_top2: NULL pointer");
+    APS_HIP(aps::launch_route_top2(logits, rows, num_experts, routes, nullptr,
+                                   static_cast<hipStream_t>(stream)),
+            "route_top2 launch");
+    return APS_OK;
+}
+
+int aps_moe_dispatch(const uint8_t* routes, int64_t rows, int32_t num_experts, uint32_t* counts,
+                     uint32_t* offsets, uint32_t* assignment_rows, uint32_t* route_positions,
+                     void* scratch, size_t scratch_bytes, void* stream) {
+    if (rows < 0 || num_experts < 2 || num_experts > aps::kMaxExperts)
+        return fail(APS_ERR_SHAPE, "dispatch: rows %lld experts %d", (long long)rows, num_experts);
+    if (!counts || !offsets) return fail(APS_ERR_ARG, "dispatch: NULL counts/offsets");
+    if (rows > 0 && (!routes || !assignment_rows || !route_positions))
+        return fail(APS_ERR_ARG, "dispatch: NULL pointer");
+    const size_t need = aps_moe_dispatch_workspace_size(rows, num_experts);
+    if (need && (!scratch || scratch_bytes < need))
+        return fail(APS_ERR_WORKSPACE, "dispatch: scratch %zu bytes, need %zu", scratch_bytes, need);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto* tiles = static_cast<uint32_t*>(scratch);
+    APS_HIP(aps::launch_tile_hist(routes, rows, num_experts, tiles, s), "tile_hist launch");
+    APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, num_experts, counts, offsets,
+                                         assignment_rows, route_positions, s),
+            "dispatch launch");
+    return APS_OK;
+}
+
+int aps_moe_expert_ffn(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows,
+                       const uint32_t* offsets, const uint32_t* assignment_rows, void* act,
+                       float* act_scale, void* y_perm, void* stream) {
+    (void)act_scale;
+    const WeightSet* w = lookup(handle);
+    if (!w) return fail(APS_ERR_HANDLE, "grouped MoE shape or handle: invalid handle %llu",
+                        (unsigned long long)handle);
+    if (int rc = check_device(*w)) return rc;
+    if (rows < 0) return fail(APS_ERR_SHAPE, "expert_ffn: rows %lld", (long long)rows);
+    if (int rc = check_x_dtype(*w, x_dtype)) return rc;
+    if (rows > 0 && (!x || !offsets || !assignment_rows || !act || !y_perm))
+        return fail(APS_ERR_ARG, "expert_ffn: NULL pointer");
+    return run_ffn(*w, x, rows, offsets, assignment_rows, act, y_perm, static_cast<hipStream_t>(stream));
+}
+
+int aps_moe_ffn_up(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows,
+                   const uint32_t* offsets, const uint32_t* assignment_rows, void* act,
+                   float* act_scale, void* stream) {
+    (void)act_scale;
+    const WeightSet* w = lookup(handle);
+    if (!w) return fail(APS_ERR_HANDLE, "grouped MoE shape or handle: invalid handle %llu",
+                        (unsigned long long)handle);
+    if (int rc = check_device(*w)) return rc;
+    if (rows < 0) return fail(APS_ERR_SHAPE, "ffn_up: rows %lld", (long long)rows);
+    if (int rc = check_x_dtype(*w, x_dtype)) return rc;
+    if (rows > 0 && (!x || !offsets || !assignment_rows || !act)) return fail(APS_ERR_ARG, "ffn_up: NULL pointer");
+    return run_ffn_up(*w, x, rows, offsets, assignment_rows, act, static_cast<hipStream_t>(stream));
+}
+
+int aps_moe_ffn_down(uint64_t handle, const void* act, const float* act_scale, int64_t rows,
+                     const uint32_t* offsets, void* y_perm, void* stream) {
+    (void)act_scale;
+    const WeightSet* w = lookup(handle);
+    if (!w) return fail(APS_ERR_HANDLE, "grouped MoE shape or handle: invalid handle %llu",
+                        (unsigned long long)handle);
+    if (int rc = check_device(*w)) return rc;
+    if (rows < 0) return fail(APS_ERR_SHAPE, "ffn_down: rows %lld", (long long)rows);
+    if (rows > 0 && (!act || !offsets || !y_perm)) return fail(APS_ERR_ARG, "ffn_down: NULL pointer");
+    return run_ffn_down(*w, act, rows, offsets, y_perm, static_cast<hipStream_t>(stream));
+}
+
+int aps_moe_combine(const void* y_perm, int32_t y_dtype, const uint32_t* route_positions,
+                    int64_t rows, int32_t hidden, void* out, int32_t out_dtype, void* stream) {
+    if (rows < 0 || hidden <= 0 || hidden % 8 != 0)
+        return fail(APS_ERR_SHAPE, "combine: rows %lld hidden %d", (long long)rows, hidden);
+    if ((y_dtype != APS_DTYPE_F32 && y_dtype != APS_DTYPE_BF16) ||
+        (out_dtype != APS_DTYPE_F32 && out_dtype != APS_DTYPE_BF16))
+        return fail(APS_ERR_DTYPE, "combine: y dtype %d / out dtype %d", y_dtype, out_dtype);
+    if (rows > 0 && (!y_perm || !route_positions || !out)) return fail(APS_ERR_ARG, "combine: NULL pointer");
+    APS_HIP(aps::launch_combine(y_perm, y_dtype == APS_DTYPE_BF16, route_positions, rows, hidden, out,
+                                out_dtype == APS_DTYPE_BF16, static_cast<hipStream_t>(stream)),
+            "combine launch");
+    return APS_OK;
+}
+
+static int forward_common(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows, void* out,
+                          int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                          const WeightSet** w_out, aps_moe_ws_layout* L) {
+    const WeightSet* w = lookup(handle);
+    // reference: "grouped MoE shape or handle" (src/tensor.cu:2793-2797)
+    if (!w) return fail(APS_ERR_HANDLE, "grouped MoE shape or handle: invalid handle %llu",
+                        (unsigned long long)handle);
+    if (int rc = check_device(*w)) return rc;
+    if (rows < 0 || rows > (int64_t(1) << 30))
+        return fail(APS_ERR_SHAPE, "grouped MoE shape or handle: rows %lld", (long long)rows);
+    if (int rc = check_x_dtype(*w, x_dtype)) return rc;
+    if (out_dtype != APS_DTYPE_F32 && out_dtype != APS_DTYPE_BF16)
+        return fail(APS_ERR_DTYPE, "out dtype %d not supported", out_dtype);
+    make_layout(*w, rows, L);
+    if (rows > 0) {
+        if (!x || !out) return fail(APS_ERR_ARG, "forward: NULL x or out");
+        if (!workspace || workspace_bytes < L->total_bytes)
+            return fail(APS_ERR_WORKSPACE, "workspace %zu bytes, need %zu", workspace_bytes, L->total_bytes);
+    }
+    *w_out = w;
+    return APS_OK;
+}
+
+int aps_moe_forward_grouped(uint64_t handle, const void* x, int32_t x_dtype,
+                            const float* router_logits, int64_t rows, void* out, int32_t out_dtype,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+    const WeightSet* w = nullptr;
+    aps_moe_ws_layout L;
+    if (int rc = forward_common(handle, x, x_dtype, rows, out, out_dtype, workspace, workspace_bytes, &w, &L))
+        return rc;
+    if (rows == 0) return APS_OK;
+    if (!router_logits) return fail(APS_ERR_ARG, "forward_grouped: NULL router logits");
+    return grouped_from_logits(*w, x, router_logits, rows, out, out_dtype, static_cast<char*>(workspace),
+                               L, static_cast<hipStream_t>(stream));
+}
+
+int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float* gate, int64_t rows,
+                    void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    const WeightSet* w = nullptr;
+    aps_moe_ws_layout L;
+    if (int rc = forward_common(handle, x, x_dtype, rows, out, out_dtype, workspace, workspace_bytes, &w, &L))
+        return rc;
+    if (rows == 0) return APS_OK;
+    if (!gate) return fail(APS_ERR_ARG, "forward: NULL gate");
+    char* ws = static_cast<char*>(workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    float* logits = reinterpret_cast<float*>(ws + L.logits);
+    APS_HIP(aps::launch_router_logits(x, w->compute != APS_DTYPE_F32, gate, rows, w->H, w->E, logits, s),
+            "router_logits launch");
+    return grouped_from_logits(*w, x, logits, rows, out, out_dtype, ws, L, s);
+}
+
+}  // extern "C"

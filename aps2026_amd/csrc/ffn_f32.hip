@@ -1,0 +1,197 @@
+// Grouped expert FFN in fp32 with the reference's accumulation order.
+//
+// Reference: k_moe_pair_silu_8x8 (src/tensor.cu:1838-1966) and
+// k_moe_matmul_8x8 (src/tensor.cu:1740-1836) give every output ONE fp32
+// accumulator walked over k ascending with FMA (nvcc contracts
+// `acc += a * b`), and the SiLU epilogue evaluates exp in double:
+// a = g / (1 + (float)exp((double)-g)) * u.
+//
+// These kernels keep exactly that arithmetic, so for fp32 weights the result
+// equals the CPU oracle bit for bit (the only libm call, exp in double, is
+// rounded to float afterwards).  They are SIMT kernels: each thread owns a
+// 4 x 4 block of outputs per operand and walks k in order; operand tiles are
+// staged k-major in LDS so the inner step is three ds_read_b128 + 32 FMAs.
+// This is the exactness path; the throughput path is
+// the bf16 MFMA kernel.
+#include "common.hpp"
+
+namespace aps {
+namespace {
+
+constexpr int kBK = 16;
+
+__device__ inline bool locate_tile(const uint32_t* __restrict__ offsets, int E, int tile, int bm,
+                                   int& expert, uint32_t& m0, uint32_t& end) {
+    int cum = 0;
+    for (int e = 0; e < E; ++e) {
+        const uint32_t lo = offsets[e], hi = offsets[e + 1];
+        const int nt = static_cast<int>((hi - lo + bm - 1) / bm);
+        if (tile < cum + nt) {
+            expert = e;
+            m0 = lo + static_cast<uint32_t>(tile - cum) * bm;
+            end = hi;
+            return true;
+        }
+        cum += nt;
+    }
+    return false;
+}
+
+// a = g / (1 + (float)exp((double)-g)) * u, each operation rounded on its own
+// (src/tensor.cu:1961-1963, src/layer.cu:8-11).
+__device__ inline float swiglu_exact(float g, float u) {
+    const float ex = static_cast<float>(exp(-static_cast<double>(g)));
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, ex)), u);
+}
+
+// 64 rows x 64 intermediate columns of gate AND up per block.
+__global__ void __launch_bounds__(256)
+k_ffn_up_f32(const float* __restrict__ x, const uint32_t* __restrict__ offsets,
+             const uint32_t* __restrict__ assignment_rows, const float* __restrict__ w1,
+             const float* __restrict__ w3, float* __restrict__ act, int H, int F, int E) {
+    __shared__ __align__(16) float As[kBK][kF32BM];
+    __shared__ __align__(16) float Gs[kBK][kF32BN];
+    __shared__ __align__(16) float Us[kBK][kF32BN];
+
+    int e;
+    uint32_t m0, end;
+    if (!locate_tile(offsets, E, blockIdx.y, kF32BM, e, m0, end)) return;
+    const int n0 = blockIdx.x * kF32BN;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    // staging: one float4 of A, of w1 and of w3 per thread per k tile
+    const int sr = tid >> 2, sk = (tid & 3) * 4;
+    const uint32_t p = m0 + sr;
+    const bool a_ok = p < end;
+    const float* a_src = x + static_cast<int64_t>(a_ok ? assignment_rows[p] : 0) * H + sk;
+    const bool b_ok = n0 + sr < F;
+    const int64_t brow = static_cast<int64_t>(e) * F + (b_ok ? n0 + sr : 0);
+    const float* g_src = w1 + brow * H + sk;
+    const float* u_src = w3 + brow * H + sk;
+
+    float ga[4][4], ua[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) { ga[r][c] = 0.0f; ua[r][c] = 0.0f; }
+
+    for (int k0 = 0; k0 < H; k0 += kBK) {
+        const float4 av = a_ok ? *reinterpret_cast<const float4*>(a_src + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 gv = b_ok ? *reinterpret_cast<const float4*>(g_src + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 uv = b_ok ? *reinterpret_cast<const float4*>(u_src + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        __syncthreads();
+        As[sk + 0][sr] = av.x; As[sk + 1][sr] = av.y; As[sk + 2][sr] = av.z; As[sk + 3][sr] = av.w;
+        Gs[sk + 0][sr] = gv.x; Gs[sk + 1][sr] = gv.y; Gs[sk + 2][sr] = gv.z; Gs[sk + 3][sr] = gv.w;
+        Us[sk + 0][sr] = uv.x; Us[sk + 1][sr] = uv.y; Us[sk + 2][sr] = uv.z; Us[sk + 3][sr] = uv.w;
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kBK; ++kk) {
+            const float4 a = *reinterpret_cast<const float4*>(&As[kk][ty * 4]);
+            const float4 g = *reinterpret_cast<const float4*>(&Gs[kk][tx * 4]);
+            const float4 u = *reinterpret_cast<const float4*>(&Us[kk][tx * 4]);
+            const float ar[4] = {a.x, a.y, a.z, a.w};
+            const float gr[4] = {g.x, g.y, g.z, g.w};
+            const float ur[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    ga[r][c] = __builtin_fmaf(ar[r], gr[c], ga[r][c]);
+                    ua[r][c] = __builtin_fmaf(ar[r], ur[c], ua[r][c]);
+                }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t pr = m0 + ty * 4 + r;
+        if (pr >= end) continue;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int col = n0 + tx * 4 + c;
+            if (col < F) act[static_cast<int64_t>(pr) * F + col] = swiglu_exact(ga[r][c], ua[r][c]);
+        }
+    }
+}
+
+// 64 rows x 64 hidden columns per block; K = F walked ascending.
+__global__ void __launch_bounds__(256)
+k_ffn_down_f32(const float* __restrict__ act, const uint32_t* __restrict__ offsets,
+               const float* __restrict__ w2, float* __restrict__ y, int H, int F, int E) {
+    __shared__ __align__(16) float As[kBK][kF32BM];
+    __shared__ __align__(16) float Bs[kBK][kF32BN];
+
+    int e;
+    uint32_t m0, end;
+    if (!locate_tile(offsets, E, blockIdx.y, kF32BM, e, m0, end)) return;
+    const int n0 = blockIdx.x * kF32BN;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int sr = tid >> 2, sk = (tid & 3) * 4;
+    const uint32_t p = m0 + sr;
+    const bool a_ok = p < end;
+    const float* a_src = act + static_cast<int64_t>(a_ok ? p : m0) * F + sk;
+    const bool b_ok = n0 + sr < H;
+    const float* b_src = w2 + (static_cast<int64_t>(e) * H + (b_ok ? n0 + sr : 0)) * F + sk;
+
+    float acc[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[r][c] = 0.0f;
+
+    for (int k0 = 0; k0 < F; k0 += kBK) {
+        const float4 av = a_ok ? *reinterpret_cast<const float4*>(a_src + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 bv = b_ok ? *reinterpret_cast<const float4*>(b_src + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        __syncthreads();
+        As[sk + 0][sr] = av.x; As[sk + 1][sr] = av.y; As[sk + 2][sr] = av.z; As[sk + 3][sr] = av.w;
+        Bs[sk + 0][sr] = bv.x; Bs[sk + 1][sr] = bv.y; Bs[sk + 2][sr] = bv.z; Bs[sk + 3][sr] = bv.w;
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kBK; ++kk) {
+            const float4 a = *reinterpret_cast<const float4*>(&As[kk][ty * 4]);
+            const float4 b = *reinterpret_cast<const float4*>(&Bs[kk][tx * 4]);
+            const float ar[4] = {a.x, a.y, a.z, a.w};
+            const float br[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[r][c] = __builtin_fmaf(ar[r], br[c], acc[r][c]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t pr = m0 + ty * 4 + r;
+        if (pr >= end) continue;
+        const int col = n0 + tx * 4;
+        if (col + 3 < H)
+            *reinterpret_cast<float4*>(y + static_cast<int64_t>(pr) * H + col) =
+                make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_ffn_up_f32(const float* x, const uint32_t* offsets,
+                             const uint32_t* assignment_rows, const float* w1,
+                             const float* w3, float* act, int64_t rows, int hidden, int ffn,
+                             int experts, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (hidden % kBK != 0 || ffn % 4 != 0) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(ceil_div(ffn, kF32BN)),
+                    static_cast<unsigned>(max_row_tiles(2 * rows, kF32BM, experts)));
+    hipLaunchKernelGGL(k_ffn_up_f32, grid, dim3(256), 0, s, x, offsets, assignment_rows, w1, w3,
+                       act, hidden, ffn, experts);
+    return hipGetLastError();
+}
+
+hipError_t launch_ffn_down_f32(const float* act, const uint32_t* offsets, const float* w2,
+                               float* y, int64_t rows, int hidden, int ffn, int experts,
+                               hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (ffn % kBK != 0 || hidden % kF32BN != 0) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(hidden / kF32BN),
+                    static_cast<unsigned>(max_row_tiles(2 * rows, kF32BM, experts)));
+    hipLaunchKernelGGL(k_ffn_down_f32, grid, dim3(256), 0, s, act, offsets, w2, y, hidden, ffn,
+                       experts);
+    return hipGetLastError();
+}
+
+}  // namespace aps

@@ -1,0 +1,212 @@
+"""Benchmark of the MoE feed-forward block on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+
+One step = one full MoE block (router GEMM, quantised top-2, dispatch,
+grouped w1||w3 + SwiGLU, grouped w2, combine) over one batch of synthetic
+tokens already resident in HBM.  Workload (default): BASELINE config C2 --
+4096 tokens, hidden 4096, 16 experts top-2, expert FFN 448, bf16, router bias
+giving Zipf(1.1) expert loads.  Steps rotate over LAYERS distinct device
+copies of the expert weights (4 x 176 MB > the 256 MB MALL), as consecutive
+decoder layers would, so expert weights stream from HBM every step instead
+of sitting in the Infinity Cache.
+
+Prints ONE JSON line.  `roofline` covers the dominant kernel (the grouped
+w1||w3 + SwiGLU GEMM, k_ffn_up_bf16), timed with HIP events on the stream it
+is launched on; `cpu_baseline` times the CPU oracle (the reference CPU-path
+algorithm, src/layer.cu:113-148) on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-block prefill tokens/s + grouped-GEMM % MFMA peak, 4096 tok, 1 GPU"
+PEAK_BF16 = 2.5e15       # MI355X dense bf16 MFMA, FLOP/s
+PEAK_F32 = 157.3e12
+PEAK_HBM = 8.0e12        # bytes/s
+LAYERS = 4
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
+    ap.add_argument("--cpu-runs", type=int, default=3)
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
+              "multi-GPU sharding is designed but not built", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from aps2026_amd import capi, moe, synth
+
+    dev = torch.device("cuda:0")
+    inp = synth.make_config(args.config)
+    T, H, E, F = inp.T, inp.H, inp.E, inp.F
+    A = 2 * T
+    bf16 = inp.dtype == "bf16"
+    tdt = torch.bfloat16 if bf16 else torch.float32
+
+    def dev_bits(bits):
+        return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(dev).view(torch.bfloat16)
+
+    if bf16:
+        x = dev_bits(inp.packed["x_bf16"])
+        host_w = {nm: inp.packed[nm + "_bf16"] for nm in ("w1", "w2", "w3")}
+    else:
+        x = torch.from_numpy(inp.x).to(dev)
+        host_w = {nm: getattr(inp, nm) for nm in ("w1", "w2", "w3")}
+    gate = torch.from_numpy(inp.gate).to(dev)
+    layers = []
+    for _ in range(LAYERS):
+        lists = []
+        for nm in ("w1", "w2", "w3"):
+            d = dev_bits(host_w[nm]) if bf16 else torch.from_numpy(host_w[nm]).to(dev)
+            lists.append([d[e].contiguous() for e in range(E)])
+        layers.append(moe.register_moe_weights_gpu(*lists, compute_dtype=tdt))
+        del lists
+    torch.cuda.synchronize()
+
+    L = capi.lib()
+    lay = layers[0].layout(T)
+    ws = torch.empty(lay.total_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty((T, H), dtype=tdt, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    xd = capi.DTYPE_BF16 if bf16 else capi.DTYPE_F32
+    args_fwd = [(w.handle, ctypes.c_void_p(x.data_ptr()), xd, ctypes.c_void_p(gate.data_ptr()), T,
+                 ctypes.c_void_p(out.data_ptr()), xd, ctypes.c_void_p(ws.data_ptr()), ws.numel(), sptr)
+                for w in layers]
+
+    def step(i):
+        rc = L.aps_moe_forward(*args_fwd[i % LAYERS])
+        if rc:
+            raise RuntimeError(capi.last_error())
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+    tokens_per_s = T * args.steps / elapsed
+
+    # ---- per-stage timing with HIP events on the launch stream ------------
+    def p(t):
+        return ctypes.c_void_p(t.data_ptr())
+
+    logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+    routes = torch.empty((T, 2), dtype=torch.uint8, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    arows = torch.empty(A, dtype=torch.int32, device=dev)
+    rpos = torch.empty(A, dtype=torch.int32, device=dev)
+    scratch = torch.empty(max(L.aps_moe_dispatch_workspace_size(T, E), 1), dtype=torch.uint8, device=dev)
+    act = torch.empty((A, F), dtype=tdt, device=dev)
+    y = torch.empty((A, H), dtype=tdt, device=dev)
+    stages = ["router_logits", "route_top2", "dispatch", "ffn_up", "ffn_down", "combine"]
+    times = {s: [] for s in stages}
+    n_stage = max(args.steps, 10)
+    for i in range(n_stage + 2):
+        w = layers[i % LAYERS]
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
+        ev[0].record(stream)
+        calls = [
+            lambda: L.aps_router_logits(p(x), xd, p(gate), T, H, E, p(logits), sptr),
+            lambda: L.aps_moe_route_top2(p(logits), T, E, p(routes), sptr),
+            lambda: L.aps_moe_dispatch(p(routes), T, E, p(counts), p(offsets), p(arows), p(rpos), p(scratch),
+                                       scratch.numel(), sptr),
+            lambda: L.aps_moe_ffn_up(w.handle, p(x), xd, T, p(offsets), p(arows), p(act), None, sptr),
+            lambda: L.aps_moe_ffn_down(w.handle, p(act), None, T, p(offsets), p(y), sptr),
+            lambda: L.aps_moe_combine(p(y), xd, p(rpos), T, H, p(out), xd, sptr),
+        ]
+        for k, c in enumerate(calls):
+            rc = c()
+            if rc:
+                raise RuntimeError(f"{stages[k]}: {capi.last_error()}")
+            ev[k + 1].record(stream)
+        torch.cuda.synchronize()
+        if i >= 2:
+            for k, s in enumerate(stages):
+                times[s].append(ev[k].elapsed_time(ev[k + 1]) * 1e-3)
+    mean_t = {s: statistics.mean(v) for s, v in times.items()}
+
+    esz = 2 if bf16 else 4
+    flops_up = 4.0 * A * H * F
+    flops_down = 2.0 * A * F * H
+    peak = PEAK_BF16 if bf16 else PEAK_F32
+    bytes_router = T * H * esz + E * H * 4 + T * E * 4
+    bytes_combine = A * H * esz + T * H * esz + A * 4
+    stage_report = {
+        "router_logits": {"us": mean_t["router_logits"] * 1e6,
+                          "GB_s": bytes_router / mean_t["router_logits"] / 1e9},
+        "route_top2": {"us": mean_t["route_top2"] * 1e6},
+        "dispatch": {"us": mean_t["dispatch"] * 1e6},
+        "ffn_up": {"us": mean_t["ffn_up"] * 1e6, "TFLOP_s": flops_up / mean_t["ffn_up"] / 1e12},
+        "ffn_down": {"us": mean_t["ffn_down"] * 1e6, "TFLOP_s": flops_down / mean_t["ffn_down"] / 1e12},
+        "combine": {"us": mean_t["combine"] * 1e6, "GB_s": bytes_combine / mean_t["combine"] / 1e9},
+        "grouped_gemm_total_TFLOP_s": (flops_up + flops_down) / (mean_t["ffn_up"] + mean_t["ffn_down"]) / 1e12,
+    }
+    achieved = flops_up / mean_t["ffn_up"]
+    roofline = {"bound": "mfma", "kernel": "k_ffn_up_bf16" if bf16 else "k_ffn_up_f32",
+                "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                "frac": achieved / peak, "traffic": None,
+                "flops_per_launch": flops_up, "launch_us": mean_t["ffn_up"] * 1e6}
+
+    # ---- CPU baseline: the reference CPU-path algorithm on the host cores ----
+    cpu = None
+    if args.cpu_baseline == "auto":
+        import oracle
+        runs = []
+        oracle.moe_forward(inp.x[:256], inp.gate, inp.w1, inp.w3, inp.w2)  # warm-up
+        for _ in range(args.cpu_runs):
+            t = time.perf_counter()
+            oracle.moe_forward(inp.x, inp.gate, inp.w1, inp.w3, inp.w2)
+            runs.append(time.perf_counter() - t)
+        med = statistics.median(runs)
+        cpu = {"value": T / med, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
+               "sample": f"full {args.config} batch ({T} tokens), values upcast to fp32, reference CPU-path "
+                         f"order (router, route, per-expert gather/FFN/scatter-add), 1 warm-up + median of "
+                         f"{args.cpu_runs} runs ({med:.2f} s each)"}
+
+    line = {
+        "metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if bf16 else "f32", "data": "synthetic (seeded PCG64 normals, random-init weights)",
+        "config": {"workload": f"{args.config}: MoE FFN block, {T} tokens, hidden {H}, {E} experts top-2, "
+                               f"ffn {F}, {inp.dtype}" + (", Zipf(1.1) expert loads" if inp.zipf else ""),
+                   "tokens": T, "hidden": H, "experts": E, "ffn": F, "layers_rotated": LAYERS},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "stages": stage_report,
+    }
+    print(json.dumps(line), flush=True)
+    for w in layers:
+        w.release()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,205 @@
+/*
+ * aps_moe.h -- C ABI of the MI355X (gfx950) MoE feed-forward engine.
+ *
+ * Plain C: integer/pointer/size arguments only.  Every `void* stream` is a
+ * hipStream_t (NULL = the legacy default stream, which is the ordering the
+ * reference relies on: all of its kernels go to stream 0).  Every device
+ * array is caller-owned device memory; every entry point except the weight
+ * registration is asynchronous on `stream` and allocates nothing.
+ *
+ * Return codes: APS_OK (0) or a negative aps_status; aps_moe_last_error()
+ * then gives a thread-local message.  The reference raises
+ * std::invalid_argument / std::runtime_error for the same conditions
+ * (src/tensor.cu:370-374, 2761-2764, 2793-2797); the C++ layer in
+ * include/tensor.h turns these codes back into those exception types.
+ *
+ * Routing semantics are the reference's, bit for bit:
+ *   logits[t][e] = fp32 FMA chain over k = 0..H-1 ascending, +0 init
+ *   q = sign(l) * floorf(|l| / 1e-3f + 0.5f) * 1e-3f
+ *   top-2 = greedy scan, later expert wins only if q > q_best + 2e-2f
+ *   weights 0.5 / 0.5; stable counting sort by expert, ties by token.
+ */
+#ifndef APS_MOE_H
+#define APS_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define APS_MOE_ABI_VERSION 1
+
+#if defined(__GNUC__) || defined(__clang__)
+#define APS_API __attribute__((visibility("default")))
+#else
+#define APS_API
+#endif
+
+typedef enum aps_status {
+    APS_OK = 0,
+    APS_ERR_SHAPE = -1,     /* inconsistent or unsupported sizes          */
+    APS_ERR_HANDLE = -2,    /* weight handle 0, released or out of range   */
+    APS_ERR_DTYPE = -3,     /* dtype code not supported for this argument  */
+    APS_ERR_HIP = -4,       /* a HIP runtime call failed                   */
+    APS_ERR_ARG = -5,       /* NULL pointer or other invalid argument      */
+    APS_ERR_WORKSPACE = -6  /* workspace missing or smaller than required  */
+} aps_status;
+
+typedef enum aps_dtype {
+    APS_DTYPE_F32 = 0,
+    APS_DTYPE_BF16 = 1,
+    APS_DTYPE_E4M3 = 2      /* OCP fp8 e4m3 ("fn"): bias 7, max 448        */
+} aps_dtype;
+
+/* Weight set of one MoE layer (the reference's MoeWeightSet,
+ * src/tensor.cu:1216-1220).  w1/w3/w2 are HOST arrays of num_experts DEVICE
+ * pointers in the reference's nn.Linear layout: w1[e], w3[e] are
+ * [ffn][hidden], w2[e] is [hidden][ffn], row-major.
+ * compute_dtype picks the kernels:
+ *   APS_DTYPE_F32  - fp32 FMA-chain kernels, accumulation order identical to
+ *                    the reference (k ascending), src_dtype must be F32;
+ *   APS_DTYPE_BF16 - bf16 MFMA kernels, fp32 accumulate; src F32 or BF16;
+ *   APS_DTYPE_E4M3 - fp8 MFMA kernels; src E4M3 with per-output-channel fp32
+ *                    scales (w1_scale[e], w3_scale[e]: [ffn] device arrays,
+ *                    w2_scale[e]: [hidden]).
+ * Registration copies the weights into the library's own packed layout
+ * (the caller's buffers may be freed afterwards). */
+typedef struct aps_moe_weights_desc {
+    int32_t num_experts;
+    int32_t hidden;
+    int32_t ffn;
+    int32_t src_dtype;
+    int32_t compute_dtype;
+    const void* const* w1;
+    const void* const* w3;
+    const void* const* w2;
+    const float* const* w1_scale;
+    const float* const* w3_scale;
+    const float* const* w2_scale;
+} aps_moe_weights_desc;
+
+/* Byte offsets of the intermediate arrays inside a forward workspace, for
+ * callers (and tests) that want to read the routing plan back. */
+typedef struct aps_moe_ws_layout {
+    size_t total_bytes;
+    size_t logits;          /* f32 [rows][E]                        */
+    size_t routes;          /* u8  [rows][2], slot 0 = first pick   */
+    size_t tile_counts;     /* u32 [ceil(rows/64)][E]               */
+    size_t counts;          /* u32 [E]                              */
+    size_t offsets;         /* u32 [E+1]                            */
+    size_t assignment_rows; /* u32 [2*rows] position -> token       */
+    size_t route_positions; /* u32 [2*rows] (token, slot) -> position */
+    size_t act;             /* [2*rows][ffn], compute dtype (f32 or bf16) */
+    size_t act_scale;       /* f32 [2*rows] (fp8 path only)         */
+    size_t y;               /* [2*rows][hidden], f32 (F32 path) or bf16 */
+    size_t xq;              /* fp8 path: e4m3 x [rows][hidden]      */
+    size_t xq_scale;        /* fp8 path: f32 [rows]                 */
+} aps_moe_ws_layout;
+
+/* ---- weights ----------------------------------------------------------- */
+
+/* Replaces tensor_ops::register_moe_weights_gpu (reference
+ * include/tensor.h:142-145, src/tensor.cu:2757-2788).  Writes a 1-based
+ * handle (0 is never a valid handle, as in the reference).  Synchronous. */
+APS_API int aps_moe_weights_register(const aps_moe_weights_desc* desc, void* stream,
+                             uint64_t* handle_out);
+
+/* Frees the packed copies.  No reference counterpart: the reference's
+ * registry is never freed (src/tensor.cu:1222-1225). */
+APS_API int aps_moe_weights_release(uint64_t handle);
+
+/* ---- sizes ------------------------------------------------------------- */
+
+/* Workspace needed by aps_moe_forward / aps_moe_forward_grouped for `rows`
+ * tokens with this weight set, and where each array lives in it.  Replaces
+ * the reference's grow-only static scratch (src/tensor.cu:1227-1291) and its
+ * per-call intermediate Tensors (src/tensor.cu:2835, 2867). */
+APS_API int aps_moe_workspace_layout(uint64_t handle, int64_t rows, aps_moe_ws_layout* out);
+
+/* Scratch for aps_moe_dispatch: u32 [ceil(rows/64)][num_experts]. */
+APS_API size_t aps_moe_dispatch_workspace_size(int64_t rows, int32_t num_experts);
+
+/* ---- stages ------------------------------------------------------------ */
+
+/* Router GEMM logits[rows][E] = x[rows][H] . gate[E][H]^T as one fp32 FMA
+ * chain per output, k ascending.  Replaces tensor_ops::matmul_transposed_gpu
+ * (reference include/tensor.h:72, src/tensor.cu:3034-3065) on the narrow
+ * path it takes for the router (k_matmul_transposed_narrow,
+ * src/tensor.cu:2943-3006).  x_dtype: F32 or BF16 (exact upcast). */
+APS_API int aps_router_logits(const void* x, int32_t x_dtype, const float* gate,
+                      int64_t rows, int32_t hidden, int32_t num_experts,
+                      float* logits, void* stream);
+
+/* Quantise + greedy top-2 (reference k_moe_top2, src/tensor.cu:1293-1331;
+ * PhiMoE::route, src/layer.cu:69-92).  routes: u8 [rows][2]. */
+APS_API int aps_moe_route_top2(const float* logits, int64_t rows, int32_t num_experts,
+                       uint8_t* routes, void* stream);
+
+/* Stable counting-sort dispatch (reference k_moe_offsets_work +
+ * k_moe_fill_stable, src/tensor.cu:1333-1418).  Outputs counts[E],
+ * offsets[E+1], assignment_rows[2*rows], route_positions[2*rows].
+ * `scratch` must hold aps_moe_dispatch_workspace_size(rows, E) bytes. */
+APS_API int aps_moe_dispatch(const uint8_t* routes, int64_t rows, int32_t num_experts,
+                     uint32_t* counts, uint32_t* offsets,
+                     uint32_t* assignment_rows, uint32_t* route_positions,
+                     void* scratch, size_t scratch_bytes, void* stream);
+
+/* Grouped expert FFN over the permuted assignments (reference
+ * k_moe_pair_silu_8x8 + k_moe_matmul_8x8, src/tensor.cu:1740-1966):
+ * y_perm[p] = w2[e] . (silu(w1[e] . x[t]) * (w3[e] . x[t])) for
+ * t = assignment_rows[p], p in [offsets[e], offsets[e+1]).
+ * act: [2*rows][ffn] scratch of the compute dtype (f32 or bf16; for the
+ * fp8 path e4m3 plus act_scale f32 [2*rows]).  y_perm: [2*rows][hidden],
+ * f32 for the F32 path, bf16 otherwise.  x_dtype must match the weight
+ * set: F32 for the F32 path, BF16 otherwise. */
+APS_API int aps_moe_expert_ffn(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows,
+                       const uint32_t* offsets, const uint32_t* assignment_rows,
+                       void* act, float* act_scale, void* y_perm, void* stream);
+
+/* The two halves of aps_moe_expert_ffn, for callers that schedule or time
+ * them separately.  ffn_up replaces k_moe_pair_silu_8x8 (reference
+ * src/tensor.cu:1838-1966): act[p] = silu(w1[e] . x[t]) * (w3[e] . x[t]).
+ * ffn_down replaces k_moe_matmul_8x8 (src/tensor.cu:1740-1836):
+ * y_perm[p] = w2[e] . act[p]. */
+APS_API int aps_moe_ffn_up(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows,
+                           const uint32_t* offsets, const uint32_t* assignment_rows,
+                           void* act, float* act_scale, void* stream);
+APS_API int aps_moe_ffn_down(uint64_t handle, const void* act, const float* act_scale,
+                             int64_t rows, const uint32_t* offsets, void* y_perm,
+                             void* stream);
+
+/* Weighted combine (reference k_moe_combine, src/tensor.cu:1968-1988):
+ * out[t] = 0.5 * y_perm[route_positions[2t]] + 0.5 * y_perm[route_positions[2t+1]],
+ * summed in fp32, rounded once to out_dtype (F32 or BF16). */
+APS_API int aps_moe_combine(const void* y_perm, int32_t y_dtype, const uint32_t* route_positions,
+                    int64_t rows, int32_t hidden, void* out, int32_t out_dtype,
+                    void* stream);
+
+/* ---- whole block ------------------------------------------------------- */
+
+/* Replaces tensor_ops::moe_forward_grouped_gpu (reference
+ * include/tensor.h:146-147, src/tensor.cu:2790-2928): routing from
+ * precomputed logits [rows][E], then dispatch, expert FFN and combine. */
+APS_API int aps_moe_forward_grouped(uint64_t handle, const void* x, int32_t x_dtype,
+                            const float* router_logits, int64_t rows,
+                            void* out, int32_t out_dtype,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Replaces the body of PhiMoE::forward (reference src/layer.cu:113-121):
+ * router GEMM (gate [E][H] fp32) + the grouped path above, in one call. */
+APS_API int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float* gate,
+                    int64_t rows, void* out, int32_t out_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- diagnostics ------------------------------------------------------- */
+
+APS_API const char* aps_moe_last_error(void);
+APS_API int aps_moe_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* APS_MOE_H */

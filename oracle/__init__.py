@@ -1,0 +1,186 @@
+"""ctypes wrapper over the CPU oracle (liboracle_moe.so, built from
+moe_oracle.c by the Makefile beside it).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, always as the checker or the timed CPU
+baseline, never as part of the product path.  Each function restates one
+step of the reference MoE path; the reference file:line it follows is given
+in moe_oracle.c.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional, Tuple
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle_moe.so")
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+_lib = None
+
+
+def build() -> str:
+    """Compile liboracle_moe.so with gcc (no GPU needed)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.oracle_router_logits.argtypes = [_f32p, _f32p, _i64, _i32, _i32, _f32p]
+        L.oracle_quantise.argtypes = [ctypes.c_float, ctypes.c_float]
+        L.oracle_quantise.restype = ctypes.c_float
+        L.oracle_route_top2.argtypes = [_f32p, _i64, _i32, ctypes.c_float, ctypes.c_float, _i32p, ctypes.c_void_p]
+        L.oracle_dispatch.argtypes = [_i32p, _i64, _i32, _u32p, _u32p, _u32p, _u32p]
+        L.oracle_ffn_rows.argtypes = [_f32p, _i32p, _i64, _i32, _i32, _i32, _f32p, _f32p, _f32p,
+                                      ctypes.c_void_p, _f32p]
+        L.oracle_combine.argtypes = [_f32p, _i32p, _u32p, _i64, _i32, _f32p]
+        L.oracle_moe_forward.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _i32, _i32, _i32,
+                                         _f32p, ctypes.c_void_p, ctypes.c_void_p]
+        L.oracle_bf16_to_f32.argtypes = [_u16p, _f32p, _i64]
+        L.oracle_e4m3_to_f32.argtypes = [_u8p, _f32p, _i64]
+        L.oracle_default_quantum.restype = ctypes.c_float
+        L.oracle_default_tie_eps.restype = ctypes.c_float
+        L.oracle_num_threads.restype = ctypes.c_int
+        L.oracle_set_num_threads.argtypes = [ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"oracle {what} failed with code {rc}")
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+QUANTUM = np.float32(1.0e-3)
+TIE_EPS = np.float32(2.0e-2)
+
+
+def num_threads() -> int:
+    return lib().oracle_num_threads()
+
+
+def set_num_threads(n: int) -> None:
+    lib().oracle_set_num_threads(int(n))
+
+
+def router_logits(x: np.ndarray, gate: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32); gate = _c(gate, np.float32)
+    T, H = x.shape
+    E = gate.shape[0]
+    out = np.empty((T, E), np.float32)
+    _check(lib().oracle_router_logits(x, gate, T, H, E, out), "router_logits")
+    return out
+
+
+def quantise(l: float, quantum: float = float(QUANTUM)) -> np.float32:
+    return np.float32(lib().oracle_quantise(float(np.float32(l)), float(np.float32(quantum))))
+
+
+def route_top2(logits: np.ndarray, quantum=QUANTUM, tie_eps=TIE_EPS) -> np.ndarray:
+    """Returns routes int32 [T, 2] (slot 0 = first pick)."""
+    logits = _c(logits, np.float32)
+    T, E = logits.shape
+    routes = np.empty((T, 2), np.int32)
+    _check(lib().oracle_route_top2(logits, T, E, float(quantum), float(tie_eps), routes, None), "route_top2")
+    return routes
+
+
+def dispatch(routes: np.ndarray, E: int) -> Tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]:
+    """Returns (counts[E], offsets[E+1], assignment_rows[2T], route_positions[2T])."""
+    routes = _c(routes, np.int32)
+    T = routes.shape[0]
+    counts = np.empty(E, np.uint32)
+    offsets = np.empty(E + 1, np.uint32)
+    rows = np.empty(2 * T, np.uint32)
+    pos = np.empty(2 * T, np.uint32)
+    _check(lib().oracle_dispatch(routes, T, E, counts, offsets, rows, pos), "dispatch")
+    return counts, offsets, rows, pos
+
+
+def ffn_rows(xrows: np.ndarray, experts: np.ndarray, w1, w3, w2,
+             want_act: bool = False):
+    """Expert FFN for n (row, expert) pairs; returns y [n, H] (and act [n, F])."""
+    xrows = _c(xrows, np.float32)
+    experts = _c(experts, np.int32)
+    w1 = _c(w1, np.float32); w3 = _c(w3, np.float32); w2 = _c(w2, np.float32)
+    n, H = xrows.shape
+    E, F, _ = w1.shape
+    y = np.empty((n, H), np.float32)
+    act = np.empty((n, F), np.float32) if want_act else None
+    _check(lib().oracle_ffn_rows(xrows, experts, n, H, F, E, w1, w3, w2,
+                                 act.ctypes.data if act is not None else None, y), "ffn_rows")
+    return (y, act) if want_act else y
+
+
+def combine(y: np.ndarray, routes: np.ndarray, route_positions: np.ndarray) -> np.ndarray:
+    y = _c(y, np.float32)
+    routes = _c(routes, np.int32)
+    route_positions = _c(route_positions, np.uint32)
+    T = routes.shape[0]
+    H = y.shape[1]
+    out = np.empty((T, H), np.float32)
+    _check(lib().oracle_combine(y, routes, route_positions, T, H, out), "combine")
+    return out
+
+
+def moe_forward(x, gate, w1, w3, w2, want_intermediate: bool = False):
+    """Whole block in the reference CPU path's order (src/layer.cu:113-148)."""
+    x = _c(x, np.float32); gate = _c(gate, np.float32)
+    w1 = _c(w1, np.float32); w3 = _c(w3, np.float32); w2 = _c(w2, np.float32)
+    T, H = x.shape
+    E, F, _ = w1.shape
+    out = np.empty((T, H), np.float32)
+    logits = np.empty((T, E), np.float32) if want_intermediate else None
+    routes = np.empty((T, 2), np.int32) if want_intermediate else None
+    _check(lib().oracle_moe_forward(x, gate, w1, w3, w2, T, H, F, E, out,
+                                    logits.ctypes.data if logits is not None else None,
+                                    routes.ctypes.data if routes is not None else None), "moe_forward")
+    return (out, logits, routes) if want_intermediate else out
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    bits = _c(bits, np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().oracle_bf16_to_f32(bits.reshape(-1), out.reshape(-1), bits.size)
+    return out
+
+
+def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
+    codes = _c(codes, np.uint8)
+    out = np.empty(codes.shape, np.float32)
+    lib().oracle_e4m3_to_f32(codes.reshape(-1), out.reshape(-1), codes.size)
+    return out
+
+
+def reference_path(x, gate, w1, w3, w2):
+    """Full staged oracle (GPU-path semantics): returns a dict with logits,
+    routes, counts, offsets, assignment_rows, route_positions, y, out."""
+    logits = router_logits(x, gate)
+    routes = route_top2(logits)
+    E = gate.shape[0]
+    counts, offsets, rows, pos = dispatch(routes, E)
+    experts = np.repeat(np.arange(E, dtype=np.int32), counts.astype(np.int64))
+    y = ffn_rows(np.asarray(x)[rows.astype(np.int64)], experts, w1, w3, w2)
+    out = combine(y, routes, pos)
+    return dict(logits=logits, routes=routes, counts=counts, offsets=offsets,
+                assignment_rows=rows, route_positions=pos, y=y, out=out)

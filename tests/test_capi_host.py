@@ -1,0 +1,84 @@
+"""Host-side checks of the C ABI that need no GPU: the library loads, exports
+exactly what include/aps_moe.h declares, and rejects bad arguments with the
+documented status codes before touching the device."""
+import ctypes
+
+import pytest
+import torch
+
+from aps2026_amd import capi, moe
+
+
+def test_library_exports_every_declared_symbol():
+    L = capi.lib()
+    names = capi.declared_symbols()
+    assert len(names) == 15
+    for n in names:
+        assert hasattr(L, n), n
+    assert L.aps_moe_abi_version() == 1
+
+
+def _desc(E=16, H=4096, F=448, src=capi.DTYPE_BF16, compute=capi.DTYPE_BF16, null_table=False):
+    fake = (ctypes.c_void_p * E)(*([0x1000] * E))
+    tab = None if null_table else ctypes.cast(fake, ctypes.POINTER(ctypes.c_void_p))
+    d = capi.WeightsDesc(E, H, F, src, compute, tab, tab, tab, None, None, None)
+    d._keep = fake
+    return d
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(E=1), capi.APS_ERR_SHAPE),            # reference: "MoE weight table size"
+    (dict(E=65), capi.APS_ERR_SHAPE),
+    (dict(H=4000), capi.APS_ERR_SHAPE),
+    (dict(F=100), capi.APS_ERR_SHAPE),
+    (dict(null_table=True), capi.APS_ERR_ARG),
+    (dict(compute=7), capi.APS_ERR_DTYPE),
+    (dict(src=capi.DTYPE_BF16, compute=capi.DTYPE_F32), capi.APS_ERR_DTYPE),
+])
+def test_register_rejects(kw, code):
+    d = _desc(**kw)
+    h = ctypes.c_uint64(123)
+    rc = capi.lib().aps_moe_weights_register(ctypes.byref(d), None, ctypes.byref(h))
+    assert rc == code, capi.last_error()
+    assert h.value == 0
+    assert capi.last_error()
+
+
+def test_register_null_descriptor():
+    h = ctypes.c_uint64(0)
+    assert capi.lib().aps_moe_weights_register(None, None, ctypes.byref(h)) == capi.APS_ERR_ARG
+
+
+@pytest.mark.parametrize("handle", [0, 999])
+def test_forward_rejects_bad_handle(handle):
+    L = capi.lib()
+    rc = L.aps_moe_forward(handle, None, capi.DTYPE_BF16, None, 16, None, capi.DTYPE_BF16, None, 0, None)
+    assert rc == capi.APS_ERR_HANDLE
+    assert "grouped MoE shape or handle" in capi.last_error()
+    rc = L.aps_moe_forward_grouped(handle, None, capi.DTYPE_BF16, None, 16, None, capi.DTYPE_BF16, None, 0, None)
+    assert rc == capi.APS_ERR_HANDLE
+    lay = capi.WsLayout()
+    assert L.aps_moe_workspace_layout(handle, 16, ctypes.byref(lay)) == capi.APS_ERR_HANDLE
+    assert L.aps_moe_weights_release(handle) == capi.APS_ERR_HANDLE
+
+
+def test_stage_argument_checks():
+    L = capi.lib()
+    assert L.aps_router_logits(None, capi.DTYPE_F32, None, 8, 100, 16, None, None) == capi.APS_ERR_SHAPE
+    assert L.aps_router_logits(None, capi.DTYPE_E4M3, None, 8, 4096, 16, None, None) == capi.APS_ERR_DTYPE
+    assert L.aps_router_logits(None, capi.DTYPE_F32, None, 8, 4096, 16, None, None) == capi.APS_ERR_ARG
+    assert L.aps_router_logits(None, capi.DTYPE_F32, None, 0, 4096, 16, None, None) == capi.APS_OK
+    assert L.aps_moe_route_top2(None, 8, 1, None, None) == capi.APS_ERR_SHAPE
+    assert L.aps_moe_combine(None, capi.DTYPE_BF16, None, 8, 12, None, capi.DTYPE_BF16, None) == capi.APS_ERR_SHAPE
+    assert L.aps_moe_combine(None, capi.DTYPE_E4M3, None, 8, 16, None, capi.DTYPE_BF16, None) == capi.APS_ERR_DTYPE
+    assert L.aps_moe_dispatch(None, 8, 16, None, None, None, None, None, 0, None) == capi.APS_ERR_ARG
+    assert L.aps_moe_dispatch_workspace_size(0, 16) == 0
+    assert L.aps_moe_dispatch_workspace_size(65, 16) == 2 * 16 * 4
+
+
+def test_python_mirror_raises_value_error_on_shapes():
+    a = torch.zeros(4, 256)
+    with pytest.raises(ValueError, match="matmul_transposed_gpu shape"):
+        moe.matmul_transposed_gpu(a, torch.zeros(16, 128), torch.zeros(4, 16))
+    with pytest.raises(ValueError, match="MoE weight table size"):
+        moe.MoeWeights([torch.zeros(448, 4096)], [torch.zeros(4096, 448)], [torch.zeros(448, 4096)])

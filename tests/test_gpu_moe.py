@@ -1,0 +1,247 @@
+"""GPU parity of the HIP MoE path against the CPU oracle, through the C ABI.
+
+Bars:
+  routing indices, per-expert counts, offsets and permutation: bit-exact
+  fp32 path (config C1): output within 1e-5 relative, normwise per row
+  bf16 path (config C2): output within 2e-2 relative, normwise per row
+At C2's full size the oracle checks routing bit for bit on every token and
+the expert FFN on a token subset; size-independent properties (the combine
+identity on the GPU's own expert outputs, determinism across runs, the staged
+and fused entry points agreeing bit for bit) cover the rest.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from aps2026_amd import capi, moe, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+TOL_BF16 = 2e-2
+
+
+def note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def to_dev_bf16(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def bf16_to_np(t):
+    return synth.bf16_bits_to_f32(t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+def as_np_f32(t):
+    return bf16_to_np(t) if t.dtype == torch.bfloat16 else t.float().cpu().numpy()
+
+
+def weights_for(inp, dev, compute=None, src=None):
+    compute = compute or (torch.float32 if inp.dtype == "f32" else torch.bfloat16)
+    src = src or ("bf16" if inp.dtype == "bf16" else "f32")
+    lists = []
+    for nm in ("w1", "w2", "w3"):
+        if src == "bf16":
+            b = to_dev_bf16(inp.packed[nm + "_bf16"], dev)
+        else:
+            b = torch.from_numpy(getattr(inp, nm)).to(dev)
+        lists.append([b[e].contiguous() for e in range(inp.E)])
+    return moe.register_moe_weights_gpu(lists[0], lists[1], lists[2], compute_dtype=compute)
+
+
+def x_for(inp, dev):
+    if inp.dtype == "f32":
+        return torch.from_numpy(inp.x).to(dev)
+    return to_dev_bf16(inp.packed["x_bf16"], dev)
+
+
+def rowwise_err(got, ref):
+    num = np.linalg.norm(got.astype(np.float64) - ref.astype(np.float64), axis=1)
+    den = np.maximum(np.linalg.norm(ref.astype(np.float64), axis=1), 1e-30)
+    return num / den
+
+
+def check_plan(plan, ref, T):
+    np.testing.assert_array_equal(plan["routes"].cpu().numpy().astype(np.int32), ref["routes"])
+    np.testing.assert_array_equal(plan["counts"].cpu().numpy().view(np.uint32), ref["counts"])
+    np.testing.assert_array_equal(plan["offsets"].cpu().numpy().view(np.uint32), ref["offsets"])
+    np.testing.assert_array_equal(plan["assignment_rows"].cpu().numpy().view(np.uint32), ref["assignment_rows"])
+    np.testing.assert_array_equal(plan["route_positions"].cpu().numpy().view(np.uint32), ref["route_positions"])
+
+
+def oracle_routing(inp):
+    logits = oracle.router_logits(inp.x, inp.gate)
+    routes = oracle.route_top2(logits)
+    counts, offsets, rows, pos = oracle.dispatch(routes, inp.E)
+    return dict(logits=logits, routes=routes, counts=counts, offsets=offsets,
+                assignment_rows=rows, route_positions=pos)
+
+
+# ---------------------------------------------------------------------------
+
+def test_c1_fp32_full_parity(gpu_device):
+    note("C1 fp32 T=512 full block vs oracle")
+    inp = synth.make_config("c1")
+    w = weights_for(inp, gpu_device)
+    x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+    out = moe.moe_forward_gpu(x, gate, w, out_dtype=torch.float32)
+    plan = w.plan_views(inp.T)
+    torch.cuda.synchronize()
+    ref = oracle.reference_path(inp.x, inp.gate, inp.w1, inp.w3, inp.w2)
+    np.testing.assert_array_equal(plan["logits"].cpu().numpy().view(np.uint32), ref["logits"].view(np.uint32))
+    check_plan(plan, ref, inp.T)
+    y = plan["y"].cpu().numpy()
+    assert rowwise_err(y, ref["y"]).max() <= TOL_F32
+    got = out.cpu().numpy()
+    err = rowwise_err(got, ref["out"])
+    same = np.mean(got.view(np.uint32) == ref["out"].view(np.uint32))
+    note(f"C1 max normwise err {err.max():.3e}, bit-identical fraction {same:.6f}")
+    assert err.max() <= TOL_F32
+    w.release()
+
+
+def test_c2_bf16_zipf_parity(gpu_device):
+    note("C2 bf16 T=4096 Zipf(1.1): routing full size, FFN on a token subset")
+    inp = synth.make_config("c2")
+    w = weights_for(inp, gpu_device)
+    x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+    out = moe.moe_forward_gpu(x, gate, w, out_dtype=torch.bfloat16)
+    plan = w.plan_views(inp.T)
+    torch.cuda.synchronize()
+    ref = oracle_routing(inp)
+    np.testing.assert_array_equal(plan["logits"].cpu().numpy().view(np.uint32), ref["logits"].view(np.uint32))
+    check_plan(plan, ref, inp.T)
+    counts = ref["counts"].astype(np.int64)
+    note(f"C2 counts {counts.tolist()} top/mean {counts.max() / counts.mean():.2f}")
+
+    # expert FFN + combine on a subset spanning every expert, incl. the coldest
+    rng = np.random.default_rng(0)
+    cold = int(np.argmin(counts))
+    cold_tokens = np.where((ref["routes"] == cold).any(1))[0][:32]
+    toks = np.unique(np.concatenate([np.arange(48), cold_tokens, rng.choice(inp.T, 160, replace=False)]))
+    xs = np.repeat(inp.x[toks], 2, axis=0)
+    ex = ref["routes"][toks].reshape(-1)
+    y_ref = oracle.ffn_rows(xs, ex, inp.w1, inp.w3, inp.w2)
+    pos = ref["route_positions"].reshape(-1, 2)[toks].reshape(-1).astype(np.int64)
+    y_gpu = bf16_to_np(plan["y"])
+    assert rowwise_err(y_gpu[pos], y_ref).max() <= TOL_BF16
+    out_ref = (0.5 * (y_ref[0::2].astype(np.float64) + y_ref[1::2])).astype(np.float32)
+    got = bf16_to_np(out)
+    err = rowwise_err(got[toks], out_ref)
+    note(f"C2 subset ({toks.size} tokens) max normwise err {err.max():.3e}")
+    assert err.max() <= TOL_BF16
+
+    # full size: combine identity on the GPU's own expert outputs (bf16 y),
+    # summed in fp32 and rounded once to bf16
+    p = plan["route_positions"].cpu().numpy().astype(np.int64)
+    comb = y_gpu[p[0::2]] * np.float32(0.5) + y_gpu[p[1::2]] * np.float32(0.5)
+    np.testing.assert_array_equal(got, synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(comb)))
+    assert np.isfinite(got).all()
+    w.release()
+
+
+def test_c2_deterministic_and_entry_points_agree(gpu_device):
+    note("C2 determinism + fused vs grouped vs staged entry points (T=1024)")
+    inp = synth.make_config("c2", T=1024)
+    w = weights_for(inp, gpu_device)
+    x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+    a = moe.moe_forward_gpu(x, gate, w).clone()
+    b = moe.moe_forward_gpu(x, gate, w).clone()
+    logits = torch.empty((inp.T, inp.E), dtype=torch.float32, device=gpu_device)
+    moe.matmul_transposed_gpu(x, gate, logits)
+    c = moe.moe_forward_grouped_gpu(x, logits, w).clone()
+    routes = moe.route_top2(logits)
+    counts, offsets, arows, rpos = moe.dispatch(routes, inp.E)
+    y = moe.expert_ffn(w, x, offsets, arows)
+    d = moe.combine(y, rpos, inp.T, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    for other in (b, c, d):
+        assert torch.equal(a.view(torch.int16), other.view(torch.int16))
+    w.release()
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 63, 64, 65, 127, 129, 300])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_ragged_rows_small_shapes(gpu_device, T, dtype):
+    note(f"ragged T={T} {dtype} H=256 F=64 E=16")
+    inp = synth.make_moe_inputs(T=T, H=256, E=16, F=64, dtype=dtype, seed=100 + T)
+    w = weights_for(inp, gpu_device)
+    x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+    out = moe.moe_forward_gpu(x, gate, w, out_dtype=torch.float32)
+    plan = w.plan_views(T)
+    torch.cuda.synchronize()
+    ref = oracle.reference_path(inp.x, inp.gate, inp.w1, inp.w3, inp.w2)
+    np.testing.assert_array_equal(plan["logits"].cpu().numpy().view(np.uint32), ref["logits"].view(np.uint32))
+    check_plan(plan, ref, T)
+    tol = TOL_F32 if dtype == "f32" else TOL_BF16
+    assert rowwise_err(out.cpu().numpy(), ref["out"]).max() <= tol
+    w.release()
+
+
+def test_empty_batch(gpu_device):
+    note("T=0")
+    inp = synth.make_moe_inputs(T=0, H=256, E=16, F=64, dtype="bf16", seed=1)
+    w = weights_for(inp, gpu_device)
+    x = torch.empty((0, 256), dtype=torch.bfloat16, device=gpu_device)
+    gate = torch.from_numpy(inp.gate).to(gpu_device)
+    out = moe.moe_forward_gpu(x, gate, w)
+    torch.cuda.synchronize()
+    assert out.shape == (0, 256)
+    counts, offsets, arows, rpos = moe.dispatch(torch.empty((0, 2), dtype=torch.uint8, device=gpu_device), 16)
+    torch.cuda.synchronize()
+    assert counts.abs().sum().item() == 0 and offsets.abs().sum().item() == 0
+    w.release()
+
+
+def test_all_tokens_tie_to_two_experts(gpu_device):
+    note("all logits 0: every token -> experts (0, 1); one expert owns every row")
+    inp = synth.make_moe_inputs(T=700, H=512, E=16, F=128, dtype="bf16", seed=5)
+    inp.gate[:] = 0.0
+    w = weights_for(inp, gpu_device)
+    x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+    out = moe.moe_forward_gpu(x, gate, w, out_dtype=torch.float32)
+    plan = w.plan_views(inp.T)
+    torch.cuda.synchronize()
+    ref = oracle.reference_path(inp.x, inp.gate, inp.w1, inp.w3, inp.w2)
+    assert (ref["routes"] == np.array([0, 1])).all()
+    check_plan(plan, ref, inp.T)
+    assert rowwise_err(out.cpu().numpy(), ref["out"]).max() <= TOL_BF16
+    w.release()
+
+
+def test_fp32_source_weights_convert_like_bf16_source(gpu_device):
+    note("register fp32 weights for bf16 compute == register bf16 weights")
+    inp = synth.make_moe_inputs(T=200, H=512, E=8, F=128, dtype="bf16", seed=9)
+    w_b = weights_for(inp, gpu_device, src="bf16")
+    w_f = weights_for(inp, gpu_device, src="f32", compute=torch.bfloat16)
+    x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+    a = moe.moe_forward_gpu(x, gate, w_b)
+    b = moe.moe_forward_gpu(x, gate, w_f)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    w_b.release()
+    w_f.release()
+
+
+def test_argument_errors_on_device(gpu_device):
+    note("error paths with live weights")
+    inp = synth.make_moe_inputs(T=16, H=256, E=16, F=64, dtype="bf16", seed=2)
+    w = weights_for(inp, gpu_device)
+    gate = torch.from_numpy(inp.gate).to(gpu_device)
+    xf = torch.zeros((16, 256), dtype=torch.float32, device=gpu_device)
+    with pytest.raises(ValueError):
+        moe.moe_forward_gpu(xf, gate, w)           # x dtype does not match bf16 weights
+    x = x_for(inp, gpu_device)
+    out = torch.empty((16, 256), dtype=torch.bfloat16, device=gpu_device)
+    L = capi.lib()
+    rc = L.aps_moe_forward(w.handle, x.data_ptr(), capi.DTYPE_BF16, gate.data_ptr(), 16, out.data_ptr(),
+                           capi.DTYPE_BF16, 0, 0, None)
+    assert rc == capi.APS_ERR_WORKSPACE
+    w.release()
+    with pytest.raises(ValueError):
+        moe.moe_forward_gpu(x, gate, w)            # released handle
