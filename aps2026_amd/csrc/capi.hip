@@ -50,8 +50,8 @@ struct WeightSet {
     int E = 0, H = 0, F = 0;
     int compute = APS_DTYPE_F32;
     // bf16 path
-    aps::bf16_t* w13 = nullptr;  // [E][F/64][128][H]
-    aps::bf16_t* w2b = nullptr;  // [E][H][F]
+    aps::bf16_t* w13 = nullptr;  // tile images [E][F/64][H/64][128][64]
+    aps::bf16_t* w2b = nullptr;  // tile images [E][H/128][F/64][128][64]
     // f32 path
     float* w1 = nullptr;         // [E][F][H]
     float* w3 = nullptr;         // [E][F][H]
@@ -78,15 +78,6 @@ WeightSet* lookup(uint64_t handle) {
 
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
-
-int dtype_size(int dt) {
-    switch (dt) {
-        case APS_DTYPE_F32: return 4;
-        case APS_DTYPE_BF16: return 2;
-        case APS_DTYPE_E4M3: return 1;
-        default: return 0;
-    }
-}
 
 void make_layout(const WeightSet& w, int64_t rows, aps_moe_ws_layout* L) {
     std::memset(L, 0, sizeof(*L));
@@ -238,15 +229,7 @@ int aps_moe_weights_register(const aps_moe_weights_desc* d, void* stream, uint64
         APS_HIP(hipMalloc(&w->w2b, n * 2), "hipMalloc w2");
         APS_HIP(aps::launch_pack_w13_bf16(d->w1, d->w3, src_bf16, w->w13, w->E, w->F, w->H, s),
                 "pack w1/w3");
-        for (int e = 0; e < w->E; ++e) {
-            if (src_bf16)
-                APS_HIP(hipMemcpyAsync(w->w2b + e * fh, d->w2[e], fh * 2, hipMemcpyDeviceToDevice, s),
-                        "copy w2");
-            else
-                APS_HIP(aps::launch_convert_to_bf16(static_cast<const float*>(d->w2[e]), w->w2b + e * fh,
-                                                    static_cast<int64_t>(fh), s),
-                        "convert w2");
-        }
+        APS_HIP(aps::launch_pack_w2_bf16(d->w2, src_bf16, w->w2b, w->E, w->F, w->H, s), "pack w2");
     }
     APS_HIP(hipStreamSynchronize(s), "register: synchronize");
     std::lock_guard<std::mutex> lk(g_mu);

@@ -69,25 +69,38 @@ k_combine(const void* __restrict__ y, const uint32_t* __restrict__ route_positio
     }
 }
 
-// Copies `nrows` rows of length H into the packed gate||up slab layout
-// [F/64][128][H]: source row r goes to slab r/64, row (half*64 + r%64).
+// Weight packing into MFMA tile images.  A B-operand stage of the grouped
+// GEMMs is a 128-row x 64-k bf16 tile (16 KB).  Registration stores every
+// such tile contiguously and already in the XOR-swizzled order the kernels
+// keep in LDS (physical 16-byte chunk = chunk ^ ((row >> 1) & 7)), so one
+// stage is one contiguous 16 KB block: the direct-to-LDS loads of a stage
+// spread evenly over the L2 channels (a row-major weight would put every
+// row of a stage 8 KB apart) and lane i simply copies bytes [16i, 16i+16)
+// of each 1 KB slot.
+//   w13: [E][F/64][H/64][128][64]  tile rows 0..63 = w1 rows nb*64 + r,
+//                                  rows 64..127   = w3 rows nb*64 + r - 64
+//   w2 : [E][H/128][F/64][128][64] tile rows = w2 rows nb*128 + r
+// `split` is 64 for w13 (two sources) and 128 for w2 (one source).
 template <bool SRC_BF16>
-__global__ void k_pack_rows_bf16(const void* __restrict__ src, bf16_t* __restrict__ dst, int nrows,
-                                 int H, int half) {
+__global__ void k_pack_tiles(const void* __restrict__ src_lo, const void* __restrict__ src_hi,
+                             bf16_t* __restrict__ dst, int K, int n_blocks, int split) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= static_cast<int64_t>(nrows) * H) return;
-    const int r = static_cast<int>(i / H);
-    const int k = static_cast<int>(i - static_cast<int64_t>(r) * H);
-    const int64_t drow = static_cast<int64_t>(r / 64) * 128 + half * 64 + (r % 64);
+    const int KT = K / 64;
+    const int64_t total = static_cast<int64_t>(n_blocks) * KT * 128 * 64;
+    if (i >= total) return;
+    const int pk = static_cast<int>(i & 63);
+    const int r = static_cast<int>((i >> 6) & 127);
+    const int64_t t = i >> 13;             // tile index = nb * KT + kt
+    const int kt = static_cast<int>(t % KT);
+    const int nb = static_cast<int>(t / KT);
+    const int c = (pk >> 3) ^ ((r >> 1) & 7);
+    const int k = kt * 64 + c * 8 + (pk & 7);
+    const void* src = (split == 64 && r >= 64) ? src_hi : src_lo;
+    const int64_t srow = static_cast<int64_t>(nb) * split + (r % split);
     uint32_t v;
-    if (SRC_BF16) v = static_cast<const bf16_t*>(src)[i];
-    else v = f32_to_bf16_bits(static_cast<const float*>(src)[i]);
-    dst[drow * H + k] = static_cast<bf16_t>(v);
-}
-
-__global__ void k_convert_bf16(const float* __restrict__ src, bf16_t* __restrict__ dst, int64_t n) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i < n) dst[i] = static_cast<bf16_t>(f32_to_bf16_bits(src[i]));
+    if (SRC_BF16) v = static_cast<const bf16_t*>(src)[srow * K + k];
+    else v = f32_to_bf16_bits(static_cast<const float*>(src)[srow * K + k]);
+    dst[i] = static_cast<bf16_t>(v);
 }
 
 }  // namespace
@@ -110,25 +123,29 @@ hipError_t launch_combine(const void* y, bool y_bf16, const uint32_t* route_posi
 
 hipError_t launch_pack_w13_bf16(const void* const* w1, const void* const* w3, bool src_bf16,
                                 bf16_t* dst, int experts, int ffn, int hidden, hipStream_t s) {
-    const int64_t n = static_cast<int64_t>(ffn) * hidden;
-    const dim3 grid(static_cast<unsigned>(ceil_div(n, 256)));
+    const int64_t per_expert = static_cast<int64_t>(2) * ffn * hidden;
+    const dim3 grid(static_cast<unsigned>(ceil_div(per_expert, 256)));
     for (int e = 0; e < experts; ++e) {
-        bf16_t* d = dst + static_cast<int64_t>(e) * 2 * n;
-        for (int half = 0; half < 2; ++half) {
-            const void* src = half ? w3[e] : w1[e];
-            if (src_bf16)
-                hipLaunchKernelGGL(k_pack_rows_bf16<true>, grid, dim3(256), 0, s, src, d, ffn, hidden, half);
-            else
-                hipLaunchKernelGGL(k_pack_rows_bf16<false>, grid, dim3(256), 0, s, src, d, ffn, hidden, half);
-        }
+        bf16_t* d = dst + static_cast<int64_t>(e) * per_expert;
+        if (src_bf16)
+            hipLaunchKernelGGL(k_pack_tiles<true>, grid, dim3(256), 0, s, w1[e], w3[e], d, hidden, ffn / 64, 64);
+        else
+            hipLaunchKernelGGL(k_pack_tiles<false>, grid, dim3(256), 0, s, w1[e], w3[e], d, hidden, ffn / 64, 64);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_convert_to_bf16(const float* src, bf16_t* dst, int64_t n, hipStream_t s) {
-    if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_convert_bf16, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0,
-                       s, src, dst, n);
+hipError_t launch_pack_w2_bf16(const void* const* w2, bool src_bf16, bf16_t* dst, int experts, int ffn,
+                               int hidden, hipStream_t s) {
+    const int64_t per_expert = static_cast<int64_t>(ffn) * hidden;
+    const dim3 grid(static_cast<unsigned>(ceil_div(per_expert, 256)));
+    for (int e = 0; e < experts; ++e) {
+        bf16_t* d = dst + static_cast<int64_t>(e) * per_expert;
+        if (src_bf16)
+            hipLaunchKernelGGL(k_pack_tiles<true>, grid, dim3(256), 0, s, w2[e], w2[e], d, ffn, hidden / 128, 128);
+        else
+            hipLaunchKernelGGL(k_pack_tiles<false>, grid, dim3(256), 0, s, w2[e], w2[e], d, ffn, hidden / 128, 128);
+    }
     return hipGetLastError();
 }
 

@@ -46,8 +46,8 @@ hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_c
                                    uint32_t* offsets, uint32_t* assignment_rows,
                                    uint32_t* route_positions, hipStream_t s);
 
-// bf16 MFMA path.  w13 is the packed [E][F/64][128][H] gate||up weight,
-// w2 is [E][H][F]; act/y are bf16.
+// bf16 MFMA path.  w13 / w2 are packed tile images (see launch_pack_*):
+// w13 [E][F/64][H/64][128][64], w2 [E][H/128][F/64][128][64]; act/y bf16.
 hipError_t launch_ffn_up_bf16(const bf16_t* x, const uint32_t* offsets,
                               const uint32_t* assignment_rows, const bf16_t* w13,
                               bf16_t* act, int64_t rows, int hidden, int ffn, int experts,
@@ -72,6 +72,7 @@ hipError_t launch_combine(const void* y, bool y_bf16, const uint32_t* route_posi
 // Weight packing helpers (registration time).
 hipError_t launch_pack_w13_bf16(const void* const* w1, const void* const* w3, bool src_bf16,
                                 bf16_t* dst, int experts, int ffn, int hidden, hipStream_t s);
-hipError_t launch_convert_to_bf16(const float* src, bf16_t* dst, int64_t n, hipStream_t s);
+hipError_t launch_pack_w2_bf16(const void* const* w2, bool src_bf16, bf16_t* dst, int experts, int ffn,
+                               int hidden, hipStream_t s);
 
 }  // namespace aps

@@ -15,15 +15,18 @@
 //    with register prefetch; 16-byte chunks are XOR-swizzled by (row & 7) so
 //    that both the row-contiguous global->LDS stores and the per-lane
 //    ds_read_b128 MFMA operand fetches are bank-conflict free.
-//  * w1 and w3 are re-packed at registration to [E][F/64][128][H]: the 64
-//    gate rows and 64 up rows of one column block are one contiguous 1 MB
-//    slab, so the B tile of a block is a single strided stream.
+//  * w1/w3 and w2 are re-packed at registration into swizzled 128 x 64 tile
+//    images (launch_pack_*): each B stage is one contiguous 16 KB block whose
+//    bytes are copied to LDS unchanged.
 //  * The token gather of the w1||w3 kernel is an index on the A load, as in
 //    the reference: no permuted copy of x is ever written.
-//  * Work list: blockIdx.y is a linear row-tile index over all experts
-//    (sum_e ceil(count_e / 128) tiles); each block finds its expert from
+//  * Work list: (row tile, column block) pairs over all experts (sum_e
+//    ceil(count_e / 128) row tiles), dealt to XCDs in contiguous slices so
+//    operand reuse stays inside one L2; each block finds its expert from
 //    offsets[] with a wave-uniform scan (scalar loads), so skewed experts
 //    simply own more tiles and no host round trip is needed.
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace aps {
@@ -39,8 +42,14 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kBK = 64;        // k per LDS stage
 constexpr int kTileRows = 128; // rows of an LDS operand tile
 
-// Element offset of 16-byte chunk `chunk` (0..7) of tile row `row`.
-__device__ inline int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
+// Element offset of 16-byte chunk `chunk` (0..7) of tile row `row`.  gfx950's
+// LDS has 64 four-byte banks (a 256-byte bank row = two 128-byte tile rows)
+// and serves a ds_read_b128 16 lanes at a time.  An MFMA operand fetch reads
+// the same logical chunk from 16 consecutive rows, so the physical chunk is
+// chunk ^ ((row >> 1) & 7): rows 2m and 2m+1 sit in the two halves of a bank
+// row, and the eight pairs of a 16-row group get eight different chunks --
+// sixteen distinct 16-byte bank groups, no conflict.
+__device__ inline int swz(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
 __device__ inline bf16_t f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);
@@ -55,10 +64,28 @@ __device__ inline f32x16_t mfma(bf16x8_t a, bf16x8_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Finds (expert, first position, end position) of row tile `tile` of size
-// `bm`; returns false when the tile index is past the last tile.
-__device__ inline bool locate_tile(const uint32_t* __restrict__ offsets, int E, int tile, int bm,
-                                   int& expert, uint32_t& m0, uint32_t& end) {
+// XCD-aware tile map.  The work is a list of (row tile, column block)
+// pairs, row-tile major: row tiles run over experts in order, each expert
+// owning ceil(count_e / bm) of them.  Workgroups are dealt round-robin to the
+// 8 XCDs (workgroup b runs on XCD b % 8), so XCD x takes the contiguous slice
+// [x * per, (x + 1) * per) of the list: the column blocks of one row tile
+// (sharing A rows) and the row tiles of one expert (sharing B) then meet in
+// one XCD's L2 instead of being fetched by all eight.  Returns false for
+// workgroups past the end of the list (the grid is sized for the worst case).
+constexpr int kXcds = 8;
+
+__device__ inline bool locate_tile(const uint32_t* __restrict__ offsets, int E, int bm, int n_blocks,
+                                   int& expert, uint32_t& m0, uint32_t& end, int& nb) {
+    int total_m = 0;
+    for (int e = 0; e < E; ++e) total_m += static_cast<int>((offsets[e + 1] - offsets[e] + bm - 1) / bm);
+    const int total = total_m * n_blocks;
+    const int b = blockIdx.x;
+    const int per = (total + kXcds - 1) / kXcds;
+    const int l = b / kXcds;
+    const int t = (b % kXcds) * per + l;
+    if (l >= per || t >= total) return false;
+    const int tile = t / n_blocks;
+    nb = t - tile * n_blocks;
     int cum = 0;
     for (int e = 0; e < E; ++e) {
         const uint32_t lo = offsets[e], hi = offsets[e + 1];
@@ -78,96 +105,215 @@ __device__ inline bool locate_tile(const uint32_t* __restrict__ offsets, int E, 
 // D[row(v, l)][l % 32] with row = 8 * (v / 4) + 4 * (l / 32) + v % 4.
 __device__ inline int acc_row(int v, int lane) { return ((v >> 2) << 3) + ((lane >> 5) << 2) + (v & 3); }
 
-// silu(g) * u for the bf16 path (fp32 math, hardware exp2).
+// silu(g) * u for the bf16 path: fp32 math with the hardware exp2 and
+// reciprocal (result is rounded to bf16, far coarser than their error).
 __device__ inline float swiglu(float g, float u) {
-    return g / (1.0f + __expf(-g)) * u;
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
 // ---------------------------------------------------------------------------
-// act[p][n] = silu(x[t] . w1[e][n]) * (x[t] . w3[e][n]),  t = assignment_rows[p]
-__global__ void __launch_bounds__(256, 2)
-k_ffn_up_bf16(const bf16_t* __restrict__ x, const uint32_t* __restrict__ offsets,
-              const uint32_t* __restrict__ assignment_rows, const bf16_t* __restrict__ w13,
-              bf16_t* __restrict__ act, int H, int F, int E) {
-    __shared__ __align__(16) bf16_t As[2][kTileRows * kBK];
-    __shared__ __align__(16) bf16_t Bs[2][kTileRows * kBK];
+// Shared main loop.  A and B tiles (128 rows x 64 k each) stream from global
+// memory straight into an S-stage LDS ring with global_load_lds_dwordx4 (no
+// VGPR staging): lane i of a wave writes LDS bytes [16i, 16i+16) of a 1 KB
+// slot = 8 tile rows, so the XOR swizzle is applied on the global side: lane
+// i fetches the logical chunk that swz() places at its slot.
+// Each wave issues 4 A + 4 B loads per stage (rows 32w .. 32w+31).  With the
+// swizzle of swz(), lane i of load j (rows 32w + 8j + i/8) fetches logical
+// chunk (i & 7) ^ ((4 * (j & 1) + (i >> 4)) & 7).  Loads
+// run S-1 stages ahead; before consuming stage kt a wave waits until at most
+// the loads of the later stages are outstanding (vmcnt), then one s_barrier
+// publishes the stage to all waves and retires the oldest slot for reuse.
+// The barrier is a raw s_barrier (not __syncthreads, whose workgroup fence
+// would drain every in-flight load and serialise the ring).
 
-    int e;
-    uint32_t m0, end;
-    if (!locate_tile(offsets, E, blockIdx.y, kUpBM, e, m0, end)) return;
-    const int nb = blockIdx.x;  // 64-column block of the intermediate dim
+struct RowPtrs {
+    const bf16_t* p0;
+    const bf16_t* p1;
+    const bf16_t* p2;
+    const bf16_t* p3;
+};
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int lc = tid & 7, lr = tid >> 3;
+#define APS_GP(p) ((const __attribute__((address_space(1))) void*)(p))
+#define APS_LP(p) ((__attribute__((address_space(3))) void*)(p))
 
-    // Per-thread load addressing as vector values (kept in registers): the
-    // four A rows this thread stages are tokens a_tok[j] (or -1 past the
-    // expert's last row); B rows are lr + 32j of the block's 128-row slab.
-    i32x4_t a_tok;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t p = m0 + lr + 32 * j;
-        a_tok[j] = p < end ? static_cast<int>(assignment_rows[p]) : -1;
+__device__ inline void dma16(const bf16_t* src, bf16_t* lds_slot) {
+    __builtin_amdgcn_global_load_lds(APS_GP(src), APS_LP(lds_slot), 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt[5:4] at bits [15:14]); n must be a constant.
+template <int N>
+__device__ inline void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+}
+
+__device__ inline void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int S>
+struct Ring {
+    bf16_t a[S][kTileRows * kBK];
+    bf16_t b[S][kTileRows * kBK];
+};
+
+// Stage `kt`'s loads of this wave go to ring slot kt % S.  A row pointers
+// advance by 64 elements per stage (row-major rows); B pointers by one
+// 128 x 64 tile image (8192 elements).  issue_a / issue_b each send 4 loads.
+constexpr int kTileElems = kTileRows * kBK;
+
+template <int S>
+__device__ inline void issue_a(Ring<S>& ring, const RowPtrs& A, int kt, int wave) {
+    bf16_t* a = ring.a[kt % S] + wave * 32 * kBK;
+    const int ka = kt * kBK;
+    dma16(A.p0 + ka, a);
+    dma16(A.p1 + ka, a + 8 * kBK);
+    dma16(A.p2 + ka, a + 16 * kBK);
+    dma16(A.p3 + ka, a + 24 * kBK);
+}
+
+template <int S>
+__device__ inline void issue_b(Ring<S>& ring, const RowPtrs& B, int kt, int wave) {
+    bf16_t* b = ring.b[kt % S] + wave * 32 * kBK;
+    const int kb = kt * kTileElems;
+    dma16(B.p0 + kb, b);
+    dma16(B.p1 + kb, b + 8 * kBK);
+    dma16(B.p2 + kb, b + 16 * kBK);
+    dma16(B.p3 + kb, b + 24 * kBK);
+}
+
+// Wait until this wave's loads of stage kt have landed: the loads of the
+// min(S-2, KT-1-kt) later stages (8 each) may stay in flight.
+template <int S>
+__device__ inline void wait_stage(int later) {
+    if constexpr (S >= 4) {
+        if (later >= 2) { wait_vm_lgkm0<16>(); return; }
     }
-    const bf16_t* b_ptr = w13 + (static_cast<int64_t>(e) * (F / kUpBN) + nb) * 128 * static_cast<int64_t>(H) +
-                          static_cast<int64_t>(lr) * H + lc * 8;
-    const int64_t b_step = 32 * static_cast<int64_t>(H);
-    u32x4_t ra[4], rb[4];
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int tok = a_tok[j];
-            ra[j] = tok >= 0 ? *reinterpret_cast<const u32x4_t*>(x + static_cast<int64_t>(tok) * H + k0 + lc * 8)
-                             : u32x4_t{0u, 0u, 0u, 0u};
-            rb[j] = *reinterpret_cast<const u32x4_t*>(b_ptr + j * b_step + k0);
-        }
-    };
-    auto lstore = [&](int st) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = lr + 32 * j;
-            *reinterpret_cast<u32x4_t*>(&As[st][swz(row, lc)]) = ra[j];
-            *reinterpret_cast<u32x4_t*>(&Bs[st][swz(row, lc)]) = rb[j];
-        }
-    };
+    if constexpr (S >= 3) {
+        if (later >= 1) { wait_vm_lgkm0<8>(); return; }
+    }
+    wait_vm_lgkm0<0>();
+}
 
-    f32x16_t acc[2][2];
+// MFMA operands of one 16-k step: two A fragments (rows wm*64 + 32i) and two
+// B fragments (rows bb0, bb1).
+struct Frags {
+    bf16x8_t a[2];
+    bf16x8_t b[2];
+};
+
+__device__ inline void load_frags(Frags& f, const bf16_t* as, const bf16_t* bs, int kk, int lane, int wm,
+                                  int bb0, int bb1) {
+    const int chunk = kk * 2 + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        f.a[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(as + swz(wm * 64 + i * 32 + (lane & 31), chunk)));
+    f.b[0] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(bs + swz(bb0 + (lane & 31), chunk)));
+    f.b[1] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(bs + swz(bb1 + (lane & 31), chunk)));
+}
+
+__device__ inline void mma(const Frags& f, f32x16_t (&acc)[2][2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma(f.a[i], f.b[j], acc[i][j]);
+}
+
+#define APS_PIN() __builtin_amdgcn_sched_barrier(0)
+
+// acc[i][j] += A rows (wm*64 + 32i ..) x B rows (bb0/bb1 ..) over K = KT*64.
+// Per stage: the LDS operand reads of step kk+1 are issued before the MFMAs
+// of step kk (two fragment sets, ping-pong), and the next stage's 8 loads
+// are spread between the MFMA groups; APS_PIN keeps that order.
+template <int S>
+__device__ inline void mainloop(Ring<S>& ring, const RowPtrs& A, const RowPtrs& B, int KT, int wave,
+                                int lane, int wm, int bb0, int bb1, f32x16_t (&acc)[2][2]) {
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) {
+        if (s < KT) {
+            issue_a<S>(ring, A, s, wave);
+            issue_b<S>(ring, B, s, wave);
+        }
+    }
+    for (int kt = 0; kt < KT; ++kt) {
+        const int later = (KT - 1 - kt) < (S - 2) ? (KT - 1 - kt) : (S - 2);
+        wait_stage<S>(later);
+        raw_barrier();
+        const bool more = kt + S - 1 < KT;
+        const bf16_t* as = ring.a[kt % S];
+        const bf16_t* bs = ring.b[kt % S];
+        Frags f0, f1;
+        load_frags(f0, as, bs, 0, lane, wm, bb0, bb1);
+        if (more) issue_a<S>(ring, A, kt + S - 1, wave);
+        load_frags(f1, as, bs, 1, lane, wm, bb0, bb1);
+        APS_PIN();
+        mma(f0, acc);
+        APS_PIN();
+        if (more) issue_b<S>(ring, B, kt + S - 1, wave);
+        load_frags(f0, as, bs, 2, lane, wm, bb0, bb1);
+        APS_PIN();
+        mma(f1, acc);
+        APS_PIN();
+        load_frags(f1, as, bs, 3, lane, wm, bb0, bb1);
+        APS_PIN();
+        mma(f0, acc);
+        APS_PIN();
+        mma(f1, acc);
+    }
+}
+
+// Row (within the 128-row tile) and logical chunk of this lane's load in
+// load instruction j: row 32*wave + 8j + lane/8 lands at physical chunk
+// lane & 7, so it must fetch logical chunk (lane & 7) ^ ((row >> 1) & 7).
+__device__ inline int dma_row(int wave, int j, int lane) { return wave * 32 + j * 8 + (lane >> 3); }
+__device__ inline int dma_chunk(int wave, int j, int lane) {
+    return (lane & 7) ^ ((dma_row(wave, j, lane) >> 1) & 7);
+}
+
+__device__ inline void zero_acc(f32x16_t (&acc)[2][2]) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][h][v] = 0.0f;
+}
 
-    const int KT = H / kBK;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int st = kt & 1;
-        if (kt + 1 < KT) gload((kt + 1) * kBK);
-#pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const int chunk = kk * 2 + (lane >> 5);
-            bf16x8_t af[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int row = wm * 64 + i * 32 + (lane & 31);
-                af[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&As[st][swz(row, chunk)]));
-            }
-            const int bg_row = wn * 32 + (lane & 31);
-            const bf16x8_t bg = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&Bs[st][swz(bg_row, chunk)]));
-            const bf16x8_t bu = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&Bs[st][swz(bg_row + 64, chunk)]));
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                acc[i][0] = mfma(af[i], bg, acc[i][0]);
-                acc[i][1] = mfma(af[i], bu, acc[i][1]);
-            }
-        }
-        if (kt + 1 < KT) lstore(st ^ 1);
-        __syncthreads();
-    }
+// ---------------------------------------------------------------------------
+// act[p][n] = silu(x[t] . w1[e][n]) * (x[t] . w3[e][n]),  t = assignment_rows[p]
+// Block: 128 positions x 64 intermediate columns (64 gate + the same 64 up
+// rows of the packed slab); wave (wm, wn) owns rows wm*64.. and gate/up
+// columns wn*32.. so SiLU(g)*u closes inside each lane.
+template <int S, int OCC>
+__global__ void __launch_bounds__(256, OCC)
+k_ffn_up_bf16(const bf16_t* __restrict__ x, const uint32_t* __restrict__ offsets,
+              const uint32_t* __restrict__ assignment_rows, const bf16_t* __restrict__ w13,
+              bf16_t* __restrict__ act, int H, int F, int E) {
+    __shared__ __align__(16) Ring<S> ring;
+
+    int e, nb;
+    uint32_t m0, end;
+    if (!locate_tile(offsets, E, kUpBM, F / kUpBN, e, m0, end, nb)) return;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, lives in an SGPR
+    const int wm = wave >> 1, wn = wave & 1;
+    // A: gathered token rows (positions past the expert's end reuse its last
+    // row -- always a valid address; those output rows are never stored)
+    auto a_row = [&](int j) {
+        uint32_t p = m0 + dma_row(wave, j, lane);
+        p = p < end ? p : end - 1;
+        return x + static_cast<int64_t>(assignment_rows[p]) * H + dma_chunk(wave, j, lane) * 8;
+    };
+    const RowPtrs A{a_row(0), a_row(1), a_row(2), a_row(3)};
+    // B: tile images, one contiguous 16 KB per stage; load j of this wave
+    // copies the 1 KB holding tile rows 32w + 8j .. +8.
+    const bf16_t* slab = w13 + (static_cast<int64_t>(e) * (F / kUpBN) + nb) * 128 * static_cast<int64_t>(H);
+    auto b_row = [&](int j) { return slab + (wave * 32 + j * 8) * kBK + lane * 8; };
+    const RowPtrs B{b_row(0), b_row(1), b_row(2), b_row(3)};
+
+    f32x16_t acc[2][2];
+    zero_acc(acc);
+    mainloop<S>(ring, A, B, H / kBK, wave, lane, wm, wn * 32, 64 + wn * 32, acc);
 
     const int col = nb * kUpBN + wn * 32 + (lane & 31);
 #pragma unroll
@@ -181,81 +327,33 @@ k_ffn_up_bf16(const bf16_t* __restrict__ x, const uint32_t* __restrict__ offsets
 }
 
 // ---------------------------------------------------------------------------
-// y[p][n] = act[p] . w2[e][n]
-__global__ void __launch_bounds__(256, 2)
+// y[p][n] = act[p] . w2[e][n]; block: 128 positions x 128 hidden columns.
+template <int S, int OCC>
+__global__ void __launch_bounds__(256, OCC)
 k_ffn_down_bf16(const bf16_t* __restrict__ act, const uint32_t* __restrict__ offsets,
                 const bf16_t* __restrict__ w2, bf16_t* __restrict__ y, int H, int F, int E) {
-    __shared__ __align__(16) bf16_t As[2][kTileRows * kBK];
-    __shared__ __align__(16) bf16_t Bs[2][kTileRows * kBK];
+    __shared__ __align__(16) Ring<S> ring;
 
-    int e;
+    int e, nb;
     uint32_t m0, end;
-    if (!locate_tile(offsets, E, blockIdx.y, kDownBM, e, m0, end)) return;
-    const int nb = blockIdx.x;  // 128-column block of the hidden dim
+    if (!locate_tile(offsets, E, kDownBM, H / kDownBN, e, m0, end, nb)) return;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, lives in an SGPR
     const int wm = wave >> 1, wn = wave & 1;
-    const int lc = tid & 7, lr = tid >> 3;
-
-    // A rows m0 + lr + 32j are live while below `end`; B rows are hidden
-    // columns nb*128 + lr + 32j of w2[e].
-    const uint32_t a_row0 = m0 + lr;
-    const bf16_t* a_ptr = act + static_cast<int64_t>(a_row0) * F + lc * 8;
-    const int64_t a_step = 32 * static_cast<int64_t>(F);
-    const bf16_t* b_ptr = w2 + (static_cast<int64_t>(e) * H + static_cast<int64_t>(nb) * kDownBN + lr) * F + lc * 8;
-    const int64_t b_step = 32 * static_cast<int64_t>(F);
-    u32x4_t ra[4], rb[4];
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            ra[j] = a_row0 + 32 * j < end ? *reinterpret_cast<const u32x4_t*>(a_ptr + j * a_step + k0)
-                                          : u32x4_t{0u, 0u, 0u, 0u};
-            rb[j] = *reinterpret_cast<const u32x4_t*>(b_ptr + j * b_step + k0);
-        }
+    auto a_row = [&](int j) {
+        uint32_t p = m0 + dma_row(wave, j, lane);
+        p = p < end ? p : end - 1;
+        return act + static_cast<int64_t>(p) * F + dma_chunk(wave, j, lane) * 8;
     };
-    auto lstore = [&](int st) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = lr + 32 * j;
-            *reinterpret_cast<u32x4_t*>(&As[st][swz(row, lc)]) = ra[j];
-            *reinterpret_cast<u32x4_t*>(&Bs[st][swz(row, lc)]) = rb[j];
-        }
-    };
+    const RowPtrs A{a_row(0), a_row(1), a_row(2), a_row(3)};
+    const bf16_t* wb = w2 + (static_cast<int64_t>(e) * (H / kDownBN) + nb) * 128 * static_cast<int64_t>(F);
+    auto b_row = [&](int j) { return wb + (wave * 32 + j * 8) * kBK + lane * 8; };
+    const RowPtrs B{b_row(0), b_row(1), b_row(2), b_row(3)};
 
     f32x16_t acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][h][v] = 0.0f;
-
-    const int KT = F / kBK;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int st = kt & 1;
-        if (kt + 1 < KT) gload((kt + 1) * kBK);
-#pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const int chunk = kk * 2 + (lane >> 5);
-            bf16x8_t af[2], bf[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int row = wm * 64 + i * 32 + (lane & 31);
-                af[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&As[st][swz(row, chunk)]));
-                const int brow = wn * 64 + i * 32 + (lane & 31);
-                bf[i] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&Bs[st][swz(brow, chunk)]));
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma(af[i], bf[j], acc[i][j]);
-        }
-        if (kt + 1 < KT) lstore(st ^ 1);
-        __syncthreads();
-    }
+    zero_acc(acc);
+    mainloop<S>(ring, A, B, F / kBK, wave, lane, wm, wn * 64, wn * 64 + 32, acc);
 
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -273,16 +371,38 @@ k_ffn_down_bf16(const bf16_t* __restrict__ act, const uint32_t* __restrict__ off
 
 }  // namespace
 
+// Pipeline depth / occupancy variant (S stages of 32 KB; OCC blocks per CU).
+// APS_FFN_VARIANT selects one for tuning runs: 0 = (4, 1), 1 = (2, 2),
+// 2 = (3, 1).
+static int ffn_variant() {
+    static const int v = [] {
+        const char* e = getenv("APS_FFN_VARIANT");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
 hipError_t launch_ffn_up_bf16(const bf16_t* x, const uint32_t* offsets,
                               const uint32_t* assignment_rows, const bf16_t* w13,
                               bf16_t* act, int64_t rows, int hidden, int ffn, int experts,
                               hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (hidden % kBK != 0 || ffn % kUpBN != 0) return hipErrorInvalidValue;
-    const dim3 grid(static_cast<unsigned>(ffn / kUpBN),
-                    static_cast<unsigned>(max_row_tiles(2 * rows, kUpBM, experts)));
-    hipLaunchKernelGGL(k_ffn_up_bf16, grid, dim3(256), 0, s, x, offsets, assignment_rows, w13, act,
-                       hidden, ffn, experts);
+    const int64_t tiles = max_row_tiles(2 * rows, kUpBM, experts) * (ffn / kUpBN);
+    const dim3 grid(static_cast<unsigned>(ceil_div(tiles, kXcds) * kXcds));
+    switch (ffn_variant()) {
+        case 1:
+            hipLaunchKernelGGL((k_ffn_up_bf16<2, 2>), grid, dim3(256), 0, s, x, offsets, assignment_rows, w13,
+                               act, hidden, ffn, experts);
+            break;
+        case 2:
+            hipLaunchKernelGGL((k_ffn_up_bf16<3, 1>), grid, dim3(256), 0, s, x, offsets, assignment_rows, w13,
+                               act, hidden, ffn, experts);
+            break;
+        default:
+            hipLaunchKernelGGL((k_ffn_up_bf16<4, 1>), grid, dim3(256), 0, s, x, offsets, assignment_rows, w13,
+                               act, hidden, ffn, experts);
+    }
     return hipGetLastError();
 }
 
@@ -291,10 +411,21 @@ hipError_t launch_ffn_down_bf16(const bf16_t* act, const uint32_t* offsets, cons
                                 hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (hidden % kDownBN != 0 || ffn % kBK != 0) return hipErrorInvalidValue;
-    const dim3 grid(static_cast<unsigned>(hidden / kDownBN),
-                    static_cast<unsigned>(max_row_tiles(2 * rows, kDownBM, experts)));
-    hipLaunchKernelGGL(k_ffn_down_bf16, grid, dim3(256), 0, s, act, offsets, w2, y, hidden, ffn,
-                       experts);
+    const int64_t tiles = max_row_tiles(2 * rows, kDownBM, experts) * (hidden / kDownBN);
+    const dim3 grid(static_cast<unsigned>(ceil_div(tiles, kXcds) * kXcds));
+    switch (ffn_variant()) {
+        case 1:
+            hipLaunchKernelGGL((k_ffn_down_bf16<2, 2>), grid, dim3(256), 0, s, act, offsets, w2, y, hidden, ffn,
+                               experts);
+            break;
+        case 2:
+            hipLaunchKernelGGL((k_ffn_down_bf16<3, 1>), grid, dim3(256), 0, s, act, offsets, w2, y, hidden, ffn,
+                               experts);
+            break;
+        default:
+            hipLaunchKernelGGL((k_ffn_down_bf16<4, 1>), grid, dim3(256), 0, s, act, offsets, w2, y, hidden, ffn,
+                               experts);
+    }
     return hipGetLastError();
 }
 
