@@ -14,11 +14,17 @@ namespace {
 
 __device__ inline float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
+// fp32 -> bf16 bits, round to nearest even (gfx950 v_cvt_pk_bf16_f32).
 __device__ inline uint32_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t pack2_bf16(float lo, float hi) {
+    bf16x2_t v;
+    v[0] = static_cast<__bf16>(lo);
+    v[1] = static_cast<__bf16>(hi);
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 template <bool YBF16>
@@ -57,10 +63,10 @@ k_combine(const void* __restrict__ y, const uint32_t* __restrict__ route_positio
     for (int k = 0; k < 8; ++k) o[k] = __fadd_rn(__fmul_rn(0.5f, a[k]), __fmul_rn(0.5f, b[k]));
     if (OBF16) {
         uint4 q;
-        q.x = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
-        q.y = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
-        q.z = f32_to_bf16_bits(o[4]) | (f32_to_bf16_bits(o[5]) << 16);
-        q.w = f32_to_bf16_bits(o[6]) | (f32_to_bf16_bits(o[7]) << 16);
+        q.x = pack2_bf16(o[0], o[1]);
+        q.y = pack2_bf16(o[2], o[3]);
+        q.z = pack2_bf16(o[4], o[5]);
+        q.w = pack2_bf16(o[6], o[7]);
         *reinterpret_cast<uint4*>(static_cast<bf16_t*>(out) + t * H + c) = q;
     } else {
         float* d = static_cast<float*>(out) + t * H + c;

@@ -33,6 +33,46 @@ __host__ __device__ inline int64_t max_row_tiles(int64_t n, int64_t bm, int64_t 
     return ceil_div(n, bm) + E;
 }
 
+// Row-tile lookup shared by the grouped GEMMs.  Row tiles run over experts
+// in order, expert e owning ceil(count_e / bm) tiles of bm positions.  One
+// vector load brings offsets[0..E] into lanes 0..E, a wave prefix scan turns
+// per-expert tile counts into running totals, and a ballot finds the expert
+// of `tile` -- one memory round trip instead of a dependent chain of scalar
+// loads.  Every output is wave-uniform.  E <= 64.
+struct RowTile {
+    int expert;
+    uint32_t m0, end;
+};
+
+__device__ inline int wave_tile_scan(const uint32_t* __restrict__ offsets, int E, int bm, uint32_t& lo,
+                                     uint32_t& hi, int& incl) {
+    const int lane = threadIdx.x & 63;
+    lo = lane < E ? offsets[lane] : 0u;
+    hi = __shfl_down(lo, 1);
+    if (lane == E - 1) hi = offsets[E];
+    const int nt = lane < E ? static_cast<int>((hi - lo + bm - 1) / bm) : 0;
+    incl = nt;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d);
+        if (lane >= d) incl += v;
+    }
+    return __shfl(incl, 63);  // total row tiles
+}
+
+__device__ inline RowTile wave_find_tile(int tile, int bm, uint32_t lo, uint32_t hi, int incl, int E) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t m = __ballot(lane < E && incl > tile);
+    const int e = __ffsll(static_cast<unsigned long long>(m)) - 1;
+    const int start = __shfl(incl, e > 0 ? e - 1 : 0);
+    const int before = e > 0 ? start : 0;
+    RowTile r;
+    r.expert = e;
+    r.m0 = __shfl(lo, e) + static_cast<uint32_t>(tile - before) * bm;
+    r.end = __shfl(hi, e);
+    return r;
+}
+
 // ---- launchers (defined in the .hip files) --------------------------------
 
 hipError_t launch_router_logits(const void* x, bool x_bf16, const float* gate, int64_t rows,

@@ -57,23 +57,20 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
     const int64_t ntiles = (rows + kWave - 1) / kWave;
     if (tile >= ntiles) return;  // wave-uniform
 
-    // 1. per-expert totals and the prefix before this tile (lane = expert)
+    // 1. per-expert totals and the prefix before this tile (lane = expert).
+    //    Loads go out 32 tiles at a time (independent), so the wave waits a
+    //    handful of L2 round trips rather than one per tile.
     uint32_t total = 0, before = 0;
     if (lane < E) {
-        int64_t j = 0;
-        for (; j + 4 <= ntiles; j += 4) {
-            const uint32_t c0 = tile_counts[(j + 0) * E + lane];
-            const uint32_t c1 = tile_counts[(j + 1) * E + lane];
-            const uint32_t c2 = tile_counts[(j + 2) * E + lane];
-            const uint32_t c3 = tile_counts[(j + 3) * E + lane];
-            total += c0 + c1 + c2 + c3;
-            before += (j + 0 < tile ? c0 : 0u) + (j + 1 < tile ? c1 : 0u) +
-                      (j + 2 < tile ? c2 : 0u) + (j + 3 < tile ? c3 : 0u);
-        }
-        for (; j < ntiles; ++j) {
-            const uint32_t c = tile_counts[j * E + lane];
-            total += c;
-            if (j < tile) before += c;
+        for (int64_t j0 = 0; j0 < ntiles; j0 += 32) {
+            uint32_t c[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) c[i] = j0 + i < ntiles ? tile_counts[(j0 + i) * E + lane] : 0u;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                total += c[i];
+                before += j0 + i < tile ? c[i] : 0u;
+            }
         }
     }
     // 2. exclusive scan of totals over lanes 0..E-1

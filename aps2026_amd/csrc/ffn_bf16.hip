@@ -51,12 +51,7 @@ constexpr int kTileRows = 128; // rows of an LDS operand tile
 // sixteen distinct 16-byte bank groups, no conflict.
 __device__ inline int swz(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
-__device__ inline bf16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<bf16_t>(u >> 16);
-}
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ inline bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -76,8 +71,9 @@ constexpr int kXcds = 8;
 
 __device__ inline bool locate_tile(const uint32_t* __restrict__ offsets, int E, int bm, int n_blocks,
                                    int& expert, uint32_t& m0, uint32_t& end, int& nb) {
-    int total_m = 0;
-    for (int e = 0; e < E; ++e) total_m += static_cast<int>((offsets[e + 1] - offsets[e] + bm - 1) / bm);
+    uint32_t lo, hi;
+    int incl;
+    const int total_m = wave_tile_scan(offsets, E, bm, lo, hi, incl);
     const int total = total_m * n_blocks;
     const int b = blockIdx.x;
     const int per = (total + kXcds - 1) / kXcds;
@@ -86,24 +82,27 @@ __device__ inline bool locate_tile(const uint32_t* __restrict__ offsets, int E, 
     if (l >= per || t >= total) return false;
     const int tile = t / n_blocks;
     nb = t - tile * n_blocks;
-    int cum = 0;
-    for (int e = 0; e < E; ++e) {
-        const uint32_t lo = offsets[e], hi = offsets[e + 1];
-        const int nt = static_cast<int>((hi - lo + bm - 1) / bm);
-        if (tile < cum + nt) {
-            expert = e;
-            m0 = lo + static_cast<uint32_t>(tile - cum) * bm;
-            end = hi;
-            return true;
-        }
-        cum += nt;
-    }
-    return false;
+    const RowTile r = wave_find_tile(tile, bm, lo, hi, incl, E);
+    expert = r.expert;
+    m0 = r.m0;
+    end = r.end;
+    return true;
 }
 
 // The 32x32 MFMA accumulator layout: register v of lane l holds
-// D[row(v, l)][l % 32] with row = 8 * (v / 4) + 4 * (l / 32) + v % 4.
-__device__ inline int acc_row(int v, int lane) { return ((v >> 2) << 3) + ((lane >> 5) << 2) + (v & 3); }
+// D[8 * (v / 4) + 4 * (l / 32) + v % 4][l % 32].  With the B operand first
+// (see mma()), D's row index is the output column: register group q = v / 4
+// of lane l covers output columns 8q + 4 * (l / 32) .. +3 of token row l % 32.
+
+// Two fp32 -> packed bf16, round to nearest even (one v_cvt_pk_bf16_f32).
+__device__ inline uint32_t pack2_bf16(float lo, float hi) {
+    bf16x2_t v;
+    v[0] = static_cast<__bf16>(lo);
+    v[1] = static_cast<__bf16>(hi);
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // silu(g) * u for the bf16 path: fp32 math with the hardware exp2 and
 // reciprocal (result is rounded to bf16, far coarser than their error).
@@ -211,11 +210,15 @@ __device__ inline void load_frags(Frags& f, const bf16_t* as, const bf16_t* bs, 
     f.b[1] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(bs + swz(bb1 + (lane & 31), chunk)));
 }
 
+// B fragments go in the MFMA's first operand slot: the result is then the
+// transposed tile, so each lane holds one token row (lane % 32) and, per
+// accumulator register group, four consecutive output columns -- the shape
+// the epilogue stores as 8-byte runs.
 __device__ inline void mma(const Frags& f, f32x16_t (&acc)[2][2]) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma(f.a[i], f.b[j], acc[i][j]);
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma(f.b[j], f.a[i], acc[i][j]);
 }
 
 #define APS_PIN() __builtin_amdgcn_sched_barrier(0)
@@ -315,14 +318,35 @@ k_ffn_up_bf16(const bf16_t* __restrict__ x, const uint32_t* __restrict__ offsets
     zero_acc(acc);
     mainloop<S>(ring, A, B, H / kBK, wave, lane, wm, wn * 32, 64 + wn * 32, acc);
 
-    const int col = nb * kUpBN + wn * 32 + (lane & 31);
+    // Epilogue: SwiGLU in registers, the 128 x 64 bf16 act tile staged in the
+    // (now idle) LDS ring, then written out as 16-byte row chunks.
+    constexpr int kPitch = kUpBN + 8;  // 144-byte rows: 16-byte aligned, banks staggered
+    bf16_t* stage = ring.a[0];
+    wait_vm_lgkm0<0>();
+    raw_barrier();
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
+        const int row = wm * 64 + i * 32 + (lane & 31);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const uint32_t p = m0 + wm * 64 + i * 32 + acc_row(v, lane);
-            if (p < end) act[static_cast<int64_t>(p) * F + col] = f32_to_bf16(swiglu(acc[i][0][v], acc[i][1][v]));
+        for (int q = 0; q < 4; ++q) {
+            const int col = wn * 32 + 8 * q + 4 * (lane >> 5);
+            const u32x2_t v = {pack2_bf16(swiglu(acc[i][0][4 * q + 0], acc[i][1][4 * q + 0]),
+                                          swiglu(acc[i][0][4 * q + 1], acc[i][1][4 * q + 1])),
+                               pack2_bf16(swiglu(acc[i][0][4 * q + 2], acc[i][1][4 * q + 2]),
+                                          swiglu(acc[i][0][4 * q + 3], acc[i][1][4 * q + 3]))};
+            *reinterpret_cast<u32x2_t*>(stage + row * kPitch + col) = v;
         }
+    }
+    wait_vm_lgkm0<0>();
+    raw_barrier();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int id = tid + 256 * c;   // 128 rows x 8 chunks of 16 bytes
+        const int r = id >> 3, cc = id & 7;
+        const uint32_t p = m0 + r;
+        if (p < end)
+            *reinterpret_cast<u32x4_t*>(act + static_cast<int64_t>(p) * F + nb * kUpBN + cc * 8) =
+                *reinterpret_cast<const u32x4_t*>(stage + r * kPitch + cc * 8);
     }
 }
 
@@ -355,17 +379,36 @@ k_ffn_down_bf16(const bf16_t* __restrict__ act, const uint32_t* __restrict__ off
     zero_acc(acc);
     mainloop<S>(ring, A, B, F / kBK, wave, lane, wm, wn * 64, wn * 64 + 32, acc);
 
+    // Epilogue: the 128 x 128 bf16 y tile staged in the (now idle) LDS ring,
+    // then written out as 16-byte row chunks (256 contiguous bytes per row).
+    constexpr int kPitch = kDownBN + 8;  // 272-byte rows: 16-byte aligned
+    bf16_t* stage = ring.a[0];
+    wait_vm_lgkm0<0>();
+    raw_barrier();
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
+        const int row = wm * 64 + i * 32 + (lane & 31);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int64_t col = static_cast<int64_t>(nb) * kDownBN + wn * 64 + j * 32 + (lane & 31);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const uint32_t p = m0 + wm * 64 + i * 32 + acc_row(v, lane);
-                if (p < end) y[static_cast<int64_t>(p) * H + col] = f32_to_bf16(acc[i][j][v]);
+            for (int q = 0; q < 4; ++q) {
+                const int col = wn * 64 + j * 32 + 8 * q + 4 * (lane >> 5);
+                const u32x2_t v = {pack2_bf16(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1]),
+                                   pack2_bf16(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
+                *reinterpret_cast<u32x2_t*>(stage + row * kPitch + col) = v;
             }
         }
+    }
+    wait_vm_lgkm0<0>();
+    raw_barrier();
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int id = tid + 256 * c;   // 128 rows x 16 chunks of 16 bytes
+        const int r = id >> 4, cc = id & 15;
+        const uint32_t p = m0 + r;
+        if (p < end)
+            *reinterpret_cast<u32x4_t*>(y + static_cast<int64_t>(p) * H + static_cast<int64_t>(nb) * kDownBN + cc * 8) =
+                *reinterpret_cast<const u32x4_t*>(stage + r * kPitch + cc * 8);
     }
 }
 

@@ -22,19 +22,15 @@ constexpr int kBK = 16;
 
 __device__ inline bool locate_tile(const uint32_t* __restrict__ offsets, int E, int tile, int bm,
                                    int& expert, uint32_t& m0, uint32_t& end) {
-    int cum = 0;
-    for (int e = 0; e < E; ++e) {
-        const uint32_t lo = offsets[e], hi = offsets[e + 1];
-        const int nt = static_cast<int>((hi - lo + bm - 1) / bm);
-        if (tile < cum + nt) {
-            expert = e;
-            m0 = lo + static_cast<uint32_t>(tile - cum) * bm;
-            end = hi;
-            return true;
-        }
-        cum += nt;
-    }
-    return false;
+    uint32_t lo, hi;
+    int incl;
+    const int total = wave_tile_scan(offsets, E, bm, lo, hi, incl);
+    if (tile >= total) return false;
+    const RowTile r = wave_find_tile(tile, bm, lo, hi, incl, E);
+    expert = r.expert;
+    m0 = r.m0;
+    end = r.end;
+    return true;
 }
 
 // a = g / (1 + (float)exp((double)-g)) * u, each operation rounded on its own
