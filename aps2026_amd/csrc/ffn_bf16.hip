@@ -415,7 +415,8 @@ k_ffn_down_bf16(const bf16_t* __restrict__ act, const uint32_t* __restrict__ off
 }  // namespace
 
 // Pipeline depth / occupancy variant (S stages of 32 KB; OCC blocks per CU).
-// APS_FFN_VARIANT selects one for tuning runs: 0 = (4, 1), 1 = (2, 2),
+// Default (2, 2): two stages per block, two blocks per CU (measured fastest
+// at C2).  APS_FFN_VARIANT selects another for tuning runs: 1 = (4, 1),
 // 2 = (3, 1).
 static int ffn_variant() {
     static const int v = [] {
@@ -435,7 +436,7 @@ hipError_t launch_ffn_up_bf16(const bf16_t* x, const uint32_t* offsets,
     const dim3 grid(static_cast<unsigned>(ceil_div(tiles, kXcds) * kXcds));
     switch (ffn_variant()) {
         case 1:
-            hipLaunchKernelGGL((k_ffn_up_bf16<2, 2>), grid, dim3(256), 0, s, x, offsets, assignment_rows, w13,
+            hipLaunchKernelGGL((k_ffn_up_bf16<4, 1>), grid, dim3(256), 0, s, x, offsets, assignment_rows, w13,
                                act, hidden, ffn, experts);
             break;
         case 2:
@@ -443,7 +444,7 @@ hipError_t launch_ffn_up_bf16(const bf16_t* x, const uint32_t* offsets,
                                act, hidden, ffn, experts);
             break;
         default:
-            hipLaunchKernelGGL((k_ffn_up_bf16<4, 1>), grid, dim3(256), 0, s, x, offsets, assignment_rows, w13,
+            hipLaunchKernelGGL((k_ffn_up_bf16<2, 2>), grid, dim3(256), 0, s, x, offsets, assignment_rows, w13,
                                act, hidden, ffn, experts);
     }
     return hipGetLastError();
@@ -458,7 +459,7 @@ hipError_t launch_ffn_down_bf16(const bf16_t* act, const uint32_t* offsets, cons
     const dim3 grid(static_cast<unsigned>(ceil_div(tiles, kXcds) * kXcds));
     switch (ffn_variant()) {
         case 1:
-            hipLaunchKernelGGL((k_ffn_down_bf16<2, 2>), grid, dim3(256), 0, s, act, offsets, w2, y, hidden, ffn,
+            hipLaunchKernelGGL((k_ffn_down_bf16<4, 1>), grid, dim3(256), 0, s, act, offsets, w2, y, hidden, ffn,
                                experts);
             break;
         case 2:
@@ -466,7 +467,7 @@ hipError_t launch_ffn_down_bf16(const bf16_t* act, const uint32_t* offsets, cons
                                experts);
             break;
         default:
-            hipLaunchKernelGGL((k_ffn_down_bf16<4, 1>), grid, dim3(256), 0, s, act, offsets, w2, y, hidden, ffn,
+            hipLaunchKernelGGL((k_ffn_down_bf16<2, 2>), grid, dim3(256), 0, s, act, offsets, w2, y, hidden, ffn,
                                experts);
     }
     return hipGetLastError();
