@@ -16,11 +16,6 @@ constexpr int kWave = 64;           // CDNA wavefront width
 constexpr int kTileTokens = 64;     // routing tile: one wave of tokens
 constexpr int kMaxExperts = 64;     // routes are u8 and lane-indexed
 
-// Grouped-GEMM row tile shared by the planner and the kernels.
-constexpr int kUpBM = 128;          // w1||w3 kernel rows per tile
-constexpr int kUpBN = 64;           // w1||w3 kernel intermediate cols per tile
-constexpr int kDownBM = 128;        // w2 kernel rows per tile
-constexpr int kDownBN = 128;        // w2 kernel hidden cols per tile
 constexpr int kF32BM = 64;          // fp32 chain kernels rows per tile
 constexpr int kF32BN = 64;          // fp32 chain kernels cols per tile
 
