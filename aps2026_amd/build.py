@@ -1,4 +1,8 @@
-"""Builds libaps_moe.so (all HIP sources under csrc/, gfx950) in-tree.
+"""Builds, in-tree:
+  libaps_moe.so     all HIP sources under csrc/ (gfx950): the C ABI;
+  libaps_layers.so  the C++ host API (cpp/*.cpp: Tensor, tensor_ops,
+                    PhiMLP, PhiMoE) over libaps_moe.so;
+  tests/cpp/layer_check  the GPU check program of the C++ API.
 
     python -m aps2026_amd.build
 
@@ -36,17 +40,43 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def build(verbose: bool = False) -> str:
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-o", tmp, *sources()]
+LAYERS_LIB = os.path.join(HERE, "libaps_layers.so")
+REPO = os.path.dirname(HERE)
+CHECK_SRC = os.path.join(REPO, "tests", "cpp", "layer_check.cpp")
+CHECK_BIN = os.path.join(REPO, "tests", "cpp", "layer_check")
+
+# host-only C++ (HIP runtime API, no device code): the system C++ compiler
+CXX = os.environ.get("CXX", "g++")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include")]
+HIP_LINK = ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath," + os.path.join(ROCM, "lib")]
+
+
+def _run(cmd, verbose):
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l and "(ignoring feature)" not in l)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{err}")
+        raise RuntimeError(f"{os.path.basename(cmd[0])} failed ({res.returncode}):\n{' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> str:
+    tmp = LIB + ".tmp"
+    _run([HIPCC, *FLAGS, "-o", tmp, *sources()], verbose)
     os.replace(tmp, LIB)
+    # C++ host API over the C ABI
+    tmp = LAYERS_LIB + ".tmp"
+    cpp = sorted(glob.glob(os.path.join(HERE, "cpp", "*.cpp")))
+    _run([CXX, *HOST_FLAGS, "-shared", "-o", tmp, *cpp, "-L" + HERE, "-laps_moe",
+          "-Wl,-rpath,$ORIGIN", *HIP_LINK], verbose)
+    os.replace(tmp, LAYERS_LIB)
+    if os.path.exists(CHECK_SRC):
+        tmp = CHECK_BIN + ".tmp"
+        _run([CXX, *HOST_FLAGS, "-o", tmp, CHECK_SRC, "-L" + HERE, "-laps_layers", "-laps_moe",
+              "-Wl,-rpath,$ORIGIN/../../aps2026_amd", *HIP_LINK], verbose)
+        os.replace(tmp, CHECK_BIN)
     return LIB
 
 

@@ -1,0 +1,51 @@
+// PhiMLP / PhiMoE over the C ABI (declared in include/layer.h).
+//
+// Reference: PhiMLP::forward (src/layer.cu:49-67), PhiMoE::PhiMoE
+// (src/layer.cu:94-111) and PhiMoE::forward (src/layer.cu:113-121, the GPU
+// branch: router GEMM, then moe_forward_grouped_gpu).
+#include "../../include/layer.h"
+
+#include <stdexcept>
+#include <utility>
+
+namespace aps_cpp_detail {
+void mlp_forward_gpu(std::size_t handle, const Tensor& x, std::size_t rows, Tensor& out);
+std::size_t register_dense(const Tensor& w1, const Tensor& w2, const Tensor& w3);
+}  // namespace aps_cpp_detail
+
+PhiMLP::PhiMLP(Tensor w1, Tensor w2, Tensor w3) : w1_(std::move(w1)), w2_(std::move(w2)), w3_(std::move(w3)) {
+    if (w1_.ndim() != 2 || w3_.shape() != w1_.shape() || w2_.ndim() != 2 || w2_.size(0) != w1_.size(1) ||
+        w2_.size(1) != w1_.size(0))
+        throw std::invalid_argument("PhiMLP weight shapes");
+}
+
+void PhiMLP::forward(const Tensor& x, Tensor& y, bool use_gpu) const {
+    if (!use_gpu) throw std::invalid_argument("PhiMLP::forward: the CPU path (use_gpu = false) is not provided");
+    const std::size_t h = x.size(x.ndim() - 1);
+    if (h != w1_.size(1)) throw std::invalid_argument("PhiMLP::forward shape");
+    const std::size_t rows = x.size() / h;
+    if (!dense_handle_) dense_handle_ = aps_cpp_detail::register_dense(w1_, w2_, w3_);
+    Tensor out({rows, w2_.size(0)});
+    if (rows) aps_cpp_detail::mlp_forward_gpu(dense_handle_, x, rows, out);
+    out.reshape(x.shape());
+    y = std::move(out);
+}
+
+PhiMoE::PhiMoE(Tensor gate, std::vector<PhiMLP> experts, aps_dtype compute)
+    : gate_(std::move(gate)), experts_(std::move(experts)) {
+    std::vector<const Tensor*> w1, w2, w3;
+    for (const PhiMLP& e : experts_) {
+        w1.push_back(&e.w1());
+        w2.push_back(&e.w2());
+        w3.push_back(&e.w3());
+    }
+    gpu_weights_handle_ = tensor_ops::register_moe_weights_gpu(w1, w2, w3, compute);
+}
+
+void PhiMoE::forward(const Tensor& x, Tensor& y, bool use_gpu) const {
+    if (!use_gpu) throw std::invalid_argument("PhiMoE::forward: the CPU path (use_gpu = false) is not provided");
+    const std::size_t rows = x.size(0);
+    Tensor router({rows, apss26::NUM_EXPERTS});
+    if (rows) tensor_ops::matmul_transposed_gpu(x, gate_, router);
+    tensor_ops::moe_forward_grouped_gpu(x, router, gpu_weights_handle_, y);
+}

@@ -1,0 +1,321 @@
+// Tensor and tensor_ops over the C ABI (declared in include/tensor.h).
+//
+// Reference behaviour mirrored: Tensor storage and lazy host/device
+// synchronisation (src/tensor.cu:20-273), register_moe_weights_gpu
+// (src/tensor.cu:2757-2788), moe_forward_grouped_gpu (src/tensor.cu:2790-2928)
+// and the error conventions of check_cuda (src/tensor.cu:370-374).
+#include "../../include/tensor.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/config.h"
+
+namespace {
+
+void hip_check(hipError_t err, const char* what) {
+    if (err != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(err));
+}
+
+// A non-zero status from the C ABI: argument errors become
+// std::invalid_argument, device errors std::runtime_error, each carrying the
+// library's message.
+[[noreturn]] void throw_status(int rc, const char* op) {
+    const std::string msg = std::string(op) + ": " + aps_moe_last_error();
+    if (rc == APS_ERR_HIP) throw std::runtime_error(msg);
+    throw std::invalid_argument(msg);
+}
+
+// Grow-only device workspace for the forward calls, ordered on the default
+// stream like the reference's moe_scratch (src/tensor.cu:1227-1291).
+struct Workspace {
+    std::mutex mu;
+    void* ptr = nullptr;
+    std::size_t bytes = 0;
+    void* get(std::size_t need) {
+        if (need <= bytes) return ptr;
+        if (ptr) hip_check(hipFreeAsync(ptr, nullptr), "hipFreeAsync workspace");
+        ptr = nullptr;
+        bytes = 0;
+        hip_check(hipMallocAsync(&ptr, need, nullptr), "hipMallocAsync workspace");
+        bytes = need;
+        return ptr;
+    }
+};
+
+Workspace& workspace() {
+    static Workspace* w = new Workspace();  // lives for the process, like the reference's scratch
+    return *w;
+}
+
+}  // namespace
+
+// ---- Tensor ----------------------------------------------------------------
+
+Tensor::Tensor(std::vector<std::size_t> shape) : shape_(std::move(shape)) {
+    numel_ = 1;
+    for (std::size_t d : shape_) numel_ *= d;
+}
+
+Tensor::~Tensor() { drop_dev(); }
+
+Tensor::Tensor(const Tensor& other) : shape_(other.shape_), numel_(other.numel_) {
+    other.ensure_host();
+    host_ = other.host_;
+}
+
+Tensor& Tensor::operator=(const Tensor& other) {
+    if (this == &other) return *this;
+    other.ensure_host();
+    drop_dev();
+    shape_ = other.shape_;
+    numel_ = other.numel_;
+    host_ = other.host_;
+    host_valid_ = true;
+    dev_valid_ = false;
+    return *this;
+}
+
+Tensor::Tensor(Tensor&& other) noexcept
+    : shape_(std::move(other.shape_)),
+      numel_(other.numel_),
+      host_(std::move(other.host_)),
+      dev_(other.dev_),
+      host_valid_(other.host_valid_),
+      dev_valid_(other.dev_valid_) {
+    other.dev_ = nullptr;
+    other.numel_ = 0;
+    other.host_valid_ = true;
+    other.dev_valid_ = false;
+}
+
+Tensor& Tensor::operator=(Tensor&& other) noexcept {
+    if (this == &other) return *this;
+    drop_dev();
+    shape_ = std::move(other.shape_);
+    numel_ = other.numel_;
+    host_ = std::move(other.host_);
+    dev_ = other.dev_;
+    host_valid_ = other.host_valid_;
+    dev_valid_ = other.dev_valid_;
+    other.dev_ = nullptr;
+    other.numel_ = 0;
+    other.host_valid_ = true;
+    other.dev_valid_ = false;
+    return *this;
+}
+
+std::size_t Tensor::size(std::size_t dim) const {
+    if (dim >= shape_.size()) throw std::out_of_range("Tensor dimension");
+    return shape_[dim];
+}
+
+void Tensor::drop_dev() {
+    if (dev_) (void)hipFreeAsync(dev_, nullptr);
+    dev_ = nullptr;
+    dev_valid_ = false;
+}
+
+void Tensor::ensure_dev_alloc() const {
+    if (!dev_ && numel_) hip_check(hipMallocAsync(reinterpret_cast<void**>(&dev_), numel_ * sizeof(float), nullptr),
+                                   "hipMallocAsync tensor");
+}
+
+void Tensor::ensure_host() const {
+    if (host_.size() != numel_) host_.assign(numel_, 0.0f);
+    if (host_valid_) return;
+    if (!dev_ || !dev_valid_) throw std::runtime_error("tensor has no valid storage");
+    hip_check(hipMemcpy(host_.data(), dev_, numel_ * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy tensor D2H");
+    host_valid_ = true;
+}
+
+void Tensor::prepare_cuda() const {
+    if (numel_ == 0) return;
+    ensure_dev_alloc();
+    if (!dev_valid_) {
+        ensure_host();
+        hip_check(hipMemcpy(dev_, host_.data(), numel_ * sizeof(float), hipMemcpyHostToDevice),
+                  "hipMemcpy tensor H2D");
+        dev_valid_ = true;
+    }
+}
+
+const float* Tensor::cuda_data() const {
+    prepare_cuda();
+    return dev_;
+}
+
+float* Tensor::cuda_data_write() {
+    ensure_dev_alloc();
+    dev_valid_ = true;
+    host_valid_ = false;
+    return dev_;
+}
+
+void Tensor::sync_cuda_to_host() const { ensure_host(); }
+
+float* Tensor::data() {
+    ensure_host();
+    dev_valid_ = false;
+    return host_.data();
+}
+
+const float* Tensor::data() const {
+    ensure_host();
+    return host_.data();
+}
+
+float& Tensor::operator[](std::size_t i) { return data()[i]; }
+const float& Tensor::operator[](std::size_t i) const { return data()[i]; }
+
+std::size_t Tensor::index(std::initializer_list<std::size_t> idx) const {
+    if (idx.size() != shape_.size()) throw std::out_of_range("Tensor index");
+    std::size_t flat = 0;
+    std::size_t d = 0;
+    for (std::size_t v : idx) {
+        if (v >= shape_[d]) throw std::out_of_range("Tensor index");
+        flat = flat * shape_[d] + v;
+        ++d;
+    }
+    return flat;
+}
+
+float& Tensor::at(std::size_t i) { return data()[index({i})]; }
+float& Tensor::at(std::size_t i, std::size_t j) { return data()[index({i, j})]; }
+float& Tensor::at(std::size_t i, std::size_t j, std::size_t k) { return data()[index({i, j, k})]; }
+float& Tensor::at(std::size_t i, std::size_t j, std::size_t k, std::size_t l) { return data()[index({i, j, k, l})]; }
+const float& Tensor::at(std::size_t i) const { return data()[index({i})]; }
+const float& Tensor::at(std::size_t i, std::size_t j) const { return data()[index({i, j})]; }
+const float& Tensor::at(std::size_t i, std::size_t j, std::size_t k) const { return data()[index({i, j, k})]; }
+const float& Tensor::at(std::size_t i, std::size_t j, std::size_t k, std::size_t l) const {
+    return data()[index({i, j, k, l})];
+}
+
+void Tensor::reshape(std::vector<std::size_t> shape) {
+    std::size_t n = 1;
+    for (std::size_t d : shape) n *= d;
+    if (n != numel_) throw std::invalid_argument("reshape changes tensor size");
+    shape_ = std::move(shape);
+}
+
+void Tensor::fill(float value) {
+    host_.assign(numel_, value);
+    host_valid_ = true;
+    dev_valid_ = false;
+}
+
+// ---- tensor_ops ------------------------------------------------------------
+
+namespace tensor_ops {
+
+void matmul_transposed_gpu(const Tensor& a, const Tensor& b, Tensor& c) {
+    const std::size_t k = a.size(a.ndim() - 1);
+    const std::size_t m = a.size() / k;
+    const std::size_t n = b.size(0);
+    if (b.size(1) != k || c.size(0) != m || c.size(1) != n)
+        throw std::invalid_argument("matmul_transposed_gpu shape");
+    if (n > 64 || k % 256 != 0)
+        throw std::invalid_argument("matmul_transposed_gpu: this build covers the router shape (n <= 64, k % 256 == 0)");
+    const float* da = a.cuda_data();
+    const float* db = b.cuda_data();
+    float* dc = c.cuda_data_write();
+    const int rc = aps_router_logits(da, APS_DTYPE_F32, db, static_cast<int64_t>(m), static_cast<int32_t>(k),
+                                     static_cast<int32_t>(n), dc, nullptr);
+    if (rc) throw_status(rc, "matmul_transposed_gpu");
+}
+
+std::size_t register_moe_weights_gpu(const std::vector<const Tensor*>& w1, const std::vector<const Tensor*>& w2,
+                                     const std::vector<const Tensor*>& w3, aps_dtype compute) {
+    if (w1.size() != apss26::NUM_EXPERTS || w2.size() != apss26::NUM_EXPERTS || w3.size() != apss26::NUM_EXPERTS)
+        throw std::invalid_argument("MoE weight table size");
+    const std::size_t E = w1.size();
+    const std::size_t F = w1[0]->size(0), H = w1[0]->size(1);
+    std::vector<const void*> p1(E), p2(E), p3(E);
+    for (std::size_t e = 0; e < E; ++e) {
+        if (w1[e]->size(0) != F || w1[e]->size(1) != H || w3[e]->size(0) != F || w3[e]->size(1) != H ||
+            w2[e]->size(0) != H || w2[e]->size(1) != F)
+            throw std::invalid_argument("MoE weight table size");
+        p1[e] = w1[e]->cuda_data();
+        p2[e] = w2[e]->cuda_data();
+        p3[e] = w3[e]->cuda_data();
+    }
+    aps_moe_weights_desc d{};
+    d.num_experts = static_cast<int32_t>(E);
+    d.hidden = static_cast<int32_t>(H);
+    d.ffn = static_cast<int32_t>(F);
+    d.src_dtype = APS_DTYPE_F32;
+    d.compute_dtype = compute;
+    d.w1 = p1.data();
+    d.w3 = p3.data();
+    d.w2 = p2.data();
+    uint64_t handle = 0;
+    const int rc = aps_moe_weights_register(&d, nullptr, &handle);
+    if (rc) throw_status(rc, "register_moe_weights_gpu");
+    return static_cast<std::size_t>(handle);
+}
+
+std::size_t register_moe_weights_gpu(const std::vector<const Tensor*>& w1, const std::vector<const Tensor*>& w2,
+                                     const std::vector<const Tensor*>& w3) {
+    return register_moe_weights_gpu(w1, w2, w3, APS_DTYPE_F32);
+}
+
+void moe_forward_grouped_gpu(const Tensor& x, const Tensor& router, std::size_t weights_handle, Tensor& out) {
+    const std::size_t rows = x.size(0), h = x.size(1);
+    aps_moe_ws_layout L{};
+    if (router.ndim() != 2 || router.size(0) != rows || router.size(1) != apss26::NUM_EXPERTS ||
+        weights_handle == 0 || aps_moe_workspace_layout(weights_handle, static_cast<int64_t>(rows), &L) != APS_OK)
+        throw std::invalid_argument("grouped MoE shape or handle");
+    out = Tensor({rows, h});
+    if (rows == 0) return;
+    const float* dx = x.cuda_data();
+    const float* dr = router.cuda_data();
+    float* dout = out.cuda_data_write();
+    Workspace& ws = workspace();
+    std::lock_guard<std::mutex> lk(ws.mu);
+    void* buf = ws.get(L.total_bytes);
+    const int rc = aps_moe_forward_grouped(weights_handle, dx, APS_DTYPE_F32, dr, static_cast<int64_t>(rows), dout,
+                                           APS_DTYPE_F32, buf, L.total_bytes, nullptr);
+    if (rc) throw_status(rc, "moe_forward_grouped_gpu");
+}
+
+}  // namespace tensor_ops
+
+// ---- dense FFN (used by PhiMLP) ---------------------------------------------
+
+namespace aps_cpp_detail {
+
+void mlp_forward_gpu(std::size_t handle, const Tensor& x, std::size_t rows, Tensor& out) {
+    const std::size_t need = aps_mlp_workspace_size(handle, static_cast<int64_t>(rows));
+    const float* dx = x.cuda_data();
+    float* dout = out.cuda_data_write();
+    Workspace& ws = workspace();
+    std::lock_guard<std::mutex> lk(ws.mu);
+    void* buf = ws.get(need ? need : 1);
+    const int rc = aps_mlp_forward(handle, dx, APS_DTYPE_F32, static_cast<int64_t>(rows), dout, buf, need, nullptr);
+    if (rc) throw_status(rc, "PhiMLP::forward");
+}
+
+std::size_t register_dense(const Tensor& w1, const Tensor& w2, const Tensor& w3) {
+    const void* p1 = w1.cuda_data();
+    const void* p2 = w2.cuda_data();
+    const void* p3 = w3.cuda_data();
+    aps_moe_weights_desc d{};
+    d.num_experts = 1;
+    d.hidden = static_cast<int32_t>(w1.size(1));
+    d.ffn = static_cast<int32_t>(w1.size(0));
+    d.src_dtype = APS_DTYPE_F32;
+    d.compute_dtype = APS_DTYPE_F32;
+    d.w1 = &p1;
+    d.w3 = &p3;
+    d.w2 = &p2;
+    uint64_t handle = 0;
+    const int rc = aps_moe_weights_register(&d, nullptr, &handle);
+    if (rc) throw_status(rc, "PhiMLP weights");
+    return static_cast<std::size_t>(handle);
+}
+
+}  // namespace aps_cpp_detail

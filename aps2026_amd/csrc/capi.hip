@@ -100,7 +100,8 @@ void make_layout(const WeightSet& w, int64_t rows, aps_moe_ws_layout* L) {
     L->act = take(2 * T * static_cast<size_t>(w.F) * elt);
     L->act_scale = 0;
     L->y = take(2 * T * static_cast<size_t>(w.H) * elt);
-    L->xq = 0;
+    // bf16 copy of x for the fused entry points when x arrives as fp32
+    L->xq = w.compute == APS_DTYPE_BF16 ? take(T * static_cast<size_t>(w.H) * 2) : 0;
     L->xq_scale = 0;
     L->total_bytes = off;
 }
@@ -154,7 +155,7 @@ int check_x_dtype(const WeightSet& w, int32_t x_dtype) {
     return APS_OK;
 }
 
-int grouped_from_logits(const WeightSet& w, const void* x, const float* logits, int64_t rows,
+int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const float* logits, int64_t rows,
                         void* out, int32_t out_dtype, char* ws, const aps_moe_ws_layout& L,
                         hipStream_t s) {
     auto* routes = reinterpret_cast<uint8_t*>(ws + L.routes);
@@ -163,6 +164,11 @@ int grouped_from_logits(const WeightSet& w, const void* x, const float* logits, 
     auto* offsets = reinterpret_cast<uint32_t*>(ws + L.offsets);
     auto* arows = reinterpret_cast<uint32_t*>(ws + L.assignment_rows);
     auto* rpos = reinterpret_cast<uint32_t*>(ws + L.route_positions);
+    if (x_is_f32 && w.compute == APS_DTYPE_BF16) {
+        auto* xb = reinterpret_cast<aps::bf16_t*>(ws + L.xq);
+        APS_HIP(aps::launch_to_bf16(static_cast<const float*>(x), xb, rows * w.H, s), "x to bf16 launch");
+        x = xb;
+    }
     APS_HIP(aps::launch_route_top2(logits, rows, w.E, routes, tiles, s), "route_top2 launch");
     APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, w.E, counts, offsets, arows, rpos, s),
             "dispatch launch");
@@ -184,9 +190,10 @@ int aps_moe_abi_version(void) { return APS_MOE_ABI_VERSION; }
 int aps_moe_weights_register(const aps_moe_weights_desc* d, void* stream, uint64_t* handle_out) {
     if (!d || !handle_out) return fail(APS_ERR_ARG, "register: NULL descriptor or handle pointer");
     *handle_out = 0;
-    // reference: "MoE weight table size" (src/tensor.cu:2761-2764)
-    if (d->num_experts < 2 || d->num_experts > aps::kMaxExperts)
-        return fail(APS_ERR_SHAPE, "MoE weight table size: %d experts (2..%d supported)",
+    // reference: "MoE weight table size" (src/tensor.cu:2761-2764).  One
+    // expert is a dense FFN (aps_mlp_forward); routing needs two or more.
+    if (d->num_experts < 1 || d->num_experts > aps::kMaxExperts)
+        return fail(APS_ERR_SHAPE, "MoE weight table size: %d experts (1..%d supported)",
                     d->num_experts, aps::kMaxExperts);
     if (d->hidden <= 0 || d->ffn <= 0 || d->hidden % 256 != 0 || d->ffn % 64 != 0)
         return fail(APS_ERR_SHAPE, "hidden %d must be a multiple of 256 and ffn %d of 64",
@@ -375,7 +382,14 @@ static int forward_common(uint64_t handle, const void* x, int32_t x_dtype, int64
     if (int rc = check_device(*w)) return rc;
     if (rows < 0 || rows > (int64_t(1) << 30))
         return fail(APS_ERR_SHAPE, "grouped MoE shape or handle: rows %lld", (long long)rows);
-    if (int rc = check_x_dtype(*w, x_dtype)) return rc;
+    if (w->E < 2) return fail(APS_ERR_SHAPE, "grouped MoE shape or handle: top-2 routing needs 2+ experts");
+    // fp32 x is accepted with bf16 weights: the router reads it exactly and
+    // the FFN gets a bf16 copy in the workspace.
+    const bool f32_into_bf16 = w->compute == APS_DTYPE_BF16 && x_dtype == APS_DTYPE_F32;
+    if (!f32_into_bf16)
+        if (int rc = check_x_dtype(*w, x_dtype)) return rc;
+    if (f32_into_bf16 && rows > 0 && (reinterpret_cast<uintptr_t>(x) & 15u))
+        return fail(APS_ERR_ARG, "forward: fp32 x must be 16-byte aligned");
     if (out_dtype != APS_DTYPE_F32 && out_dtype != APS_DTYPE_BF16)
         return fail(APS_ERR_DTYPE, "out dtype %d not supported", out_dtype);
     make_layout(*w, rows, L);
@@ -397,8 +411,8 @@ int aps_moe_forward_grouped(uint64_t handle, const void* x, int32_t x_dtype,
         return rc;
     if (rows == 0) return APS_OK;
     if (!router_logits) return fail(APS_ERR_ARG, "forward_grouped: NULL router logits");
-    return grouped_from_logits(*w, x, router_logits, rows, out, out_dtype, static_cast<char*>(workspace),
-                               L, static_cast<hipStream_t>(stream));
+    return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, router_logits, rows, out, out_dtype,
+                               static_cast<char*>(workspace), L, static_cast<hipStream_t>(stream));
 }
 
 int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float* gate, int64_t rows,
@@ -412,9 +426,50 @@ int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float
     char* ws = static_cast<char*>(workspace);
     hipStream_t s = static_cast<hipStream_t>(stream);
     float* logits = reinterpret_cast<float*>(ws + L.logits);
-    APS_HIP(aps::launch_router_logits(x, w->compute != APS_DTYPE_F32, gate, rows, w->H, w->E, logits, s),
+    APS_HIP(aps::launch_router_logits(x, x_dtype == APS_DTYPE_BF16, gate, rows, w->H, w->E, logits, s),
             "router_logits launch");
-    return grouped_from_logits(*w, x, logits, rows, out, out_dtype, ws, L, s);
+    return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, logits, rows, out, out_dtype, ws, L, s);
+}
+
+// Dense FFN of a single-expert weight set: offsets {0, rows} and the
+// identity assignment in the workspace, then the two grouped GEMMs with
+// y_perm = out (position p is row p).
+static size_t mlp_layout(const WeightSet& w, int64_t rows, size_t* arows, size_t* act) {
+    size_t off = align_up(2 * sizeof(uint32_t));
+    *arows = off;
+    off = align_up(off + static_cast<size_t>(rows) * 4);
+    *act = off;
+    const size_t elt = w.compute == APS_DTYPE_F32 ? 4 : 2;
+    return align_up(off + static_cast<size_t>(rows) * w.F * elt);
+}
+
+size_t aps_mlp_workspace_size(uint64_t handle, int64_t rows) {
+    const WeightSet* w = lookup(handle);
+    if (!w || rows < 0) return 0;
+    size_t a, b;
+    return mlp_layout(*w, rows, &a, &b);
+}
+
+int aps_mlp_forward(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows, void* out,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+    const WeightSet* w = lookup(handle);
+    if (!w) return fail(APS_ERR_HANDLE, "mlp: invalid handle %llu", (unsigned long long)handle);
+    if (int rc = check_device(*w)) return rc;
+    if (w->E != 1) return fail(APS_ERR_SHAPE, "mlp: weight set has %d experts, a dense FFN has 1", w->E);
+    if (rows < 0 || rows > (int64_t(1) << 30)) return fail(APS_ERR_SHAPE, "mlp: rows %lld", (long long)rows);
+    if (int rc = check_x_dtype(*w, x_dtype)) return rc;
+    if (rows == 0) return APS_OK;
+    size_t arows_off, act_off;
+    const size_t need = mlp_layout(*w, rows, &arows_off, &act_off);
+    if (!x || !out) return fail(APS_ERR_ARG, "mlp: NULL x or out");
+    if (!workspace || workspace_bytes < need)
+        return fail(APS_ERR_WORKSPACE, "mlp: workspace %zu bytes, need %zu", workspace_bytes, need);
+    char* ws = static_cast<char*>(workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto* offsets = reinterpret_cast<uint32_t*>(ws);
+    auto* arows = reinterpret_cast<uint32_t*>(ws + arows_off);
+    APS_HIP(aps::launch_dense_plan(offsets, arows, rows, s), "dense plan launch");
+    return run_ffn(*w, x, rows, offsets, arows, ws + act_off, out, s);
 }
 
 }  // extern "C"

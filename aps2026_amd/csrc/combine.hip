@@ -109,7 +109,32 @@ __global__ void k_pack_tiles(const void* __restrict__ src_lo, const void* __rest
     dst[i] = static_cast<bf16_t>(v);
 }
 
+// dst[i] = bf16(src[i]), round to nearest even; 8 elements per thread.
+__global__ void __launch_bounds__(256)
+k_to_bf16(const float* __restrict__ src, bf16_t* __restrict__ dst, int64_t n) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+    if (i + 8 <= n) {
+        const float4 a = *reinterpret_cast<const float4*>(src + i);
+        const float4 b = *reinterpret_cast<const float4*>(src + i + 4);
+        uint4 q;
+        q.x = pack2_bf16(a.x, a.y);
+        q.y = pack2_bf16(a.z, a.w);
+        q.z = pack2_bf16(b.x, b.y);
+        q.w = pack2_bf16(b.z, b.w);
+        *reinterpret_cast<uint4*>(dst + i) = q;
+    } else {
+        for (int64_t j = i; j < n; ++j) dst[j] = static_cast<bf16_t>(f32_to_bf16_bits(src[j]));
+    }
+}
+
 }  // namespace
+
+hipError_t launch_to_bf16(const float* src, bf16_t* dst, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_to_bf16, dim3(static_cast<unsigned>(ceil_div(ceil_div(n, 8), 256))), dim3(256), 0, s,
+                       src, dst, n);
+    return hipGetLastError();
+}
 
 hipError_t launch_combine(const void* y, bool y_bf16, const uint32_t* route_positions,
                           int64_t rows, int hidden, void* out, bool out_bf16, hipStream_t s) {

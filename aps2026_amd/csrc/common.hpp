@@ -101,6 +101,12 @@ hipError_t launch_ffn_down_f32(const float* act, const uint32_t* offsets, const 
                                float* y, int64_t rows, int hidden, int ffn, int experts,
                                hipStream_t s);
 
+// Dense (single-expert) plan: offsets = {0, rows}, assignment_rows[i] = i.
+hipError_t launch_dense_plan(uint32_t* offsets, uint32_t* assignment_rows, int64_t rows, hipStream_t s);
+
+// dst = bf16(src) element-wise, round to nearest even.
+hipError_t launch_to_bf16(const float* src, bf16_t* dst, int64_t n, hipStream_t s);
+
 hipError_t launch_combine(const void* y, bool y_bf16, const uint32_t* route_positions,
                           int64_t rows, int hidden, void* out, bool out_bf16, hipStream_t s);
 

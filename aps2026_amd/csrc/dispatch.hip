@@ -113,7 +113,25 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
     }
 }
 
+// Routing plan of a dense (single-expert) FFN: every row is position p = row
+// of expert 0.
+__global__ void k_dense_plan(uint32_t* __restrict__ offsets, uint32_t* __restrict__ rows_out, int64_t rows) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < rows) rows_out[i] = static_cast<uint32_t>(i);
+    if (i == 0) {
+        offsets[0] = 0u;
+        offsets[1] = static_cast<uint32_t>(rows);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_dense_plan(uint32_t* offsets, uint32_t* assignment_rows, int64_t rows, hipStream_t s) {
+    const int64_t n = rows > 0 ? rows : 1;
+    hipLaunchKernelGGL(k_dense_plan, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s, offsets,
+                       assignment_rows, rows);
+    return hipGetLastError();
+}
 
 hipError_t launch_tile_hist(const uint8_t* routes, int64_t rows, int experts,
                             uint32_t* tile_counts, hipStream_t s) {

@@ -297,9 +297,10 @@ __device__ inline bool locate_block(const uint32_t* __restrict__ offsets, int E,
     u.expert = e;
     u.end = __shfl(hi, e);
     const uint32_t e_lo = __shfl(lo, e);
-    if (r < pairs * nw) {
-        u.m0 = e_lo + static_cast<uint32_t>(2 * g + r / pairs) * 128u;
-        u.nb0 = 2 * (r % pairs);
+    if (!ALL_TALL && r < pairs * nw) {
+        const int pp = ALL_TALL ? 1 : pairs;     // pairs > 0 on this branch
+        u.m0 = e_lo + static_cast<uint32_t>(2 * g + r / pp) * 128u;
+        u.nb0 = 2 * (r % pp);
         u.tall = false;
     } else {
         u.m0 = e_lo + static_cast<uint32_t>(g) * 256u;

@@ -94,7 +94,9 @@ typedef struct aps_moe_ws_layout {
     size_t act;             /* [2*rows][ffn], compute dtype (f32 or bf16) */
     size_t act_scale;       /* f32 [2*rows] (fp8 path only)         */
     size_t y;               /* [2*rows][hidden], f32 (F32 path) or bf16 */
-    size_t xq;              /* fp8 path: e4m3 x [rows][hidden]      */
+    size_t xq;              /* x in the compute dtype when the caller
+                               passes another one: bf16 [rows][hidden]
+                               (bf16 weights, fp32 x), e4m3 (fp8 path) */
     size_t xq_scale;        /* fp8 path: f32 [rows]                 */
 } aps_moe_ws_layout;
 
@@ -102,7 +104,9 @@ typedef struct aps_moe_ws_layout {
 
 /* Replaces tensor_ops::register_moe_weights_gpu (reference
  * include/tensor.h:142-145, src/tensor.cu:2757-2788).  Writes a 1-based
- * handle (0 is never a valid handle, as in the reference).  Synchronous. */
+ * handle (0 is never a valid handle, as in the reference).  Synchronous.
+ * num_experts 1..64; a one-expert set is a dense FFN for aps_mlp_forward
+ * (the reference's PhiMLP weights), routing needs two or more. */
 APS_API int aps_moe_weights_register(const aps_moe_weights_desc* desc, void* stream,
                              uint64_t* handle_out);
 
@@ -181,17 +185,36 @@ APS_API int aps_moe_combine(const void* y_perm, int32_t y_dtype, const uint32_t*
 
 /* Replaces tensor_ops::moe_forward_grouped_gpu (reference
  * include/tensor.h:146-147, src/tensor.cu:2790-2928): routing from
- * precomputed logits [rows][E], then dispatch, expert FFN and combine. */
+ * precomputed logits [rows][E], then dispatch, expert FFN and combine.
+ * x_dtype is the weight set's (F32 / BF16), or F32 with a BF16 weight set
+ * (x 16-byte aligned): the FFN then reads a bf16 copy made in the
+ * workspace (layout field xq). */
 APS_API int aps_moe_forward_grouped(uint64_t handle, const void* x, int32_t x_dtype,
                             const float* router_logits, int64_t rows,
                             void* out, int32_t out_dtype,
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* Replaces the body of PhiMoE::forward (reference src/layer.cu:113-121):
- * router GEMM (gate [E][H] fp32) + the grouped path above, in one call. */
+ * router GEMM (gate [E][H] fp32) + the grouped path above, in one call.
+ * The router always reads x in the dtype given (an fp32 x is exact). */
 APS_API int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float* gate,
                     int64_t rows, void* out, int32_t out_dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- dense FFN --------------------------------------------------------- */
+
+/* Workspace bytes of aps_mlp_forward for `rows` rows (0 for a bad handle). */
+APS_API size_t aps_mlp_workspace_size(uint64_t handle, int64_t rows);
+
+/* Replaces the GPU branch of PhiMLP::forward (reference src/layer.cu:49-67:
+ * matmul_pair_silu_gpu, src/tensor.cu:3146-3170 / 967-1057, then
+ * matmul_transposed_gpu by w2): out[r] = w2 . (silu(w1 . x[r]) * (w3 . x[r]))
+ * for a one-expert weight set.  The fp32 path keeps the reference's
+ * accumulation order (k ascending FMA chains, SiLU with exp in double), so
+ * it equals the reference bit for bit.  x and out are fp32 for an F32 set,
+ * bf16 for a BF16 set. */
+APS_API int aps_mlp_forward(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows, void* out,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- diagnostics ------------------------------------------------------- */
 

@@ -1,0 +1,18 @@
+// Model constants of the MoE block, under the reference's names
+// (include/config.h:5-27 of the reference: namespace apss26).  Only the
+// constants the MoE feed-forward path reads are kept here.
+#pragma once
+
+#include <cstddef>
+
+namespace apss26 {
+constexpr std::size_t HIDDEN_SIZE = 4096;
+constexpr std::size_t NUM_EXPERTS = 16;
+constexpr std::size_t TOP_K = 2;
+constexpr std::size_t EXPERT_INTERMEDIATE_SIZE = 448;
+// Router scores are canonicalised to this grid before the deterministic
+// top-2 selection; a later expert replaces the current best only if its
+// score is larger by more than ROUTER_TIE_EPS.
+constexpr float ROUTER_SCORE_QUANTUM = 1.0e-3f;
+constexpr float ROUTER_TIE_EPS = 2.0e-2f;
+}  // namespace apss26

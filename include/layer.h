@@ -1,0 +1,47 @@
+// PhiMLP and PhiMoE layers over the C ABI (reference include/layer.h:23-43).
+//
+// The forward signatures are the reference's.  The constructors take the
+// weight tensors directly: the reference's constructors read the same
+// tensors from a ModelLoader by name (src/layer.cu:44-47, 94-111), and the
+// loader is not part of this library.  forward(..., use_gpu = true) runs the
+// HIP path; the reference's CPU branch (use_gpu = false) is not provided and
+// throws std::invalid_argument.
+#pragma once
+
+#include <cstddef>
+#include <vector>
+
+#include "config.h"
+#include "tensor.h"
+
+class PhiMLP {
+public:
+    // w1, w3: [F][H]; w2: [H][F] (nn.Linear layout).
+    PhiMLP(Tensor w1, Tensor w2, Tensor w3);
+    // y = w2 . (silu(w1 . x) * (w3 . x)) row by row; y takes x's shape.  The
+    // GPU path keeps the reference's fp32 arithmetic (src/layer.cu:49-67 with
+    // matmul_pair_silu_gpu), so it matches the reference bit for bit.
+    void forward(const Tensor& x, Tensor& y, bool use_gpu = false) const;
+    const Tensor& w1() const { return w1_; }
+    const Tensor& w2() const { return w2_; }
+    const Tensor& w3() const { return w3_; }
+
+private:
+    Tensor w1_, w2_, w3_;
+    mutable std::size_t dense_handle_ = 0;  // one-expert weight set, registered on first GPU use
+};
+
+class PhiMoE {
+public:
+    // gate: [NUM_EXPERTS][H]; experts: NUM_EXPERTS PhiMLPs.  `compute` picks
+    // the expert FFN kernels: APS_DTYPE_F32 (the reference's arithmetic) or
+    // APS_DTYPE_BF16 (MFMA, fp32 accumulate).  Routing is exact either way.
+    PhiMoE(Tensor gate, std::vector<PhiMLP> experts, aps_dtype compute = APS_DTYPE_F32);
+    // y [rows][H] = sum over the two routed experts of 0.5 * expert(x).
+    void forward(const Tensor& x, Tensor& y, bool use_gpu = false) const;
+
+private:
+    Tensor gate_;
+    std::vector<PhiMLP> experts_;
+    std::size_t gpu_weights_handle_ = 0;
+};

@@ -1,0 +1,106 @@
+// C++ tensor and the MoE tensor ops, over the C ABI of include/aps_moe.h.
+//
+// Mirrors the reference's Tensor (include/tensor.h:8-61) and the tensor_ops
+// entry points the MoE path calls (include/tensor.h:72, 142-147): same
+// names, signatures, argument meaning and exception types/messages, so a
+// caller of the reference compiles against this header unchanged for this
+// path.  Tensors are dense fp32, row-major, with a host copy and a device
+// copy (HIP) that are synchronised lazily, as in the reference:
+//   * cuda_data()        device pointer for reading; uploads a stale copy;
+//   * cuda_data_write()  device pointer for writing; the device copy becomes
+//                        the valid one and the host copy is refreshed on the
+//                        next host access;
+//   * data() / at() / operator[] (non-const) make the host copy the valid one.
+// Device memory is stream-ordered on the legacy default stream, where every
+// op below runs (the reference's ordering: all of its work is on stream 0).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <initializer_list>
+#include <vector>
+
+#include "aps_moe.h"
+
+class Tensor {
+public:
+    Tensor() = default;
+    explicit Tensor(std::vector<std::size_t> shape);
+    ~Tensor();
+    Tensor(const Tensor& other);
+    Tensor& operator=(const Tensor& other);
+    Tensor(Tensor&& other) noexcept;
+    Tensor& operator=(Tensor&& other) noexcept;
+
+    std::size_t ndim() const { return shape_.size(); }
+    std::size_t size() const { return numel_; }
+    std::size_t size(std::size_t dim) const;
+    const std::vector<std::size_t>& shape() const { return shape_; }
+
+    float* data();
+    const float* data() const;
+    float& operator[](std::size_t i);
+    const float& operator[](std::size_t i) const;
+
+    float& at(std::size_t i);
+    float& at(std::size_t i, std::size_t j);
+    float& at(std::size_t i, std::size_t j, std::size_t k);
+    float& at(std::size_t i, std::size_t j, std::size_t k, std::size_t l);
+    const float& at(std::size_t i) const;
+    const float& at(std::size_t i, std::size_t j) const;
+    const float& at(std::size_t i, std::size_t j, std::size_t k) const;
+    const float& at(std::size_t i, std::size_t j, std::size_t k, std::size_t l) const;
+
+    void reshape(std::vector<std::size_t> shape);
+    void fill(float value);
+    void zero() { fill(0.0f); }
+    void prepare_cuda() const;
+    const float* cuda_data() const;
+    float* cuda_data_write();
+    void sync_cuda_to_host() const;
+
+private:
+    std::vector<std::size_t> shape_;
+    std::size_t numel_ = 0;
+    mutable std::vector<float> host_;
+    mutable float* dev_ = nullptr;
+    mutable bool host_valid_ = true;
+    mutable bool dev_valid_ = false;
+
+    std::size_t index(std::initializer_list<std::size_t> idx) const;
+    void ensure_host() const;
+    void ensure_dev_alloc() const;
+    void drop_dev();
+};
+
+namespace tensor_ops {
+
+// c[m][n] = a[m][k] . b[n][k]^T on the GPU.  This build provides the narrow
+// shape the MoE router uses (n <= 64, k a multiple of 256), computed as one
+// fp32 FMA chain per output, k ascending (the reference's
+// k_matmul_transposed_narrow, src/tensor.cu:2943-3006).  Mismatched shapes
+// throw std::invalid_argument("matmul_transposed_gpu shape") as the
+// reference does; other valid shapes throw std::invalid_argument naming the
+// limit.
+void matmul_transposed_gpu(const Tensor& a, const Tensor& b, Tensor& c);
+
+// Registers the 16 experts' w1 / w2 / w3 (nn.Linear layout: w1, w3 [F][H],
+// w2 [H][F]) and returns a 1-based handle.  Throws
+// std::invalid_argument("MoE weight table size") unless each table has
+// apss26::NUM_EXPERTS entries (reference src/tensor.cu:2757-2788).  The
+// default computes in fp32 with the reference's accumulation order; the
+// overload selects bf16 MFMA compute (APS_DTYPE_BF16).
+std::size_t register_moe_weights_gpu(const std::vector<const Tensor*>& w1,
+                                     const std::vector<const Tensor*>& w2,
+                                     const std::vector<const Tensor*>& w3);
+std::size_t register_moe_weights_gpu(const std::vector<const Tensor*>& w1,
+                                     const std::vector<const Tensor*>& w2,
+                                     const std::vector<const Tensor*>& w3, aps_dtype compute);
+
+// out = MoE block of x [rows][H] given router logits [rows][16] and a
+// registered handle (reference src/tensor.cu:2790-2928).  Allocates `out`
+// as [rows][H].  Throws std::invalid_argument("grouped MoE shape or handle")
+// for a router of the wrong shape or an invalid handle.
+void moe_forward_grouped_gpu(const Tensor& x, const Tensor& router, std::size_t weights_handle, Tensor& out);
+
+}  // namespace tensor_ops

@@ -1,0 +1,188 @@
+// GPU check of the C++ host API (include/tensor.h, include/layer.h).
+//
+//   layer_check <out_dir>
+//
+// Builds a small synthetic MoE layer (16 experts, H = 512, F = 128, 96
+// tokens), runs PhiMoE::forward in fp32 and bf16 compute and PhiMLP::forward
+// (expert 0 as a dense FFN) on the GPU, and writes inputs and outputs as
+// raw little-endian fp32 files into <out_dir> for tests/test_gpu_cpp_layer.py
+// to compare with the CPU oracle.  It also checks, in process, the
+// reference's exception types and messages and the Tensor host/device
+// synchronisation rules.  Exit status 0 means every in-process check passed.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/layer.h"
+
+namespace {
+
+int g_failures = 0;
+
+void expect(bool ok, const char* what) {
+    if (!ok) {
+        std::fprintf(stderr, "FAIL: %s\n", what);
+        ++g_failures;
+    }
+}
+
+template <class Ex, class Fn>
+void expect_throw(Fn fn, const char* message, const char* what) {
+    try {
+        fn();
+    } catch (const Ex& e) {
+        if (message && std::string(e.what()) != message) {
+            std::fprintf(stderr, "FAIL: %s: message \"%s\", want \"%s\"\n", what, e.what(), message);
+            ++g_failures;
+        }
+        return;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "FAIL: %s: wrong exception type (%s)\n", what, e.what());
+        ++g_failures;
+        return;
+    }
+    std::fprintf(stderr, "FAIL: %s: no exception\n", what);
+    ++g_failures;
+}
+
+// Deterministic normal samples (xorshift64* + Box-Muller).
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed * 0x9E3779B97F4A7C15ull + 1) {}
+    double uniform() {
+        s ^= s >> 12;
+        s ^= s << 25;
+        s ^= s >> 27;
+        return ((s * 0x2545F4914F6CDD1Dull) >> 11) * (1.0 / 9007199254740992.0);
+    }
+    float normal(float sigma) {
+        const double u1 = uniform() + 1e-300, u2 = uniform();
+        return static_cast<float>(sigma * std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
+    }
+};
+
+Tensor random_tensor(std::vector<std::size_t> shape, Rng& rng, float sigma) {
+    Tensor t(std::move(shape));
+    float* p = t.data();
+    for (std::size_t i = 0; i < t.size(); ++i) p[i] = rng.normal(sigma);
+    return t;
+}
+
+void write_raw(const std::string& dir, const char* name, const Tensor& t) {
+    const std::string path = dir + "/" + name + ".f32";
+    FILE* f = std::fopen(path.c_str(), "wb");
+    if (!f) throw std::runtime_error("cannot write " + path);
+    std::fwrite(t.data(), sizeof(float), t.size(), f);
+    std::fclose(f);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc != 2) {
+        std::fprintf(stderr, "usage: %s <out_dir>\n", argv[0]);
+        return 2;
+    }
+    const std::string dir = argv[1];
+    const std::size_t T = 96, H = 512, F = 128, E = apss26::NUM_EXPERTS;
+    Rng rng(20260);
+
+    Tensor x = random_tensor({T, H}, rng, 1.0f);
+    Tensor gate = random_tensor({E, H}, rng, 0.02f);
+    std::vector<PhiMLP> experts;
+    Tensor w1_all({E, F, H}), w2_all({E, H, F}), w3_all({E, F, H});
+    for (std::size_t e = 0; e < E; ++e) {
+        Tensor w1 = random_tensor({F, H}, rng, 0.02f);
+        Tensor w2 = random_tensor({H, F}, rng, 0.02f);
+        Tensor w3 = random_tensor({F, H}, rng, 0.02f);
+        std::memcpy(w1_all.data() + e * F * H, w1.data(), F * H * sizeof(float));
+        std::memcpy(w2_all.data() + e * H * F, w2.data(), H * F * sizeof(float));
+        std::memcpy(w3_all.data() + e * F * H, w3.data(), F * H * sizeof(float));
+        experts.emplace_back(std::move(w1), std::move(w2), std::move(w3));
+    }
+
+    // --- MoE block, fp32 and bf16 compute -----------------------------------
+    PhiMoE moe32(gate, experts, APS_DTYPE_F32);
+    PhiMoE moe16(gate, experts, APS_DTYPE_BF16);
+    Tensor y32, y16;
+    moe32.forward(x, y32, true);
+    moe16.forward(x, y16, true);
+    expect(y32.ndim() == 2 && y32.size(0) == T && y32.size(1) == H, "PhiMoE output shape");
+    expect(y16.size() == T * H, "PhiMoE bf16 output size");
+
+    // --- dense FFN (expert 0 as PhiMLP) --------------------------------------
+    Tensor x3 = x;
+    x3.reshape({2, T / 2, H});
+    Tensor ymlp;
+    experts[0].forward(x3, ymlp, true);
+    expect(ymlp.shape() == x3.shape(), "PhiMLP keeps the input shape");
+
+    // --- router GEMM on its own ----------------------------------------------
+    Tensor logits({T, E});
+    tensor_ops::matmul_transposed_gpu(x, gate, logits);
+
+    // --- Tensor synchronisation rules ----------------------------------------
+    {
+        Tensor t({4, 8});
+        t.fill(2.0f);
+        const float* d = t.cuda_data();       // upload
+        expect(d != nullptr, "cuda_data uploads");
+        float* w = t.cuda_data_write();       // device copy becomes the valid one
+        expect(hipMemset(w, 0, 32 * sizeof(float)) == hipSuccess, "device memset");
+        expect(hipDeviceSynchronize() == hipSuccess, "device sync");
+        expect(t.at(3, 7) == 0.0f, "host sees the device write after cuda_data_write");
+        t.at(0, 0) = 5.0f;                    // host copy becomes the valid one
+        const float* d2 = t.cuda_data();
+        float back = 0.0f;
+        expect(hipMemcpy(&back, d2, sizeof(float), hipMemcpyDeviceToHost) == hipSuccess, "readback");
+        expect(back == 5.0f, "device sees the host write after a non-const at()");
+        Tensor u = t;                         // deep copy of the host data
+        u.at(0, 0) = 7.0f;
+        expect(t.at(0, 0) == 5.0f, "copies are independent");
+        expect_throw<std::out_of_range>([&] { (void)t.at(4, 0); }, "Tensor index", "at() bounds");
+        expect_throw<std::invalid_argument>([&] { t.reshape({5, 7}); }, "reshape changes tensor size", "reshape");
+    }
+
+    // --- the reference's exceptions -------------------------------------------
+    {
+        std::vector<const Tensor*> w1, w2, w3;
+        for (std::size_t e = 0; e + 1 < E; ++e) {
+            w1.push_back(&experts[e].w1());
+            w2.push_back(&experts[e].w2());
+            w3.push_back(&experts[e].w3());
+        }
+        expect_throw<std::invalid_argument>([&] { tensor_ops::register_moe_weights_gpu(w1, w2, w3); },
+                                            "MoE weight table size", "15-expert table");
+        Tensor bad_router({T, E - 1}), out;
+        expect_throw<std::invalid_argument>([&] { tensor_ops::moe_forward_grouped_gpu(x, bad_router, 1, out); },
+                                            "grouped MoE shape or handle", "router shape");
+        Tensor router({T, E});
+        expect_throw<std::invalid_argument>([&] { tensor_ops::moe_forward_grouped_gpu(x, router, 0, out); },
+                                            "grouped MoE shape or handle", "handle 0");
+        expect_throw<std::invalid_argument>([&] { tensor_ops::moe_forward_grouped_gpu(x, router, 1u << 20, out); },
+                                            "grouped MoE shape or handle", "unknown handle");
+        Tensor c({T, 3});
+        expect_throw<std::invalid_argument>([&] { tensor_ops::matmul_transposed_gpu(x, gate, c); },
+                                            "matmul_transposed_gpu shape", "matmul shape");
+        Tensor y;
+        expect_throw<std::invalid_argument>([&] { moe32.forward(x, y, false); }, nullptr, "CPU path");
+    }
+
+    write_raw(dir, "x", x);
+    write_raw(dir, "gate", gate);
+    write_raw(dir, "w1", w1_all);
+    write_raw(dir, "w2", w2_all);
+    write_raw(dir, "w3", w3_all);
+    write_raw(dir, "y_f32", y32);
+    write_raw(dir, "y_bf16", y16);
+    write_raw(dir, "mlp_y", ymlp);
+    write_raw(dir, "logits", logits);
+    std::printf("layer_check: %d failure(s)\n", g_failures);
+    return g_failures ? 1 : 0;
+}
