@@ -51,7 +51,7 @@ class WeightsDesc(ctypes.Structure):
 class WsLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in (
         "total_bytes", "logits", "routes", "tile_counts", "counts", "offsets",
-        "assignment_rows", "route_positions", "act", "act_scale", "y", "xq", "xq_scale")]
+        "assignment_rows", "route_positions", "act", "act_scale", "y", "xq", "xq_scale", "actq")]
 
 
 class ApsError(RuntimeError):

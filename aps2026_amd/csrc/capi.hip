@@ -56,12 +56,20 @@ struct WeightSet {
     float* w1 = nullptr;         // [E][F][H]
     float* w3 = nullptr;         // [E][F][H]
     float* w2 = nullptr;         // [E][H][F]
+    // fp8 path
+    uint8_t* q13 = nullptr;      // e4m3 tile images [E][F/64][H/128][128][128]
+    uint8_t* q2 = nullptr;       // e4m3 tile images [E][H/128][Kp/128][128][128]
+    float* s1 = nullptr;         // [E][F] per-channel scales of w1
+    float* s3 = nullptr;         // [E][F]
+    float* s2 = nullptr;         // [E][H]
     ~WeightSet() {
         int cur = 0;
         (void)hipGetDevice(&cur);
         if (cur != device) (void)hipSetDevice(device);
         for (void* p : {static_cast<void*>(w13), static_cast<void*>(w2b), static_cast<void*>(w1),
-                        static_cast<void*>(w3), static_cast<void*>(w2)})
+                        static_cast<void*>(w3), static_cast<void*>(w2), static_cast<void*>(q13),
+                        static_cast<void*>(q2), static_cast<void*>(s1), static_cast<void*>(s3),
+                        static_cast<void*>(s2)})
             if (p) (void)hipFree(p);
         if (cur != device) (void)hipSetDevice(cur);
     }
@@ -78,6 +86,8 @@ WeightSet* lookup(uint64_t handle) {
 
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+size_t kpad128(int n) { return (static_cast<size_t>(n) + 127) / 128 * 128; }
 
 void make_layout(const WeightSet& w, int64_t rows, aps_moe_ws_layout* L) {
     std::memset(L, 0, sizeof(*L));
@@ -98,11 +108,20 @@ void make_layout(const WeightSet& w, int64_t rows, aps_moe_ws_layout* L) {
     L->assignment_rows = take(2 * T * 4);
     L->route_positions = take(2 * T * 4);
     L->act = take(2 * T * static_cast<size_t>(w.F) * elt);
-    L->act_scale = 0;
     L->y = take(2 * T * static_cast<size_t>(w.H) * elt);
-    // bf16 copy of x for the fused entry points when x arrives as fp32
-    L->xq = w.compute == APS_DTYPE_BF16 ? take(T * static_cast<size_t>(w.H) * 2) : 0;
+    L->act_scale = 0;
+    L->actq = 0;
+    L->xq = 0;
     L->xq_scale = 0;
+    if (w.compute == APS_DTYPE_BF16) {
+        // bf16 copy of x for the fused entry points when x arrives as fp32
+        L->xq = take(T * static_cast<size_t>(w.H) * 2);
+    } else if (w.compute == APS_DTYPE_E4M3) {
+        L->xq = take(T * static_cast<size_t>(w.H));
+        L->xq_scale = take(T * 4);
+        L->actq = take(2 * T * static_cast<size_t>(kpad128(w.F)));
+        L->act_scale = take(2 * T * 4);
+    }
     L->total_bytes = off;
 }
 
@@ -148,8 +167,16 @@ int run_ffn(const WeightSet& w, const void* x, int64_t rows, const uint32_t* off
     return run_ffn_down(w, act, rows, offsets, y, s);
 }
 
+// The fp8 path quantises x and the activations per row inside the fused
+// entry points, so its staged GEMMs are not exposed on their own.
+int check_not_fp8(const WeightSet& w, const char* what) {
+    if (w.compute == APS_DTYPE_E4M3)
+        return fail(APS_ERR_DTYPE, "%s: fp8 weight sets run through aps_moe_forward / aps_moe_forward_grouped", what);
+    return APS_OK;
+}
+
 int check_x_dtype(const WeightSet& w, int32_t x_dtype) {
-    const int want = w.compute == APS_DTYPE_F32 ? APS_DTYPE_F32 : APS_DTYPE_BF16;
+    const int want = w.compute == APS_DTYPE_F32 ? APS_DTYPE_F32 : APS_DTYPE_BF16;  // fp8 sets quantise bf16 x
     if (x_dtype != want)
         return fail(APS_ERR_DTYPE, "x dtype %d does not match the weight set (expects %d)", x_dtype, want);
     return APS_OK;
@@ -172,8 +199,25 @@ int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const 
     APS_HIP(aps::launch_route_top2(logits, rows, w.E, routes, tiles, s), "route_top2 launch");
     APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, w.E, counts, offsets, arows, rpos, s),
             "dispatch launch");
-    int rc = run_ffn(w, x, rows, offsets, arows, ws + L.act, ws + L.y, s);
-    if (rc) return rc;
+    if (w.compute == APS_DTYPE_E4M3) {
+        auto* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
+        auto* xs = reinterpret_cast<float*>(ws + L.xq_scale);
+        auto* act = reinterpret_cast<aps::bf16_t*>(ws + L.act);
+        auto* actq = reinterpret_cast<uint8_t*>(ws + L.actq);
+        auto* as = reinterpret_cast<float*>(ws + L.act_scale);
+        const int64_t kp = static_cast<int64_t>(kpad128(w.F));
+        APS_HIP(aps::launch_quant_rows_e4m3(static_cast<const aps::bf16_t*>(x), w.H, w.H, xq, w.H, xs, rows, s),
+                "quantise x launch");
+        APS_HIP(aps::launch_ffn_up_fp8(xq, xs, offsets, arows, w.q13, w.s1, w.s3, act, rows, w.H, w.F, w.E, s),
+                "ffn_up_fp8 launch");
+        APS_HIP(aps::launch_quant_rows_e4m3(act, w.F, w.F, actq, kp, as, 2 * rows, s), "quantise act launch");
+        APS_HIP(aps::launch_ffn_down_fp8(actq, as, offsets, w.q2, w.s2, reinterpret_cast<aps::bf16_t*>(ws + L.y),
+                                         rows, w.H, w.F, w.E, s),
+                "ffn_down_fp8 launch");
+    } else {
+        int rc = run_ffn(w, x, rows, offsets, arows, ws + L.act, ws + L.y, s);
+        if (rc) return rc;
+    }
     APS_HIP(aps::launch_combine(ws + L.y, w.compute != APS_DTYPE_F32, rpos, rows, w.H, out,
                                 out_dtype == APS_DTYPE_BF16, s),
             "combine launch");
@@ -208,6 +252,14 @@ int aps_moe_weights_register(const aps_moe_weights_desc* d, void* stream, uint64
     } else if (d->compute_dtype == APS_DTYPE_BF16) {
         if (d->src_dtype != APS_DTYPE_F32 && d->src_dtype != APS_DTYPE_BF16)
             return fail(APS_ERR_DTYPE, "bf16 compute needs fp32 or bf16 source weights");
+    } else if (d->compute_dtype == APS_DTYPE_E4M3) {
+        if (d->src_dtype != APS_DTYPE_E4M3)
+            return fail(APS_ERR_DTYPE, "fp8 compute needs e4m3 source weights with per-channel scales");
+        if (!d->w1_scale || !d->w3_scale || !d->w2_scale)
+            return fail(APS_ERR_ARG, "register: NULL fp8 scale table");
+        for (int e = 0; e < d->num_experts; ++e)
+            if (!d->w1_scale[e] || !d->w3_scale[e] || !d->w2_scale[e])
+                return fail(APS_ERR_ARG, "register: NULL fp8 scale pointer for expert %d", e);
     } else {
         return fail(APS_ERR_DTYPE, "compute dtype %d not supported", d->compute_dtype);
     }
@@ -230,6 +282,23 @@ int aps_moe_weights_register(const aps_moe_weights_desc* d, void* stream, uint64
             APS_HIP(hipMemcpyAsync(w->w3 + e * fh, d->w3[e], fh * 4, hipMemcpyDeviceToDevice, s), "copy w3");
             APS_HIP(hipMemcpyAsync(w->w2 + e * fh, d->w2[e], fh * 4, hipMemcpyDeviceToDevice, s), "copy w2");
         }
+    } else if (w->compute == APS_DTYPE_E4M3) {
+        const size_t kp = kpad128(w->F);
+        APS_HIP(hipMalloc(&w->q13, 2 * n), "hipMalloc w13 fp8");
+        APS_HIP(hipMalloc(&w->q2, static_cast<size_t>(w->E) * w->H * kp), "hipMalloc w2 fp8");
+        APS_HIP(hipMalloc(&w->s1, static_cast<size_t>(w->E) * w->F * 4), "hipMalloc s1");
+        APS_HIP(hipMalloc(&w->s3, static_cast<size_t>(w->E) * w->F * 4), "hipMalloc s3");
+        APS_HIP(hipMalloc(&w->s2, static_cast<size_t>(w->E) * w->H * 4), "hipMalloc s2");
+        for (int e = 0; e < w->E; ++e) {
+            APS_HIP(hipMemcpyAsync(w->s1 + static_cast<size_t>(e) * w->F, d->w1_scale[e], w->F * 4u,
+                                   hipMemcpyDeviceToDevice, s), "copy s1");
+            APS_HIP(hipMemcpyAsync(w->s3 + static_cast<size_t>(e) * w->F, d->w3_scale[e], w->F * 4u,
+                                   hipMemcpyDeviceToDevice, s), "copy s3");
+            APS_HIP(hipMemcpyAsync(w->s2 + static_cast<size_t>(e) * w->H, d->w2_scale[e], w->H * 4u,
+                                   hipMemcpyDeviceToDevice, s), "copy s2");
+        }
+        APS_HIP(aps::launch_pack_w13_e4m3(d->w1, d->w3, w->q13, w->E, w->F, w->H, s), "pack w1/w3 fp8");
+        APS_HIP(aps::launch_pack_w2_e4m3(d->w2, w->q2, w->E, w->F, w->H, s), "pack w2 fp8");
     } else {
         const bool src_bf16 = d->src_dtype == APS_DTYPE_BF16;
         APS_HIP(hipMalloc(&w->w13, 2 * n * 2), "hipMalloc w13");
@@ -325,6 +394,7 @@ int aps_moe_expert_ffn(uint64_t handle, const void* x, int32_t x_dtype, int64_t 
     if (!w) return fail(APS_ERR_HANDLE, "grouped MoE shape or handle: invalid handle %llu",
                         (unsigned long long)handle);
     if (int rc = check_device(*w)) return rc;
+    if (int rc = check_not_fp8(*w, "expert_ffn")) return rc;
     if (rows < 0) return fail(APS_ERR_SHAPE, "expert_ffn: rows %lld", (long long)rows);
     if (int rc = check_x_dtype(*w, x_dtype)) return rc;
     if (rows > 0 && (!x || !offsets || !assignment_rows || !act || !y_perm))
@@ -340,6 +410,7 @@ int aps_moe_ffn_up(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows
     if (!w) return fail(APS_ERR_HANDLE, "grouped MoE shape or handle: invalid handle %llu",
                         (unsigned long long)handle);
     if (int rc = check_device(*w)) return rc;
+    if (int rc = check_not_fp8(*w, "ffn_up")) return rc;
     if (rows < 0) return fail(APS_ERR_SHAPE, "ffn_up: rows %lld", (long long)rows);
     if (int rc = check_x_dtype(*w, x_dtype)) return rc;
     if (rows > 0 && (!x || !offsets || !assignment_rows || !act)) return fail(APS_ERR_ARG, "ffn_up: NULL pointer");
@@ -353,6 +424,7 @@ int aps_moe_ffn_down(uint64_t handle, const void* act, const float* act_scale, i
     if (!w) return fail(APS_ERR_HANDLE, "grouped MoE shape or handle: invalid handle %llu",
                         (unsigned long long)handle);
     if (int rc = check_device(*w)) return rc;
+    if (int rc = check_not_fp8(*w, "ffn_down")) return rc;
     if (rows < 0) return fail(APS_ERR_SHAPE, "ffn_down: rows %lld", (long long)rows);
     if (rows > 0 && (!act || !offsets || !y_perm)) return fail(APS_ERR_ARG, "ffn_down: NULL pointer");
     return run_ffn_down(*w, act, rows, offsets, y_perm, static_cast<hipStream_t>(stream));
@@ -456,6 +528,7 @@ int aps_mlp_forward(uint64_t handle, const void* x, int32_t x_dtype, int64_t row
     if (!w) return fail(APS_ERR_HANDLE, "mlp: invalid handle %llu", (unsigned long long)handle);
     if (int rc = check_device(*w)) return rc;
     if (w->E != 1) return fail(APS_ERR_SHAPE, "mlp: weight set has %d experts, a dense FFN has 1", w->E);
+    if (int rc = check_not_fp8(*w, "mlp")) return rc;
     if (rows < 0 || rows > (int64_t(1) << 30)) return fail(APS_ERR_SHAPE, "mlp: rows %lld", (long long)rows);
     if (int rc = check_x_dtype(*w, x_dtype)) return rc;
     if (rows == 0) return APS_OK;

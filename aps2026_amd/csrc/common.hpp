@@ -83,6 +83,8 @@ hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_c
 
 // bf16 MFMA path.  w13 / w2 are packed tile images (see launch_pack_*):
 // w13 [E][F/64][H/64][128][64], w2 [E][H/128][F/64][128][64]; act/y bf16.
+// The fp8 path's images are 128 x 128 bytes: w13 [E][F/64][H/128][128][128],
+// w2 [E][H/128][Kp/128][128][128] (Kp = F rounded up to 128, zero padded).
 hipError_t launch_ffn_up_bf16(const bf16_t* x, const uint32_t* offsets,
                               const uint32_t* assignment_rows, const bf16_t* w13,
                               bf16_t* act, int64_t rows, int hidden, int ffn, int experts,
@@ -90,6 +92,25 @@ hipError_t launch_ffn_up_bf16(const bf16_t* x, const uint32_t* offsets,
 hipError_t launch_ffn_down_bf16(const bf16_t* act, const uint32_t* offsets, const bf16_t* w2,
                                 bf16_t* y, int64_t rows, int hidden, int ffn, int experts,
                                 hipStream_t s);
+
+// fp8 e4m3 MFMA path.  xq [rows][H] codes with x_scale [rows]; act is bf16
+// [A][F]; actq [A][Kp] codes with act_scale [A]; w*_scale per output
+// channel ([E][F] for w1/w3, [E][H] for w2); y bf16.
+hipError_t launch_ffn_up_fp8(const uint8_t* xq, const float* x_scale, const uint32_t* offsets,
+                             const uint32_t* assignment_rows, const uint8_t* w13, const float* w1_scale,
+                             const float* w3_scale, bf16_t* act, int64_t rows, int hidden, int ffn,
+                             int experts, hipStream_t s);
+hipError_t launch_ffn_down_fp8(const uint8_t* actq, const float* act_scale, const uint32_t* offsets,
+                               const uint8_t* w2, const float* w2_scale, bf16_t* y, int64_t rows, int hidden,
+                               int ffn, int experts, hipStream_t s);
+// Per-row e4m3 quantisation of bf16 rows (n values, row strides in
+// elements / bytes; codes zero-padded to dst_stride).
+hipError_t launch_quant_rows_e4m3(const bf16_t* src, int64_t src_stride, int n, uint8_t* dst, int64_t dst_stride,
+                                  float* scale, int64_t rows, hipStream_t s);
+hipError_t launch_pack_w13_e4m3(const void* const* w1, const void* const* w3, uint8_t* dst, int experts, int ffn,
+                                int hidden, hipStream_t s);
+hipError_t launch_pack_w2_e4m3(const void* const* w2, uint8_t* dst, int experts, int ffn, int hidden,
+                               hipStream_t s);
 
 // fp32 FMA-chain path (reference accumulation order).  w1/w3 [E][F][H],
 // w2 [E][H][F]; act/y are f32.

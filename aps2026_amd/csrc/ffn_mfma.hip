@@ -1,0 +1,611 @@
+// Grouped expert FFN on gfx950 MFMA: bf16 (fp32 accumulate) and fp8 e4m3
+// (fp32 accumulate, per-channel weight scales, per-row activation scales).
+//
+// Reference: k_moe_pair_silu_8x8 (src/tensor.cu:1838-1966) computes
+// silu(x . w1^T) * (x . w3^T) for each expert's row range with the gather
+// folded into the A load (assignment_rows), and k_moe_matmul_8x8
+// (src/tensor.cu:1740-1836) multiplies by w2^T.  Both are fp32 SIMT GEMMs
+// over a 128-row work list (src/tensor.cu:1333-1374).  The reference has no
+// bf16 or fp8 path; their numerics are this library's (documented at each
+// epilogue).
+//
+// gfx950 design, shared by both GEMMs and both formats.
+//  * One wave per SIMD; each wave owns a 64-row x 128-column output tile of
+//    32x32 MFMAs (2 x 4 tiles, 128 fp32 accumulators per lane).  Per MFMA
+//    k step a wave reads 2 A + 4 B operand fragments from LDS for 8 MFMAs:
+//    42.7 FLOP per LDS byte in bf16 (85 in fp8), against 32 for a 64x64
+//    wave tile, so LDS bandwidth (128 B/clk per CU) stays below the MFMA rate.
+//  * A block of 4 waves is "wide" (128 token rows x 2 column blocks) or
+//    "tall" (256 token rows x 1 column block).  A column block is 128 B
+//    rows: for w1||w3, 64 gate + the same 64 up rows (SwiGLU closes inside
+//    each lane); for w2, 128 hidden columns.
+//  * Stages are byte rows: a stage holds 384 rows of 128 bytes (48 KB) --
+//    64 k of bf16 or 128 k of fp8.  Operands stream from global memory
+//    straight into a three-stage LDS ring with global_load_lds_dwordx4 (no
+//    VGPR staging).  16-byte chunks are XOR-swizzled for gfx950's 64-bank
+//    LDS so that neither the copies nor the ds_read_b128 operand fetches
+//    conflict.
+//  * Weights are re-packed at registration into the swizzled 128-row x
+//    128-byte tile images (16 KB) the ring holds (launch_pack_*): a B row of
+//    a stage is 128 contiguous bytes, copied verbatim.
+//  * The token gather of the w1||w3 GEMM is an index on the A load, as in
+//    the reference: no permuted copy of x is ever written.
+//  * The work list is built on the device from offsets[] (no host round
+//    trip), expert by expert, and dealt to XCDs in contiguous slices so
+//    operand reuse stays inside one L2; skewed experts simply own more
+//    blocks.
+#include "common.hpp"
+
+namespace aps {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+// native vectors (not HIP's uint4 struct, whose copies become memcpy through
+// a stack slot): 16 bytes = one ds_read_b128 / global_load_dwordx4
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kRowBytes = 128;                 // one stage row: 8 chunks of 16 bytes
+constexpr int kImageBytes = 128 * kRowBytes;   // one packed weight tile image
+constexpr int kXcds = 8;
+#ifndef APS_DOWN_TALL
+#define APS_DOWN_TALL true
+#endif
+
+// Byte offset of 16-byte chunk `chunk` (0..7) of stage row `row`.  gfx950's
+// LDS has 64 four-byte banks (a 256-byte bank row = two stage rows) and
+// serves a ds_read_b128 16 lanes at a time.  An MFMA operand fetch reads the
+// same logical chunk from 16 consecutive rows, so the physical chunk is
+// chunk ^ ((row >> 1) & 7): rows 2m and 2m+1 sit in the two halves of a bank
+// row, and the eight pairs of a 16-row group get eight different chunks --
+// sixteen distinct 16-byte bank groups, no conflict.
+__device__ inline int swz(int row, int chunk) { return row * kRowBytes + ((chunk ^ ((row >> 1) & 7)) << 4); }
+
+// Two fp32 -> packed bf16, round to nearest even (one v_cvt_pk_bf16_f32).
+__device__ inline uint32_t pack2_bf16(float lo, float hi) {
+    bf16x2_t v;
+    v[0] = static_cast<__bf16>(lo);
+    v[1] = static_cast<__bf16>(hi);
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// silu(g) * u for the MFMA paths: fp32 math with the hardware exp2 and
+// reciprocal (the result is rounded to bf16, far coarser than their error).
+__device__ inline float swiglu(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
+#define APS_GP(p) ((const __attribute__((address_space(1))) void*)(p))
+#define APS_LP(p) ((__attribute__((address_space(3))) void*)(p))
+#define APS_PIN() __builtin_amdgcn_sched_barrier(0)
+
+// One direct-to-LDS copy: lane i writes LDS bytes [16i, 16i+16) of the
+// wave-uniform 1 KB slot at lds_slot (eight stage rows).
+__device__ inline void dma16(const uint8_t* src, uint8_t* lds_slot) {
+    __builtin_amdgcn_global_load_lds(APS_GP(src), APS_LP(lds_slot), 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt[5:4] at bits [15:14]); n must be a constant.
+template <int N>
+__device__ inline void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+}
+
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left at their maximum).
+__device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14)); }
+
+// A raw s_barrier: __syncthreads() adds a workgroup fence, which drains every
+// in-flight load (vmcnt(0)) and would serialise the ring.
+__device__ inline void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// ---------------------------------------------------------------------------
+// Operand formats.  kSub MFMA k steps per 128-byte stage row; a fragment is
+// one lane's share of a 32-row MFMA operand: lane l holds row l % 32 and the
+// k half (l / 32) of the step, the same for A and B.
+struct Bf16Fmt {
+    static constexpr int kSub = 4;             // 32x32x16: 16 k = 32 bytes per step
+    static constexpr int kElt = 2;
+    typedef bf16x8_t frag_t;
+    __device__ static frag_t load(const uint8_t* st, int row, int kk, int lane) {
+        return __builtin_bit_cast(frag_t, *reinterpret_cast<const u32x4_t*>(st + swz(row, 2 * kk + (lane >> 5))));
+    }
+    __device__ static f32x16_t mma(const frag_t& a, const frag_t& b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+struct Fp8Fmt {
+    static constexpr int kSub = 2;             // 32x32x64: 64 k = 64 bytes per step
+    static constexpr int kElt = 1;
+    typedef i32x8_t frag_t;
+    __device__ static frag_t load(const uint8_t* st, int row, int kk, int lane) {
+        const int c = 4 * kk + 2 * (lane >> 5);
+        const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(st + swz(row, c));
+        const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(st + swz(row, c + 1));
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+    // e4m3 x e4m3 (format code 0 for both operands), unit scales
+    __device__ static f32x16_t mma(const frag_t& a, const frag_t& b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Stage ring.  A stage holds kStageRows = 384 rows of 128 bytes: RA rows of
+// A (token rows) followed by 384 - RA rows of B (packed weight tile rows).
+constexpr int kStageRows = 384;
+constexpr int kStageBytes = kStageRows * kRowBytes;  // 48 KB
+constexpr int kStages = 3;                           // 3 x 48 KB = 144 KB of LDS
+
+struct Ring3 {
+    uint8_t s[kStages][kStageBytes];
+};
+
+template <bool TALL>
+struct Shape {
+    static constexpr int RA = TALL ? 256 : 128;  // A rows per stage
+    static constexpr int NA = RA / 32;           // A slots per wave
+};
+
+// Load slot s (0..11) of wave w copies stage rows 32s + 8w .. +8 (1 KB).
+// A slots advance one 128-byte row chunk per stage, B slots one tile image.
+struct Slots {
+    const uint8_t* p[12];
+};
+
+template <bool TALL>
+__device__ inline void issue_slots(uint8_t* stage, const Slots& sl, int kt, int wave, int lo, int hi) {
+#pragma unroll
+    for (int s = lo; s < hi; ++s) {
+        const int64_t adv = s < Shape<TALL>::NA ? static_cast<int64_t>(kt) * kRowBytes
+                                               : static_cast<int64_t>(kt) * kImageBytes;
+        dma16(sl.p[s] + adv, stage + (32 * s + 8 * wave) * kRowBytes);
+    }
+}
+
+// Stage row and logical chunk of this lane in a load slot: lane i lands at
+// physical chunk i & 7 of row 8 * (slot row group) + i / 8, so it fetches
+// the logical chunk that swz() places there.
+__device__ inline int slot_row(int s, int wave, int lane) { return 32 * s + 8 * wave + (lane >> 3); }
+__device__ inline int slot_chunk(int row, int lane) { return (lane & 7) ^ ((row >> 1) & 7); }
+
+template <class Fmt>
+struct Frags {
+    typename Fmt::frag_t a[2];
+    typename Fmt::frag_t b[4];
+};
+
+template <class Fmt>
+__device__ inline void load_frags(Frags<Fmt>& f, const uint8_t* st, int kk, int lane, int aR, int bR) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) f.a[i] = Fmt::load(st, aR + i * 32 + (lane & 31), kk, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.b[j] = Fmt::load(st, bR + j * 32 + (lane & 31), kk, lane);
+}
+
+// B fragments go in the MFMA's first operand slot: the result is then the
+// transposed tile, so each lane holds one token row (lane % 32) and, per
+// accumulator register group q = v / 4, the four consecutive output columns
+// 8q + 4 * (lane / 32) .. +3 -- the shape the epilogues stage as 8-byte runs.
+template <class Fmt>
+__device__ inline void mma_frags(const Frags<Fmt>& f, f32x16_t (&acc)[2][4]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = Fmt::mma(f.b[j], f.a[i], acc[i][j]);
+}
+
+// acc[i][j] += stage rows aR + 32i (A) x stage rows bR + 32j (B) over KT
+// stages.  The operand fragments of MFMA step g+1 are read from LDS while
+// the MFMAs of step g run (two fragment sets); each step first waits for its
+// own fragments and only then issues the next step's reads, so the compiler's
+// LDS wait never covers reads issued just before the MFMAs.  The stage
+// hand-over sits before the MFMAs of a stage's last step: wait until stage
+// kt+1 has landed (only stage kt+2 may still be in flight) and every read of
+// stage kt is done, one s_barrier, read stage kt+1's first fragments, and
+// only then issue stage kt's last MFMAs -- the barrier and the first LDS
+// latency of a stage hide behind MFMA work.  The slot freed by that barrier
+// (stage kt's) is refilled with stage kt+3 during stage kt+1's other steps.
+template <bool TALL, class Fmt>
+__device__ inline void mainloop3(Ring3& ring, const Slots& sl, int KT, int wave, int lane, int aR, int bR,
+                                 f32x16_t (&acc)[2][4]) {
+    constexpr int kSub = Fmt::kSub;
+    static_assert(kSub % 2 == 0, "ping-pong needs an even step count");
+    issue_slots<TALL>(ring.s[0], sl, 0, wave, 0, 12);
+    if (KT > 1) issue_slots<TALL>(ring.s[1], sl, 1, wave, 0, 12);
+    if (KT > 2) issue_slots<TALL>(ring.s[2], sl, 2, wave, 0, 12);
+    if (KT > 2) wait_vm_lgkm0<24>();
+    else if (KT > 1) wait_vm_lgkm0<12>();
+    else wait_vm_lgkm0<0>();
+    raw_barrier();
+    Frags<Fmt> f[2];
+    load_frags<Fmt>(f[0], ring.s[0], 0, lane, aR, bR);
+    int cur = 0;
+    int prev = 2;  // slot of stage kt - 1, refilled with stage kt + 2
+    for (int kt = 0; kt < KT; ++kt) {
+        const uint8_t* st = ring.s[cur];
+        const int nxt = cur == 2 ? 0 : cur + 1;
+        const bool refill = kt >= 1 && kt + 2 < KT;
+#pragma unroll
+        for (int s = 0; s + 1 < kSub; ++s) {
+            wait_lgkm0();
+            load_frags<Fmt>(f[(s + 1) & 1], st, s + 1, lane, aR, bR);
+            if (refill) issue_slots<TALL>(ring.s[prev], sl, kt + 2, wave, 12 * s / (kSub - 1), 12 * (s + 1) / (kSub - 1));
+            APS_PIN();
+            mma_frags<Fmt>(f[s & 1], acc);
+            APS_PIN();
+        }
+        if (kt + 1 < KT) {
+            if (kt + 2 < KT) wait_vm_lgkm0<12>();
+            else wait_vm_lgkm0<0>();
+            raw_barrier();
+            load_frags<Fmt>(f[0], ring.s[nxt], 0, lane, aR, bR);
+        } else {
+            wait_lgkm0();
+        }
+        APS_PIN();
+        mma_frags<Fmt>(f[1], acc);
+        APS_PIN();
+        prev = cur;
+        cur = nxt;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Work list, expert by expert.  `nblk` column blocks per row (F/64 for
+// w1||w3, H/128 for w2); pairs = nblk / 2 wide blocks per 128-row tile and,
+// when nblk is odd, one tall block (256 rows x the last column block) per
+// 256-row group (ALL_TALL: every column block as a tall block).  Expert e's
+// rows form 256-row groups; a group contributes, in order, the wide blocks
+// of its two row tiles (row tile major) and then its tall block(s), so
+// blocks sharing token rows are adjacent in the list and land in one XCD's
+// L2 when XCD x takes the contiguous slice [x * per, (x + 1) * per)
+// (workgroup b runs on XCD b % 8).  Every output position and column block
+// is covered exactly once.
+struct Tile {
+    int expert, nb0;
+    uint32_t m0, end;
+    bool tall;
+};
+
+template <bool ALL_TALL>
+__device__ inline bool locate_block(const uint32_t* __restrict__ offsets, int E, int nblk, Tile& u) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t lo = lane < E ? offsets[lane] : 0u;
+    uint32_t hi = __shfl_down(lo, 1);
+    if (lane == E - 1) hi = offsets[E];
+    const uint32_t cnt = lane < E ? hi - lo : 0u;
+    const int pairs = ALL_TALL ? 0 : nblk / 2, odd = ALL_TALL ? nblk : (nblk & 1);
+    const int r128 = static_cast<int>((cnt + 127) / 128);
+    int incl = pairs * r128 + odd * static_cast<int>((cnt + 255) / 256);  // blocks of this expert
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d);
+        if (lane >= d) incl += v;
+    }
+    const int total = __shfl(incl, 63);
+    const int b = blockIdx.x;
+    const int per = (total + kXcds - 1) / kXcds;
+    const int l = b / kXcds;
+    const int t = (b % kXcds) * per + l;
+    if (l >= per || t >= total) return false;
+    const uint64_t m = __ballot(lane < E && incl > t);
+    const int e = __ffsll(static_cast<unsigned long long>(m)) - 1;
+    const int before_incl = __shfl(incl, e > 0 ? e - 1 : 0);
+    const int i = t - (e > 0 ? before_incl : 0);     // block index within expert e
+    const int e_r128 = __shfl(r128, e);
+    const int gsz = 2 * pairs + odd;                 // blocks of a full 256-row group
+    const int g = i / gsz;
+    const int r = i - g * gsz;
+    const int nw = e_r128 - 2 * g < 2 ? e_r128 - 2 * g : 2;  // 128-row tiles in group g
+    u.expert = e;
+    u.end = __shfl(hi, e);
+    const uint32_t e_lo = __shfl(lo, e);
+    if (!ALL_TALL && r < pairs * nw) {
+        const int pp = ALL_TALL ? 1 : pairs;         // pairs > 0 on this branch
+        u.m0 = e_lo + static_cast<uint32_t>(2 * g + r / pp) * 128u;
+        u.nb0 = 2 * (r % pp);
+        u.tall = false;
+    } else {
+        u.m0 = e_lo + static_cast<uint32_t>(g) * 256u;
+        u.nb0 = ALL_TALL ? r : nblk - 1;
+        u.tall = true;
+    }
+    return true;
+}
+
+__device__ inline void zero_acc(f32x16_t (&acc)[2][4]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+}
+
+// Stage rows of this wave's MFMA operands: A rows aR.. (64), B rows bR.. (128).
+template <bool TALL>
+__device__ inline int wave_a_row(int wave) { return TALL ? wave * 64 : (wave & 1) * 64; }
+template <bool TALL>
+__device__ inline int wave_b_row(int wave) { return Shape<TALL>::RA + (TALL ? 0 : (wave >> 1) * 128); }
+
+// B slots: rows of the packed tile images of column blocks nb0 (and nb0+1
+// for a wide block), copied verbatim -- the images are stored pre-swizzled,
+// and RA is a multiple of 16, so a stage row and its image row share their
+// swizzle.  `image0` is the first image of column block 0 of this expert;
+// a column block holds KT images.
+template <bool TALL>
+__device__ inline const uint8_t* b_slot(const uint8_t* image0, int64_t block_bytes, int nb0, int s, int wave,
+                                        int lane) {
+    const int rb = 32 * s + 8 * wave - Shape<TALL>::RA;  // first B row of this slot
+    return image0 + static_cast<int64_t>(nb0 + rb / 128) * block_bytes + (rb % 128) * kRowBytes + lane * 16;
+}
+
+// Per-output-column scales of this lane for accumulator register group q of
+// B fragment j: columns c0 + 32j + 8q + 4 * (lane / 32) .. +3.
+__device__ inline float4 col_scales(const float* __restrict__ s, int c0, int j, int q, int lane) {
+    return *reinterpret_cast<const float4*>(s + c0 + 32 * j + 8 * q + 4 * (lane >> 5));
+}
+
+// ---------------------------------------------------------------------------
+// act[p][n] = silu(g) * u with, t = assignment_rows[p],
+//   bf16: g = x[t] . w1[e][n], u = x[t] . w3[e][n]             (fp32 accumulate)
+//   fp8 : g = (xq[t] . w1q[e][n]) * sx[t] * s1[e][n], u likewise with w3
+//         (codes multiplied exactly, fp32 accumulate, then the two scales)
+// act is stored as bf16.
+template <bool TALL, class Fmt>
+__device__ inline void ffn_up_block(Ring3& ring, const uint8_t* __restrict__ x, int64_t x_row_bytes,
+                                    const uint32_t* __restrict__ assignment_rows,
+                                    const uint8_t* __restrict__ w13, bf16_t* __restrict__ act, int H, int F,
+                                    const float* __restrict__ sx, const float* __restrict__ s1,
+                                    const float* __restrict__ s3, const Tile& u) {
+    constexpr bool kFp8 = Fmt::kElt == 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KT = H * Fmt::kElt / kRowBytes;
+    const int nblk = F / 64;
+    // A: gathered token rows; positions past the expert's end reuse its last
+    // row (a valid address; those rows are never stored).
+    Slots sl;
+    const int64_t block_bytes = static_cast<int64_t>(KT) * kImageBytes;
+    const uint8_t* image0 = w13 + static_cast<int64_t>(u.expert) * nblk * block_bytes;
+#pragma unroll
+    for (int s = 0; s < 12; ++s) {
+        if (s < Shape<TALL>::NA) {
+            const int row = slot_row(s, wave, lane);
+            uint32_t p = u.m0 + row;
+            p = p < u.end ? p : u.end - 1;
+            sl.p[s] = x + static_cast<int64_t>(assignment_rows[p]) * x_row_bytes + slot_chunk(row, lane) * 16;
+        } else {
+            sl.p[s] = b_slot<TALL>(image0, block_bytes, u.nb0, s, wave, lane);
+        }
+    }
+    const int aR = wave_a_row<TALL>(wave), bR = wave_b_row<TALL>(wave);
+    f32x16_t acc[2][4];
+    zero_acc(acc);
+    mainloop3<TALL, Fmt>(ring, sl, KT, wave, lane, aR, bR, acc);
+
+    // Epilogue: scales (fp8), SwiGLU in registers (B fragments 0,1 are gate
+    // columns 0..63 of the wave's column block, 2,3 the same up columns), the
+    // bf16 act tile staged in the idle ring, then written as 16-byte row
+    // chunks.
+    constexpr int kCols = TALL ? 64 : 128;   // act columns of the block tile
+    constexpr int kPitch = kCols + 8;        // elements; 16-byte aligned rows, banks staggered
+    bf16_t* stage = reinterpret_cast<bf16_t*>(ring.s[0]);
+    raw_barrier();
+    const int cbase = TALL ? 0 : (wave >> 1) * 64;
+    const int c0 = u.expert * F + u.nb0 * 64 + cbase;   // this wave's first gate/up column in s1 / s3
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int row = aR + i * 32 + (lane & 31);
+        float rs = 1.0f;
+        if constexpr (kFp8) {
+            uint32_t p = u.m0 + row;
+            p = p < u.end ? p : u.end - 1;
+            rs = sx[assignment_rows[p]];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float g[4], up[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    g[v] = acc[i][j][4 * q + v];
+                    up[v] = acc[i][j + 2][4 * q + v];
+                }
+                if constexpr (kFp8) {
+                    const float4 a1 = col_scales(s1, c0, j, q, lane), a3 = col_scales(s3, c0, j, q, lane);
+                    g[0] = g[0] * rs * a1.x; g[1] = g[1] * rs * a1.y; g[2] = g[2] * rs * a1.z; g[3] = g[3] * rs * a1.w;
+                    up[0] = up[0] * rs * a3.x; up[1] = up[1] * rs * a3.y; up[2] = up[2] * rs * a3.z; up[3] = up[3] * rs * a3.w;
+                }
+                const int col = cbase + 32 * j + 8 * q + 4 * (lane >> 5);
+                const u32x2_t v = {pack2_bf16(swiglu(g[0], up[0]), swiglu(g[1], up[1])),
+                                   pack2_bf16(swiglu(g[2], up[2]), swiglu(g[3], up[3]))};
+                *reinterpret_cast<u32x2_t*>(stage + row * kPitch + col) = v;
+            }
+    }
+    wait_vm_lgkm0<0>();
+    raw_barrier();
+    constexpr int kChunks = kCols / 8;       // 16-byte chunks per row
+#pragma unroll
+    for (int c = 0; c < Shape<TALL>::RA * kChunks / 256; ++c) {
+        const int id = tid + 256 * c;
+        const int r = id / kChunks, cc = id % kChunks;
+        const uint32_t p = u.m0 + r;
+        if (p < u.end)
+            *reinterpret_cast<u32x4_t*>(act + static_cast<int64_t>(p) * F + u.nb0 * 64 + cc * 8) =
+                *reinterpret_cast<const u32x4_t*>(stage + r * kPitch + cc * 8);
+    }
+}
+
+template <class Fmt>
+__global__ void __launch_bounds__(256, 1)
+k_ffn_up(const uint8_t* __restrict__ x, int64_t x_row_bytes, const uint32_t* __restrict__ offsets,
+         const uint32_t* __restrict__ assignment_rows, const uint8_t* __restrict__ w13, bf16_t* __restrict__ act,
+         int H, int F, int E, const float* __restrict__ sx, const float* __restrict__ s1,
+         const float* __restrict__ s3) {
+    __shared__ __align__(16) Ring3 ring;
+    Tile u;
+    if (!locate_block<false>(offsets, E, F / 64, u)) return;
+    if (u.tall) ffn_up_block<true, Fmt>(ring, x, x_row_bytes, assignment_rows, w13, act, H, F, sx, s1, s3, u);
+    else ffn_up_block<false, Fmt>(ring, x, x_row_bytes, assignment_rows, w13, act, H, F, sx, s1, s3, u);
+}
+
+// ---------------------------------------------------------------------------
+// y[p][n], bf16, with
+//   bf16: y = act[p] . w2[e][n]                               (fp32 accumulate)
+//   fp8 : y = (actq[p] . w2q[e][n]) * sa[p] * s2[e][n]
+// A rows are act_row_bytes apart; K = KT stages (fp8: F padded to 128).
+template <bool TALL, class Fmt>
+__device__ inline void ffn_down_block(Ring3& ring, const uint8_t* __restrict__ act, int64_t act_row_bytes,
+                                      const uint8_t* __restrict__ w2, bf16_t* __restrict__ y, int H, int KT,
+                                      const float* __restrict__ sa, const float* __restrict__ s2, const Tile& u) {
+    constexpr bool kFp8 = Fmt::kElt == 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    Slots sl;
+    const int64_t block_bytes = static_cast<int64_t>(KT) * kImageBytes;
+    const uint8_t* image0 = w2 + static_cast<int64_t>(u.expert) * (H / 128) * block_bytes;
+#pragma unroll
+    for (int s = 0; s < 12; ++s) {
+        if (s < Shape<TALL>::NA) {
+            const int row = slot_row(s, wave, lane);
+            uint32_t p = u.m0 + row;
+            p = p < u.end ? p : u.end - 1;
+            sl.p[s] = act + static_cast<int64_t>(p) * act_row_bytes + slot_chunk(row, lane) * 16;
+        } else {
+            sl.p[s] = b_slot<TALL>(image0, block_bytes, u.nb0, s, wave, lane);
+        }
+    }
+    const int aR = wave_a_row<TALL>(wave), bR = wave_b_row<TALL>(wave);
+    f32x16_t acc[2][4];
+    zero_acc(acc);
+    mainloop3<TALL, Fmt>(ring, sl, KT, wave, lane, aR, bR, acc);
+
+    // Epilogue: scales (fp8), the bf16 y tile staged in the idle ring (it
+    // spans the ring's first two stages), then written as 16-byte row chunks.
+    constexpr int kCols = TALL ? 128 : 256;  // y columns of the block tile
+    constexpr int kPitch = kCols + 8;
+    bf16_t* stage = reinterpret_cast<bf16_t*>(ring.s[0]);
+    raw_barrier();
+    const int cbase = TALL ? 0 : (wave >> 1) * 128;
+    const int c0 = u.expert * H + u.nb0 * 128 + cbase;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int row = aR + i * 32 + (lane & 31);
+        float rs = 1.0f;
+        if constexpr (kFp8) {
+            uint32_t p = u.m0 + row;
+            p = p < u.end ? p : u.end - 1;
+            rs = sa[p];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float o[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) o[v] = acc[i][j][4 * q + v];
+                if constexpr (kFp8) {
+                    const float4 a = col_scales(s2, c0, j, q, lane);
+                    o[0] = o[0] * rs * a.x; o[1] = o[1] * rs * a.y; o[2] = o[2] * rs * a.z; o[3] = o[3] * rs * a.w;
+                }
+                const int col = cbase + 32 * j + 8 * q + 4 * (lane >> 5);
+                const u32x2_t v = {pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
+                *reinterpret_cast<u32x2_t*>(stage + row * kPitch + col) = v;
+            }
+    }
+    wait_vm_lgkm0<0>();
+    raw_barrier();
+    constexpr int kChunks = kCols / 8;
+#pragma unroll
+    for (int c = 0; c < Shape<TALL>::RA * kChunks / 256; ++c) {
+        const int id = tid + 256 * c;
+        const int r = id / kChunks, cc = id % kChunks;
+        const uint32_t p = u.m0 + r;
+        if (p < u.end)
+            *reinterpret_cast<u32x4_t*>(y + static_cast<int64_t>(p) * H + u.nb0 * 128 + cc * 8) =
+                *reinterpret_cast<const u32x4_t*>(stage + r * kPitch + cc * 8);
+    }
+}
+
+template <class Fmt>
+__global__ void __launch_bounds__(256, 1)
+k_ffn_down(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint32_t* __restrict__ offsets,
+           const uint8_t* __restrict__ w2, bf16_t* __restrict__ y, int H, int KT, int E,
+           const float* __restrict__ sa, const float* __restrict__ s2) {
+    __shared__ __align__(16) Ring3 ring;
+    Tile u;
+    if (!locate_block<APS_DOWN_TALL>(offsets, E, H / 128, u)) return;
+    if (u.tall) ffn_down_block<true, Fmt>(ring, act, act_row_bytes, w2, y, H, KT, sa, s2, u);
+    else ffn_down_block<false, Fmt>(ring, act, act_row_bytes, w2, y, H, KT, sa, s2, u);
+}
+
+// Upper bound on the work-list length for A = 2 * rows positions.
+int64_t max_blocks(int64_t rows, int nblk, int experts, bool all_tall) {
+    if (all_tall) return max_row_tiles(2 * rows, 256, experts) * nblk;
+    return max_row_tiles(2 * rows, 128, experts) * (nblk / 2) +
+           ((nblk & 1) ? max_row_tiles(2 * rows, 256, experts) : 0);
+}
+
+dim3 grid_of(int64_t blocks) { return dim3(static_cast<unsigned>(ceil_div(blocks, kXcds) * kXcds)); }
+
+}  // namespace
+
+hipError_t launch_ffn_up_bf16(const bf16_t* x, const uint32_t* offsets,
+                              const uint32_t* assignment_rows, const bf16_t* w13,
+                              bf16_t* act, int64_t rows, int hidden, int ffn, int experts,
+                              hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (hidden % 64 != 0 || ffn % 64 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_ffn_up<Bf16Fmt>, grid_of(max_blocks(rows, ffn / 64, experts, false)), dim3(256), 0, s,
+                       reinterpret_cast<const uint8_t*>(x), static_cast<int64_t>(hidden) * 2, offsets,
+                       assignment_rows, reinterpret_cast<const uint8_t*>(w13), act, hidden, ffn, experts,
+                       nullptr, nullptr, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_ffn_down_bf16(const bf16_t* act, const uint32_t* offsets, const bf16_t* w2,
+                                bf16_t* y, int64_t rows, int hidden, int ffn, int experts,
+                                hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (hidden % 128 != 0 || ffn % 64 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_ffn_down<Bf16Fmt>, grid_of(max_blocks(rows, hidden / 128, experts, APS_DOWN_TALL)),
+                       dim3(256), 0, s, reinterpret_cast<const uint8_t*>(act), static_cast<int64_t>(ffn) * 2,
+                       offsets, reinterpret_cast<const uint8_t*>(w2), y, hidden, ffn / 64, experts, nullptr,
+                       nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_ffn_up_fp8(const uint8_t* xq, const float* x_scale, const uint32_t* offsets,
+                             const uint32_t* assignment_rows, const uint8_t* w13, const float* w1_scale,
+                             const float* w3_scale, bf16_t* act, int64_t rows, int hidden, int ffn,
+                             int experts, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (hidden % 128 != 0 || ffn % 64 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_ffn_up<Fp8Fmt>, grid_of(max_blocks(rows, ffn / 64, experts, false)), dim3(256), 0, s,
+                       xq, static_cast<int64_t>(hidden), offsets, assignment_rows, w13, act, hidden, ffn, experts,
+                       x_scale, w1_scale, w3_scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_ffn_down_fp8(const uint8_t* actq, const float* act_scale, const uint32_t* offsets,
+                               const uint8_t* w2, const float* w2_scale, bf16_t* y, int64_t rows, int hidden,
+                               int ffn, int experts, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (hidden % 128 != 0 || ffn % 64 != 0) return hipErrorInvalidValue;
+    const int kpad = static_cast<int>(ceil_div(ffn, 128) * 128);
+    hipLaunchKernelGGL(k_ffn_down<Fp8Fmt>, grid_of(max_blocks(rows, hidden / 128, experts, APS_DOWN_TALL)),
+                       dim3(256), 0, s, actq, static_cast<int64_t>(kpad), offsets, w2, y, hidden, kpad / 128,
+                       experts, act_scale, w2_scale);
+    return hipGetLastError();
+}
+
+}  // namespace aps

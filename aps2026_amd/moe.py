@@ -24,7 +24,9 @@ import torch
 from . import capi
 from .capi import ApsError
 
-_DTYPE_CODE = {torch.float32: capi.DTYPE_F32, torch.bfloat16: capi.DTYPE_BF16}
+_DTYPE_CODE = {torch.float32: capi.DTYPE_F32, torch.bfloat16: capi.DTYPE_BF16,
+               torch.float8_e4m3fn: capi.DTYPE_E4M3, torch.uint8: capi.DTYPE_E4M3}
+FP8 = torch.float8_e4m3fn
 
 
 def _stream(device: torch.device) -> ctypes.c_void_p:
@@ -58,10 +60,14 @@ class MoeWeights:
     """A registered expert weight set (the reference's 1-based handle)."""
 
     def __init__(self, w1: Sequence[torch.Tensor], w2: Sequence[torch.Tensor],
-                 w3: Sequence[torch.Tensor], compute_dtype: torch.dtype = torch.bfloat16):
+                 w3: Sequence[torch.Tensor], compute_dtype: torch.dtype = torch.bfloat16,
+                 scales: Optional[tuple] = None):
+        """fp8 (compute_dtype torch.float8_e4m3fn): w1/w2/w3 hold e4m3 codes
+        (uint8 or float8_e4m3fn tensors) and ``scales = (s1, s2, s3)`` the
+        per-output-channel fp32 scales ([F], [H], [F] per expert)."""
         E = len(w1)
         _require(len(w2) == E and len(w3) == E, "MoE weight table size")
-        _require(E >= 2, "MoE weight table size")
+        _require(E >= 1, "MoE weight table size")
         F, H = w1[0].shape
         src = w1[0].dtype
         for t, shp in [(t, (F, H)) for t in list(w1) + list(w3)] + [(t, (H, F)) for t in w2]:
@@ -73,13 +79,24 @@ class MoeWeights:
         self.compute_dtype = compute_dtype
         self.device = w1[0].device
         arr = ctypes.c_void_p * E
-        self._keep = (arr(*[t.data_ptr() for t in w1]), arr(*[t.data_ptr() for t in w3]),
-                      arr(*[t.data_ptr() for t in w2]))
+        self._keep = [arr(*[t.data_ptr() for t in w1]), arr(*[t.data_ptr() for t in w3]),
+                      arr(*[t.data_ptr() for t in w2])]
+        sc = [None, None, None]
+        if compute_dtype == FP8:
+            _require(scales is not None and len(scales) == 3, "fp8 weights need (s1, s2, s3) scale tables")
+            s1, s2, s3 = scales
+            for lst, n in ((s1, F), (s3, F), (s2, H)):
+                _require(len(lst) == E and all(t.dtype == torch.float32 and t.numel() == n and t.is_cuda
+                                               and t.is_contiguous() for t in lst), "MoE weight table size")
+            fa = ctypes.c_void_p * E
+            self._keep += [fa(*[t.data_ptr() for t in s1]), fa(*[t.data_ptr() for t in s3]),
+                           fa(*[t.data_ptr() for t in s2])]
+            sc = [ctypes.cast(k, ctypes.POINTER(ctypes.c_void_p)) for k in self._keep[3:]]
         desc = capi.WeightsDesc(E, H, F, _DTYPE_CODE[src], _DTYPE_CODE[compute_dtype],
                                 ctypes.cast(self._keep[0], ctypes.POINTER(ctypes.c_void_p)),
                                 ctypes.cast(self._keep[1], ctypes.POINTER(ctypes.c_void_p)),
                                 ctypes.cast(self._keep[2], ctypes.POINTER(ctypes.c_void_p)),
-                                None, None, None)
+                                sc[0], sc[1], sc[2])
         h = ctypes.c_uint64(0)
         with torch.cuda.device(self.device):
             _call(capi.lib().aps_moe_weights_register(ctypes.byref(desc), _stream(self.device), ctypes.byref(h)))
@@ -120,7 +137,7 @@ class MoeWeights:
             return ws[off:off + nbytes].view(dt).view(*shape)
 
         A = 2 * rows
-        return dict(
+        d = dict(
             logits=view(L.logits, rows * E, torch.float32, (rows, E)),
             routes=view(L.routes, A, torch.uint8, (rows, 2)),
             counts=view(L.counts, E, torch.int32, (E,)),
@@ -130,13 +147,22 @@ class MoeWeights:
             act=view(L.act, A * F, elt, (A, F)),
             y=view(L.y, A * H, elt, (A, H)),
         )
+        if self.compute_dtype == FP8:
+            kp = (F + 127) // 128 * 128
+            d.update(xq=view(L.xq, rows * H, torch.uint8, (rows, H)),
+                     x_scale=view(L.xq_scale, rows, torch.float32, (rows,)),
+                     actq=view(L.actq, A * kp, torch.uint8, (A, kp)),
+                     act_scale=view(L.act_scale, A, torch.float32, (A,)))
+        return d
 
 
 def register_moe_weights_gpu(w1: Sequence[torch.Tensor], w2: Sequence[torch.Tensor],
                              w3: Sequence[torch.Tensor],
-                             compute_dtype: torch.dtype = torch.bfloat16) -> MoeWeights:
-    """reference include/tensor.h:142-145 (argument order w1, w2, w3)."""
-    return MoeWeights(w1, w2, w3, compute_dtype)
+                             compute_dtype: torch.dtype = torch.bfloat16,
+                             scales: Optional[tuple] = None) -> MoeWeights:
+    """reference include/tensor.h:142-145 (argument order w1, w2, w3);
+    ``scales`` = (s1, s2, s3) per-channel tables for fp8 weights."""
+    return MoeWeights(w1, w2, w3, compute_dtype, scales)
 
 
 def matmul_transposed_gpu(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor) -> torch.Tensor:

@@ -61,9 +61,12 @@ typedef enum aps_dtype {
  *   APS_DTYPE_F32  - fp32 FMA-chain kernels, accumulation order identical to
  *                    the reference (k ascending), src_dtype must be F32;
  *   APS_DTYPE_BF16 - bf16 MFMA kernels, fp32 accumulate; src F32 or BF16;
- *   APS_DTYPE_E4M3 - fp8 MFMA kernels; src E4M3 with per-output-channel fp32
- *                    scales (w1_scale[e], w3_scale[e]: [ffn] device arrays,
- *                    w2_scale[e]: [hidden]).
+ *   APS_DTYPE_E4M3 - fp8 MFMA kernels; src E4M3 codes
+ *                    with per-output-channel fp32 scales (w1_scale[e],
+ *                    w3_scale[e]: [ffn] device arrays, w2_scale[e]:
+ *                    [hidden]); x (bf16) and the SwiGLU activations are
+ *                    quantised per row at run time, scale = amax / 448,
+ *                    round to nearest even; fused entry points only.
  * Registration copies the weights into the library's own packed layout
  * (the caller's buffers may be freed afterwards). */
 typedef struct aps_moe_weights_desc {
@@ -91,13 +94,15 @@ typedef struct aps_moe_ws_layout {
     size_t offsets;         /* u32 [E+1]                            */
     size_t assignment_rows; /* u32 [2*rows] position -> token       */
     size_t route_positions; /* u32 [2*rows] (token, slot) -> position */
-    size_t act;             /* [2*rows][ffn], compute dtype (f32 or bf16) */
-    size_t act_scale;       /* f32 [2*rows] (fp8 path only)         */
+    size_t act;             /* [2*rows][ffn], f32 (F32 path) or bf16 */
+    size_t act_scale;       /* fp8 path: f32 [2*rows] per-position scale */
     size_t y;               /* [2*rows][hidden], f32 (F32 path) or bf16 */
     size_t xq;              /* x in the compute dtype when the caller
                                passes another one: bf16 [rows][hidden]
                                (bf16 weights, fp32 x), e4m3 (fp8 path) */
-    size_t xq_scale;        /* fp8 path: f32 [rows]                 */
+    size_t xq_scale;        /* fp8 path: f32 [rows] per-token scale */
+    size_t actq;            /* fp8 path: e4m3 act [2*rows][ffn rounded
+                               up to 128], zero padded              */
 } aps_moe_ws_layout;
 
 /* ---- weights ----------------------------------------------------------- */

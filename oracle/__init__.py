@@ -54,6 +54,7 @@ def lib():
                                          _f32p, ctypes.c_void_p, ctypes.c_void_p]
         L.oracle_bf16_to_f32.argtypes = [_u16p, _f32p, _i64]
         L.oracle_e4m3_to_f32.argtypes = [_u8p, _f32p, _i64]
+        L.oracle_quantise_rows_e4m3.argtypes = [_f32p, _i64, _i32, _u8p, _f32p]
         L.oracle_default_quantum.restype = ctypes.c_float
         L.oracle_default_tie_eps.restype = ctypes.c_float
         L.oracle_num_threads.restype = ctypes.c_int
@@ -170,6 +171,49 @@ def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
     out = np.empty(codes.shape, np.float32)
     lib().oracle_e4m3_to_f32(codes.reshape(-1), out.reshape(-1), codes.size)
     return out
+
+
+def round_to_bf16(v: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bfloat16 value (ties to even), as float32; finite
+    inputs."""
+    u = np.ascontiguousarray(v, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+def quantise_rows_e4m3(rows: np.ndarray):
+    """Per-row e4m3: (codes uint8, scale float32 per row); scale = amax/448."""
+    rows = _c(rows, np.float32)
+    r, n = rows.shape
+    codes = np.empty((r, n), np.uint8)
+    scale = np.empty(r, np.float32)
+    lib().oracle_quantise_rows_e4m3(rows, r, n, codes, scale)
+    return codes, scale
+
+
+def dequantise_rows_e4m3(codes: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    return (e4m3_to_f32(codes) * np.asarray(scale, np.float32)[:, None]).astype(np.float32)
+
+
+def fp8_ffn_rows(x_rows: np.ndarray, experts: np.ndarray, w1, w3, w2):
+    """The fp8 path's expert FFN for n (row, expert) pairs (BASELINE C5):
+    x rows quantised per row to e4m3, the dequantised values through the
+    gate/up GEMMs and SiLU (fp32), the activations rounded to bf16 and
+    quantised per row to e4m3, then the w2 GEMM on their dequantised values.
+    w1/w3/w2 are the dequantised weights (codes x per-channel scales).
+    Returns (y [n, H] float32, act_bf16 [n, F] float32)."""
+    xq, xs = quantise_rows_e4m3(x_rows)
+    xh = dequantise_rows_e4m3(xq, xs)
+    _, act = ffn_rows(xh, experts, w1, w3, w2, want_act=True)
+    act_b = round_to_bf16(act)
+    aq, as_ = quantise_rows_e4m3(act_b)
+    ah = dequantise_rows_e4m3(aq, as_).astype(np.float64)
+    w2 = np.asarray(w2, np.float32)
+    y = np.empty((x_rows.shape[0], w2.shape[1]), np.float32)
+    for e in np.unique(experts):
+        idx = np.where(experts == e)[0]
+        y[idx] = (ah[idx] @ w2[e].astype(np.float64).T).astype(np.float32)
+    return y, act_b
 
 
 def reference_path(x, gate, w1, w3, w2):

@@ -387,3 +387,46 @@ ORACLE_API void oracle_e4m3_to_f32(const uint8_t* src, float* dst, int64_t n) {
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) dst[i] = e4m3_to_f32(src[i]);
 }
+
+/* e4m3 code of a finite float: the nearest of the 253 finite e4m3 values,
+ * ties to the even code (even mantissa), saturating at +-448.  Written from
+ * the format definition: between 2^e and 2^(e+1) (e >= -6) the spacing is
+ * 2^(e-3); below 2^-6 it is 2^-9. */
+static uint8_t f32_to_e4m3(float v) {
+    const uint8_t sign = signbit(v) ? 0x80 : 0x00;
+    double a = fabs((double)v);
+    if (a > 448.0) a = 448.0;
+    int e;
+    (void)frexp(a, &e);                    /* a = f * 2^e, f in [0.5, 1) */
+    int ue = e - 1;                        /* a in [2^ue, 2^(ue+1)) */
+    if (ue < -6) ue = -6;
+    const double step = ldexp(1.0, ue - 3);
+    double q = nearbyint(a / step) * step; /* current rounding mode: to nearest even */
+    if (q > 448.0) q = 448.0;
+    if (q < ldexp(1.0, -6)) return (uint8_t)(sign | (uint8_t)nearbyint(q / ldexp(1.0, -9)));
+    int qe;
+    (void)frexp(q, &qe);
+    qe -= 1;
+    const int mant = (int)nearbyint(q / ldexp(1.0, qe) * 8.0) - 8;
+    return (uint8_t)(sign | ((qe + 7) << 3) | mant);
+}
+
+/* Per-row e4m3 quantisation of rows x n (the fp8 path's activation format):
+ * scale[r] = fp32(amax / 448) (1 if the row is zero), codes = e4m3(fp32(v /
+ * scale)), each division rounded to fp32 first. */
+ORACLE_API void oracle_quantise_rows_e4m3(const float* src, int64_t rows, int32_t n, uint8_t* codes,
+                                          float* scale) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* row = src + r * n;
+        float amax = 0.0f;
+        for (int32_t k = 0; k < n; ++k) amax = fmaxf(amax, fabsf(row[k]));
+        volatile float sc = amax / 448.0f;
+        float s = sc > 0.0f ? sc : 1.0f;
+        scale[r] = s;
+        for (int32_t k = 0; k < n; ++k) {
+            volatile float q = row[k] / s;
+            codes[r * n + k] = f32_to_e4m3(q);
+        }
+    }
+}

@@ -12,7 +12,9 @@ fails it, without restating the oracle's own formula:
   combine       : closed form RN((a + b) / 2), slot-order independence
   whole block   : the reference CPU-path order (zero-init scatter-add per
                   expert) equals the staged GPU-path order bit for bit
-  encodings     : bf16 / fp8 e4m3 against the format definitions
+  encodings     : bf16 / fp8 e4m3 against the format definitions; the
+                  per-row e4m3 quantiser against exhaustive nearest-code
+                  search; the fp8 FFN against an fp64 textbook pipeline
 """
 import json
 import math
@@ -278,3 +280,55 @@ def test_bf16_round_trip_and_rounding():
         e = math.floor(math.log2(abs(v)))
         assert abs(r - v) <= 2.0 ** (e - 8)                 # half a bf16 ulp
     np.testing.assert_array_equal(oracle.bf16_to_f32(b), synth.bf16_bits_to_f32(b))
+
+
+# ---- fp8 path (config C5) ------------------------------------------------------
+
+def test_quantise_rows_e4m3_is_nearest_code_and_scale_rule():
+    table = oracle.e4m3_to_f32(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    finite = ~np.isnan(table)
+    rng = np.random.default_rng(21)
+    rows = rng.standard_normal((6, 200)).astype(np.float32) * np.float32(3.0)
+    rows[1] = 0.0                                            # zero row -> scale 1, codes 0
+    rows[2, :5] = [448.0, -448.0, 1e-7, -1e-7, 0.0]          # saturation and subnormal ends
+    codes, scale = oracle.quantise_rows_e4m3(rows)
+    amax = np.abs(rows).max(1)
+    want_scale = np.where(amax > 0, (amax / np.float32(448)).astype(np.float32), np.float32(1))
+    np.testing.assert_array_equal(scale, want_scale)
+    assert np.all(codes[1] == 0) and scale[1] == 1.0
+    q = (rows / scale[:, None]).astype(np.float32).astype(np.float64)   # fp32 division, as specified
+    d = np.abs(table[finite][None, :] - q.reshape(-1)[:, None])
+    best = d.min(1)
+    got = table[codes.reshape(-1)]
+    assert np.all(np.abs(got - q.reshape(-1)) == best)                 # nearest representable
+    ties = (np.sum(d == best[:, None], 1) > 1) & (best > 0)
+    assert np.all((codes.reshape(-1)[ties] & 1) == 0)                    # ties to the even code
+    np.testing.assert_array_equal(codes, synth.quantise_rows_e4m3(rows)[0])
+
+
+def test_round_to_bf16_matches_the_bf16_encoder():
+    v = np.random.default_rng(5).standard_normal(4096).astype(np.float32)
+    np.testing.assert_array_equal(oracle.round_to_bf16(v), synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(v)))
+
+
+def test_fp8_ffn_matches_fp64_textbook_pipeline():
+    rng = np.random.default_rng(9)
+    n, H, F, E = 12, 128, 64, 3
+    x = rng.standard_normal((n, H)).astype(np.float32)
+    w = {nm: rng.standard_normal(shp).astype(np.float32) * np.float32(0.05)
+         for nm, shp in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F)))}
+    ex = rng.integers(0, E, n).astype(np.int32)
+    y, act_b = oracle.fp8_ffn_rows(x, ex, w["w1"], w["w3"], w["w2"])
+    # textbook: quantise x per row, fp64 GEMMs and SiLU, bf16-round, quantise, fp64 GEMM
+    xq, xs = synth.quantise_rows_e4m3(x)[:2]
+    xh = synth.e4m3_bits_to_f32(xq).astype(np.float64) * xs[:, None]
+    g = np.einsum("nh,nfh->nf", xh, w["w1"][ex].astype(np.float64))
+    u = np.einsum("nh,nfh->nf", xh, w["w3"][ex].astype(np.float64))
+    a = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+    a = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(a))
+    aq, as_ = synth.quantise_rows_e4m3(a)[:2]
+    ah = synth.e4m3_bits_to_f32(aq).astype(np.float64) * as_[:, None]
+    yt = np.einsum("nf,nhf->nh", ah, w["w2"][ex].astype(np.float64))
+    err = np.linalg.norm(y - yt, axis=1) / np.linalg.norm(yt, axis=1)
+    assert err.max() < 2e-2, err.max()
+    assert np.abs(act_b - a).max() <= np.abs(a).max() * 2.0 ** -7
