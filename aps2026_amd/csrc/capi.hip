@@ -430,6 +430,57 @@ int aps_moe_ffn_down(uint64_t handle, const void* act, const float* act_scale, i
     return run_ffn_down(*w, act, rows, offsets, y_perm, static_cast<hipStream_t>(stream));
 }
 
+int aps_quantise_rows_e4m3(const void* src, int64_t src_stride, int32_t n, uint8_t* dst, int64_t dst_stride,
+                           float* scale, int64_t rows, void* stream) {
+    if (rows < 0 || n <= 0 || n % 8 != 0 || dst_stride < n || dst_stride % 8 != 0 || dst_stride > 8192 ||
+        src_stride < n || src_stride % 8 != 0)
+        return fail(APS_ERR_SHAPE, "quantise_rows_e4m3: rows %lld n %d strides %lld/%lld", (long long)rows, n,
+                    (long long)src_stride, (long long)dst_stride);
+    if (rows > 0 && (!src || !dst || !scale)) return fail(APS_ERR_ARG, "quantise_rows_e4m3: NULL pointer");
+    if (rows > 0 && (reinterpret_cast<uintptr_t>(src) & 15u))
+        return fail(APS_ERR_ARG, "quantise_rows_e4m3: src must be 16-byte aligned");
+    APS_HIP(aps::launch_quant_rows_e4m3(static_cast<const aps::bf16_t*>(src), src_stride, n, dst, dst_stride, scale,
+                                        rows, static_cast<hipStream_t>(stream)),
+            "quantise_rows_e4m3 launch");
+    return APS_OK;
+}
+
+static int fp8_set(uint64_t handle, const WeightSet** out, const char* what) {
+    const WeightSet* w = lookup(handle);
+    if (!w) return fail(APS_ERR_HANDLE, "grouped MoE shape or handle: invalid handle %llu",
+                        (unsigned long long)handle);
+    if (int rc = check_device(*w)) return rc;
+    if (w->compute != APS_DTYPE_E4M3) return fail(APS_ERR_DTYPE, "%s: weight set is not fp8", what);
+    *out = w;
+    return APS_OK;
+}
+
+int aps_moe_ffn_up_fp8(uint64_t handle, const uint8_t* xq, const float* x_scale, int64_t rows,
+                       const uint32_t* offsets, const uint32_t* assignment_rows, void* act, void* stream) {
+    const WeightSet* w = nullptr;
+    if (int rc = fp8_set(handle, &w, "ffn_up_fp8")) return rc;
+    if (rows < 0) return fail(APS_ERR_SHAPE, "ffn_up_fp8: rows %lld", (long long)rows);
+    if (rows > 0 && (!xq || !x_scale || !offsets || !assignment_rows || !act))
+        return fail(APS_ERR_ARG, "ffn_up_fp8: NULL pointer");
+    APS_HIP(aps::launch_ffn_up_fp8(xq, x_scale, offsets, assignment_rows, w->q13, w->s1, w->s3,
+                                   static_cast<aps::bf16_t*>(act), rows, w->H, w->F, w->E,
+                                   static_cast<hipStream_t>(stream)),
+            "ffn_up_fp8 launch");
+    return APS_OK;
+}
+
+int aps_moe_ffn_down_fp8(uint64_t handle, const uint8_t* actq, const float* act_scale, int64_t rows,
+                         const uint32_t* offsets, void* y_perm, void* stream) {
+    const WeightSet* w = nullptr;
+    if (int rc = fp8_set(handle, &w, "ffn_down_fp8")) return rc;
+    if (rows < 0) return fail(APS_ERR_SHAPE, "ffn_down_fp8: rows %lld", (long long)rows);
+    if (rows > 0 && (!actq || !act_scale || !offsets || !y_perm)) return fail(APS_ERR_ARG, "ffn_down_fp8: NULL pointer");
+    APS_HIP(aps::launch_ffn_down_fp8(actq, act_scale, offsets, w->q2, w->s2, static_cast<aps::bf16_t*>(y_perm),
+                                     rows, w->H, w->F, w->E, static_cast<hipStream_t>(stream)),
+            "ffn_down_fp8 launch");
+    return APS_OK;
+}
+
 int aps_moe_combine(const void* y_perm, int32_t y_dtype, const uint32_t* route_positions,
                     int64_t rows, int32_t hidden, void* out, int32_t out_dtype, void* stream) {
     if (rows < 0 || hidden <= 0 || hidden % 8 != 0)

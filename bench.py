@@ -33,6 +33,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "MoE-block prefill tokens/s + grouped-GEMM % MFMA peak, 4096 tok, 1 GPU"
 PEAK_BF16 = 2.5e15       # MI355X dense bf16 MFMA, FLOP/s
+PEAK_FP8 = 5.0e15        # MI355X dense fp8 MFMA, FLOP/s
 PEAK_F32 = 157.3e12
 PEAK_HBM = 8.0e12        # bytes/s
 LAYERS = 4
@@ -43,7 +44,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5"])
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--cpu-runs", type=int, default=3)
     return ap.parse_args()
@@ -63,7 +64,8 @@ def main():
     inp = synth.make_config(args.config)
     T, H, E, F = inp.T, inp.H, inp.E, inp.F
     A = 2 * T
-    bf16 = inp.dtype == "bf16"
+    fp8 = inp.dtype == "fp8"
+    bf16 = inp.dtype in ("bf16", "fp8")        # x and outputs are bf16 on both MFMA paths
     tdt = torch.bfloat16 if bf16 else torch.float32
 
     def dev_bits(bits):
@@ -71,19 +73,27 @@ def main():
 
     if bf16:
         x = dev_bits(inp.packed["x_bf16"])
-        host_w = {nm: inp.packed[nm + "_bf16"] for nm in ("w1", "w2", "w3")}
     else:
         x = torch.from_numpy(inp.x).to(dev)
-        host_w = {nm: getattr(inp, nm) for nm in ("w1", "w2", "w3")}
     gate = torch.from_numpy(inp.gate).to(dev)
     layers = []
     for _ in range(LAYERS):
-        lists = []
+        lists, scales = [], []
         for nm in ("w1", "w2", "w3"):
-            d = dev_bits(host_w[nm]) if bf16 else torch.from_numpy(host_w[nm]).to(dev)
+            if fp8:
+                d = torch.from_numpy(inp.packed[nm + "_e4m3"]).to(dev)
+                sc = torch.from_numpy(inp.packed[nm + "_scale"]).to(dev)
+                scales.append([sc[e].contiguous() for e in range(E)])
+            elif bf16:
+                d = dev_bits(inp.packed[nm + "_bf16"])
+            else:
+                d = torch.from_numpy(getattr(inp, nm)).to(dev)
             lists.append([d[e].contiguous() for e in range(E)])
-        layers.append(moe.register_moe_weights_gpu(*lists, compute_dtype=tdt))
-        del lists
+        if fp8:
+            layers.append(moe.register_moe_weights_gpu(*lists, compute_dtype=moe.FP8, scales=tuple(scales)))
+        else:
+            layers.append(moe.register_moe_weights_gpu(*lists, compute_dtype=tdt))
+        del lists, scales
     torch.cuda.synchronize()
 
     L = capi.lib()
@@ -126,7 +136,16 @@ def main():
     scratch = torch.empty(max(L.aps_moe_dispatch_workspace_size(T, E), 1), dtype=torch.uint8, device=dev)
     act = torch.empty((A, F), dtype=tdt, device=dev)
     y = torch.empty((A, H), dtype=tdt, device=dev)
-    stages = ["router_logits", "route_top2", "dispatch", "ffn_up", "ffn_down", "combine"]
+    if fp8:
+        kp = (F + 127) // 128 * 128
+        xq = torch.empty((T, H), dtype=torch.uint8, device=dev)
+        xs = torch.empty(T, dtype=torch.float32, device=dev)
+        actq = torch.empty((A, kp), dtype=torch.uint8, device=dev)
+        acts = torch.empty(A, dtype=torch.float32, device=dev)
+        stages = ["router_logits", "route_top2", "dispatch", "quant_x", "ffn_up", "quant_act", "ffn_down",
+                  "combine"]
+    else:
+        stages = ["router_logits", "route_top2", "dispatch", "ffn_up", "ffn_down", "combine"]
     times = {s: [] for s in stages}
     n_stage = max(args.steps, 10)
     for i in range(n_stage + 2):
@@ -138,10 +157,20 @@ def main():
             lambda: L.aps_moe_route_top2(p(logits), T, E, p(routes), sptr),
             lambda: L.aps_moe_dispatch(p(routes), T, E, p(counts), p(offsets), p(arows), p(rpos), p(scratch),
                                        scratch.numel(), sptr),
-            lambda: L.aps_moe_ffn_up(w.handle, p(x), xd, T, p(offsets), p(arows), p(act), None, sptr),
-            lambda: L.aps_moe_ffn_down(w.handle, p(act), None, T, p(offsets), p(y), sptr),
-            lambda: L.aps_moe_combine(p(y), xd, p(rpos), T, H, p(out), xd, sptr),
         ]
+        if fp8:
+            calls += [
+                lambda: L.aps_quantise_rows_e4m3(p(x), H, H, p(xq), H, p(xs), T, sptr),
+                lambda: L.aps_moe_ffn_up_fp8(w.handle, p(xq), p(xs), T, p(offsets), p(arows), p(act), sptr),
+                lambda: L.aps_quantise_rows_e4m3(p(act), F, F, p(actq), kp, p(acts), A, sptr),
+                lambda: L.aps_moe_ffn_down_fp8(w.handle, p(actq), p(acts), T, p(offsets), p(y), sptr),
+            ]
+        else:
+            calls += [
+                lambda: L.aps_moe_ffn_up(w.handle, p(x), xd, T, p(offsets), p(arows), p(act), None, sptr),
+                lambda: L.aps_moe_ffn_down(w.handle, p(act), None, T, p(offsets), p(y), sptr),
+            ]
+        calls.append(lambda: L.aps_moe_combine(p(y), xd, p(rpos), T, H, p(out), xd, sptr))
         for k, c in enumerate(calls):
             rc = c()
             if rc:
@@ -156,7 +185,7 @@ def main():
     esz = 2 if bf16 else 4
     flops_up = 4.0 * A * H * F
     flops_down = 2.0 * A * F * H
-    peak = PEAK_BF16 if bf16 else PEAK_F32
+    peak = PEAK_FP8 if fp8 else (PEAK_BF16 if bf16 else PEAK_F32)
     bytes_router = T * H * esz + E * H * 4 + T * E * 4
     bytes_combine = A * H * esz + T * H * esz + A * 4
     stage_report = {
@@ -167,10 +196,13 @@ def main():
         "ffn_up": {"us": mean_t["ffn_up"] * 1e6, "TFLOP_s": flops_up / mean_t["ffn_up"] / 1e12},
         "ffn_down": {"us": mean_t["ffn_down"] * 1e6, "TFLOP_s": flops_down / mean_t["ffn_down"] / 1e12},
         "combine": {"us": mean_t["combine"] * 1e6, "GB_s": bytes_combine / mean_t["combine"] / 1e9},
+        **({"quant_x": {"us": mean_t["quant_x"] * 1e6}, "quant_act": {"us": mean_t["quant_act"] * 1e6}}
+           if fp8 else {}),
         "grouped_gemm_total_TFLOP_s": (flops_up + flops_down) / (mean_t["ffn_up"] + mean_t["ffn_down"]) / 1e12,
     }
     achieved = flops_up / mean_t["ffn_up"]
-    roofline = {"bound": "mfma", "kernel": "k_ffn_up_bf16" if bf16 else "k_ffn_up_f32",
+    kname = "k_ffn_up<Fp8Fmt>" if fp8 else ("k_ffn_up<Bf16Fmt>" if bf16 else "k_ffn_up_f32")
+    roofline = {"bound": "mfma", "kernel": kname,
                 "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
                 "frac": achieved / peak, "traffic": None,
                 "flops_per_launch": flops_up, "launch_us": mean_t["ffn_up"] * 1e6}
@@ -195,7 +227,7 @@ def main():
         "metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16" if bf16 else "f32", "data": "synthetic (seeded PCG64 normals, random-init weights)",
+        "dtype": "fp8" if fp8 else ("bf16" if bf16 else "f32"), "data": "synthetic (seeded PCG64 normals, random-init weights)",
         "config": {"workload": f"{args.config}: MoE FFN block, {T} tokens, hidden {H}, {E} experts top-2, "
                                f"ffn {F}, {inp.dtype}" + (", Zipf(1.1) expert loads" if inp.zipf else ""),
                    "tokens": T, "hidden": H, "experts": E, "ffn": F, "layers_rotated": LAYERS},

@@ -179,6 +179,29 @@ APS_API int aps_moe_ffn_down(uint64_t handle, const void* act, const float* act_
                              int64_t rows, const uint32_t* offsets, void* y_perm,
                              void* stream);
 
+/* ---- fp8 stages (no reference counterpart) --------- */
+
+/* Per-row e4m3 quantisation: scale[r] = amax(|src[r]|) / 448 (1 for a zero
+ * row), dst[r][k] = e4m3(src[r][k] / scale[r]) rounded to nearest even and
+ * saturating, for k < n; zero for n <= k < dst_stride.  src bf16 rows with
+ * stride src_stride (elements, 16-byte aligned rows); n and dst_stride
+ * multiples of 8, dst_stride <= 8192. */
+APS_API int aps_quantise_rows_e4m3(const void* src, int64_t src_stride, int32_t n, uint8_t* dst,
+                                   int64_t dst_stride, float* scale, int64_t rows, void* stream);
+
+/* The fp8 set's w1||w3 GEMM: act[p] (bf16 [2*rows][ffn]) = silu(g) * u with
+ * g = (xq[t] . w1q[e]) * x_scale[t] * w1_scale[e], u likewise (xq: e4m3
+ * [rows][hidden] from aps_quantise_rows_e4m3). */
+APS_API int aps_moe_ffn_up_fp8(uint64_t handle, const uint8_t* xq, const float* x_scale, int64_t rows,
+                               const uint32_t* offsets, const uint32_t* assignment_rows, void* act,
+                               void* stream);
+
+/* The fp8 set's w2 GEMM: y_perm[p] (bf16 [2*rows][hidden]) =
+ * (actq[p] . w2q[e]) * act_scale[p] * w2_scale[e]; actq: e4m3 [2*rows][ffn
+ * rounded up to 128], zero padded (aps_quantise_rows_e4m3 of act). */
+APS_API int aps_moe_ffn_down_fp8(uint64_t handle, const uint8_t* actq, const float* act_scale, int64_t rows,
+                                 const uint32_t* offsets, void* y_perm, void* stream);
+
 /* Weighted combine (reference k_moe_combine, src/tensor.cu:1968-1988):
  * out[t] = 0.5 * y_perm[route_positions[2t]] + 0.5 * y_perm[route_positions[2t+1]],
  * summed in fp32, rounded once to out_dtype (F32 or BF16). */
