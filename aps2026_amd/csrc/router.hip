@@ -7,156 +7,256 @@
 // the chain order is fixed: no split-K, no tree reduction over k.
 //
 // gfx950 mapping.  The parallelism is T*E independent chains of length H.
-// One lane owns one chain: a wavefront is 64 tokens x 1 expert.
-//  * x: the 64 x 256 tile is staged once per workgroup in LDS as fp32 and
-//    each lane reads its own row with ds_read_b128 (row pitch 260 floats:
-//    the 16 lanes of an LDS phase land on 16 distinct 4-bank groups).
-//  * gate: the value of step k is the same for the whole wave, so the
-//    block's 4 x 256 gate chunk is staged in LDS beside x and every lane
-//    reads it with the same address (an LDS broadcast).  Keeping both
-//    operands in LDS puts all operand reads under the in-order LDS counter:
-//    the reads of the next 16 steps are issued before the current 16 FMAs
-//    (explicit ping-pong).  Scalar gate loads would return out of order and
-//    force a full lgkmcnt wait at every prefetch.
-//  * The chain is one dependent v_fmac_f32 per step; on gfx950 that issues
-//    about every 9 cycles, which bounds this kernel at T = 4096 (one chain
-//    per lane, one wave per SIMD).
-// Four waves (four experts) share an x tile; the grid is [token tiles] x
-// [E/4], and with tiles % 8 == 0 the four expert groups of a tile land on one
-// XCD (blocks are dealt round-robin over the 8 XCDs), so x is fetched from
-// HBM once per XCD L2.  The next 256-wide chunk of x and gate is
-// prefetched into registers while the current one is consumed.
+// One lane owns one chain: a wavefront is 64 tokens x 1 expert, a workgroup
+// 64 tokens x 4 experts (four waves sharing the x tile), grid [token tiles] x
+// [E/4].  At T = 4096, E = 16 that is one wave per SIMD, so the time is the
+// length of one dependent chain.  Measured on gfx950 (cycles per step):
+// dependent v_fmac_f32_dpp alone 6.1; with the bf16 -> fp32 conversion
+// interleaved 9.2; with the LDS operand reads 10.8; with the ring barrier
+// 12.4.  The design keeps everything else off the chain:
+//  * x streams into a two-slot LDS ring straight from global memory
+//    (global_load_lds_dwordx4; no VGPR staging, no conversion pass).  A slot
+//    holds 512 bytes of each of the 64 token rows, in 16-byte pieces XOR-
+//    swizzled by row so that the 16 lanes of an LDS phase, each reading its
+//    own row, hit 16 distinct 4-bank groups.  The copy of chunk c+1 is in
+//    flight while chunk c (256 bf16 steps, ~1 us) is consumed.
+//  * The gate chunk of the block's 4 experts rides in the same slot.  Lane
+//    j of every 16-lane row reads gate value j of a 16-step group, and the
+//    FMA takes it through DPP row_newbcast:j, which hands lane j's value to
+//    the whole row: a broadcast that costs no LDS bandwidth and no scalar-
+//    cache latency (scalar gate loads miss the scalar cache once per 64 B
+//    and stall the chain on L2 latency).
+//  * bf16 -> fp32 is exact (a shift or a mask).  The chain is one asm
+//    stream in which the conversion for step j+2 sits behind the FMA of
+//    step j; the FMA is v_fmac_f32_dpp(acc, gate_k, x_k), k ascending, as in
+//    the reference (the product is commutative, so operand order does not
+//    change a bit).
+//  * Operand reads for block b+1 (32 steps) are issued before block b's
+//    FMAs; the ring barrier for chunk c sits at the last block of chunk c-1,
+//    so the first reads of a chunk are also issued ahead.
+//  * 72 KB of LDS per workgroup: two workgroups per CU (two chains per SIMD
+//    once T*E exceeds 64 chains per SIMD, T > 4096 at E = 16).
+// With tiles % 8 == 0 the expert groups of a token tile land on one XCD
+// (workgroups are dealt round-robin over the 8 XCDs), so x is fetched from
+// HBM once per XCD L2.
 #include "common.hpp"
 
 namespace aps {
 namespace {
 
-constexpr int kRouterKC = 256;              // k per LDS chunk
-constexpr int kRouterPitch = kRouterKC + 4; // floats per LDS row
+constexpr int kRouterRowBytes = 512;        // bytes of one token row per chunk
+constexpr int kRouterSlots = 2;             // LDS ring depth (chunks)
+static_assert(kRouterSlots >= 2 && kRouterSlots <= 4, "chunk_ready() waits for at most two later chunks");
+constexpr int kRouterPieces = kRouterRowBytes / 16;          // 16-byte pieces per row
+constexpr int kRouterRowsPerCopy = kWave / kRouterPieces;    // rows per 1 KB copy
+constexpr int kRouterXCopies = kRouterPieces / 4;            // x copies per wave per chunk
 constexpr int kRouterExpertsPerBlock = 4;   // one wave per expert
+constexpr int kRouterBlk = 32;              // chain steps per register block
 
-// Loads one 64 x 256 chunk of x into registers, 4 consecutive k per piece:
-// 4096 pieces, 16 per thread, piece p = row p / 64, columns 4 * (p % 64).
-// Sixteen consecutive lanes therefore store 256 contiguous LDS bytes (one
-// float4 each), which covers the 64 banks once: conflict-free.
+typedef uint32_t ru32x4_t __attribute__((ext_vector_type(4)));
+
+#define APS_RGP(p) ((const __attribute__((address_space(1))) void*)(p))
+#define APS_RLP(p) ((__attribute__((address_space(3))) void*)(p))
+
 template <bool XBF16>
-struct XStage;
-
-template <>
-struct XStage<true> {
-    static constexpr int kPieces = 16;
-    uint2 v[kPieces];
-    __device__ void load(const bf16_t* x, int64_t row0, int64_t rows, int H, int k0) {
-#pragma unroll
-        for (int j = 0; j < kPieces; ++j) {
-            const int p = threadIdx.x + j * 256;
-            const int64_t row = row0 + (p >> 6);
-            v[j] = row < rows ? *reinterpret_cast<const uint2*>(x + row * H + k0 + (p & 63) * 4)
-                              : make_uint2(0, 0);
-        }
-    }
-    __device__ void store(float* xs) const {
-#pragma unroll
-        for (int j = 0; j < kPieces; ++j) {
-            const int p = threadIdx.x + j * 256;
-            *reinterpret_cast<float4*>(xs + (p >> 6) * kRouterPitch + (p & 63) * 4) =
-                make_float4(__uint_as_float(v[j].x << 16), __uint_as_float(v[j].x & 0xffff0000u),
-                            __uint_as_float(v[j].y << 16), __uint_as_float(v[j].y & 0xffff0000u));
-        }
-    }
+struct RFmt {
+    static constexpr int kElt = XBF16 ? 2 : 4;
+    static constexpr int kK = kRouterRowBytes / kElt;                 // k per chunk (256 / 128)
+    static constexpr int kBpc = kK / kRouterBlk;                      // blocks per chunk (8 / 4)
+    static constexpr int kPieces = kRouterBlk * kElt / 16;            // 16-B x pieces per block (4 / 8)
+    static constexpr int kXBytes = kWave * kRouterRowBytes;           // 32 KB
+    static constexpr int kGBytes = kRouterExpertsPerBlock * kK * 4;   // 4 KB / 2 KB
+    static constexpr int kSlotBytes = kXBytes + kGBytes;
+    static constexpr int kGateDma = kK / kWave;                       // dword copies per wave (4 / 2)
+    static constexpr int kDma = kRouterXCopies + kGateDma;            // copies per wave per chunk
 };
 
-template <>
-struct XStage<false> {
-    static constexpr int kPieces = 16;
-    float4 v[kPieces];
-    __device__ void load(const float* x, int64_t row0, int64_t rows, int H, int k0) {
-#pragma unroll
-        for (int j = 0; j < kPieces; ++j) {
-            const int p = threadIdx.x + j * 256;
-            const int64_t row = row0 + (p >> 6);
-            v[j] = row < rows ? *reinterpret_cast<const float4*>(x + row * H + k0 + (p & 63) * 4)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
-    __device__ void store(float* xs) const {
-#pragma unroll
-        for (int j = 0; j < kPieces; ++j) {
-            const int p = threadIdx.x + j * 256;
-            *reinterpret_cast<float4*>(xs + (p >> 6) * kRouterPitch + (p & 63) * 4) = v[j];
-        }
-    }
-};
+// LDS byte offset of 16-byte piece c of token row r (0..63).
+__device__ inline int rpos(int r, int c) { return r * kRouterRowBytes + ((c ^ (r & 15)) << 4); }
 
-// 16 chain steps acc = fma(x_k, g_k, acc), k ascending, one fused
-// multiply-add each (v_fmac_f32); g comes from a wave-uniform LDS broadcast.
-__device__ inline float fma16(float acc, const float4 (&x)[4], const float4 (&g)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        acc = __builtin_fmaf(x[i].x, g[i].x, acc);
-        acc = __builtin_fmaf(x[i].y, g[i].y, acc);
-        acc = __builtin_fmaf(x[i].z, g[i].z, acc);
-        acc = __builtin_fmaf(x[i].w, g[i].w, acc);
-    }
+__device__ inline void r_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14)); }
+template <int N>
+__device__ inline void r_wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+__device__ inline void r_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// ---- the chain: 32 steps per asm block --------------------------------------
+// %0 acc; bf16: %1..%4 temporaries, %5 / %6 gate groups (steps 0-15 / 16-31),
+// %7..%22 the 16 words of bf16 pairs.  Step 2i takes the low half of word i
+// (shift), step 2i+1 the high half (mask).
+#define APS_STR_(x) #x
+#define APS_STR(x) APS_STR_(x)
+#define APS_F(T, G, J) "v_fmac_f32_dpp %0, " G ", " T " row_newbcast:" APS_STR(J) " row_mask:0xf bank_mask:0xf\n\t"
+#define APS_LO(T, W) "v_lshlrev_b32 " T ", 16, " W "\n\t"
+#define APS_HI(T, W) "v_and_b32 " T ", 0xffff0000, " W "\n\t"
+// Steps 4q .. 4q+3 (words W0 = 2q, in %1 / %2, and W1 = 2q+1) and the
+// conversion of the next word WN into %1 / %2.
+#define APS_QUAD(G, J, W1, WN)                                                          \
+    APS_F("%1", G, J) APS_LO("%3", W1) APS_F("%2", G, J##_1) APS_HI("%4", W1)           \
+    APS_F("%3", G, J##_2) APS_LO("%1", WN) APS_F("%4", G, J##_3) APS_HI("%2", WN)
+#define APS_QUAD_LAST(G, J, W1)                                                         \
+    APS_F("%1", G, J) APS_LO("%3", W1) APS_F("%2", G, J##_1) APS_HI("%4", W1)           \
+    APS_F("%3", G, J##_2) APS_F("%4", G, J##_3)
+// DPP lane numbers of the four steps of each quad
+#define APS_J0 0
+#define APS_J0_1 1
+#define APS_J0_2 2
+#define APS_J0_3 3
+#define APS_J4 4
+#define APS_J4_1 5
+#define APS_J4_2 6
+#define APS_J4_3 7
+#define APS_J8 8
+#define APS_J8_1 9
+#define APS_J8_2 10
+#define APS_J8_3 11
+#define APS_J12 12
+#define APS_J12_1 13
+#define APS_J12_2 14
+#define APS_J12_3 15
+
+__device__ inline float chain32(float acc, float g0, float g1, const ru32x4_t (&xp)[4]) {
+    float t0, t1, t2, t3;
+    asm volatile(
+        "s_nop 1\n\t"  // DPP source written by a VALU copy needs two wait states
+        APS_LO("%1", "%7") APS_HI("%2", "%7")
+        APS_QUAD("%5", APS_J0, "%8", "%9") APS_QUAD("%5", APS_J4, "%10", "%11")
+        APS_QUAD("%5", APS_J8, "%12", "%13") APS_QUAD("%5", APS_J12, "%14", "%15")
+        APS_QUAD("%6", APS_J0, "%16", "%17") APS_QUAD("%6", APS_J4, "%18", "%19")
+        APS_QUAD("%6", APS_J8, "%20", "%21") APS_QUAD_LAST("%6", APS_J12, "%22")
+        : "+v"(acc), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+        : "v"(g0), "v"(g1),
+          "v"(xp[0][0]), "v"(xp[0][1]), "v"(xp[0][2]), "v"(xp[0][3]),
+          "v"(xp[1][0]), "v"(xp[1][1]), "v"(xp[1][2]), "v"(xp[1][3]),
+          "v"(xp[2][0]), "v"(xp[2][1]), "v"(xp[2][2]), "v"(xp[2][3]),
+          "v"(xp[3][0]), "v"(xp[3][1]), "v"(xp[3][2]), "v"(xp[3][3]));
     return acc;
+}
+
+// fp32 x: 16 steps, %0 acc, %1 gate group, %2..%17 the x values.
+#define APS_F4(J, A, B, C, D) APS_F(A, "%1", J) APS_F(B, "%1", J##_1) APS_F(C, "%1", J##_2) APS_F(D, "%1", J##_3)
+__device__ inline float chain16_f32(float acc, float g, const ru32x4_t& a, const ru32x4_t& b,
+                                    const ru32x4_t& c, const ru32x4_t& d) {
+    asm volatile(
+        "s_nop 1\n\t"
+        APS_F4(APS_J0, "%2", "%3", "%4", "%5") APS_F4(APS_J4, "%6", "%7", "%8", "%9")
+        APS_F4(APS_J8, "%10", "%11", "%12", "%13") APS_F4(APS_J12, "%14", "%15", "%16", "%17")
+        : "+v"(acc)
+        : "v"(g), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]),
+          "v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]), "v"(d[0]), "v"(d[1]), "v"(d[2]), "v"(d[3]));
+    return acc;
+}
+
+template <bool XBF16>
+__device__ inline float chain_block(float acc, float g0, float g1, const ru32x4_t (&xp)[RFmt<XBF16>::kPieces]) {
+    if constexpr (XBF16) {
+        return chain32(acc, g0, g1, xp);
+    } else {
+        acc = chain16_f32(acc, g0, xp[0], xp[1], xp[2], xp[3]);
+        return chain16_f32(acc, g1, xp[4], xp[5], xp[6], xp[7]);
+    }
 }
 
 template <bool XBF16>
 __global__ void __launch_bounds__(256, 2)
 k_router_logits(const void* __restrict__ xv, const float* __restrict__ gate, int64_t rows,
                 int H, int E, float* __restrict__ logits) {
-    using XT = typename std::conditional<XBF16, bf16_t, float>::type;
-    const XT* __restrict__ x = static_cast<const XT*>(xv);
-    __shared__ __align__(16) float xs[kWave * kRouterPitch];
-    __shared__ __align__(16) float gs[kRouterExpertsPerBlock][kRouterKC];
+    using F = RFmt<XBF16>;
+    // one LDS object: slot s = [x: 64 rows x 256 B][gate: 4 experts x kK floats]
+    __shared__ __align__(16) uint8_t ring[kRouterSlots * F::kSlotBytes];
 
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int e = blockIdx.y * kRouterExpertsPerBlock + w;
     const bool active = e < E;  // wave-uniform
     const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kWave;
-    const float* xrow = xs + lane * kRouterPitch;
-    const float* grow = gs[w];
-    // gate staging: thread i copies float4 i of the block's 4 x 256 chunk
-    const int ge = blockIdx.y * kRouterExpertsPerBlock + (threadIdx.x >> 6);
-    const float* gsrc = gate + static_cast<int64_t>(ge < E ? ge : 0) * H + (threadIdx.x & 63) * 4;
+    const int NC = H / F::kK;   // chunks
 
-    auto load_xg = [&](float4 (&xd)[4], float4 (&gd)[4], int kk) {
+    // x copies: copy j of a chunk fills x bytes [1024 j, 1024 j + 1024) = rows
+    // R j .. R j + R - 1 (R = kRouterRowsPerCopy); wave w issues copies
+    // X w .. X w + X - 1 (X = kRouterXCopies).  Lane i lands at piece
+    // i % kRouterPieces of row R j + i / kRouterPieces and fetches the
+    // logical piece that rpos() places there.  Rows past the end re-read the
+    // last row.
+    const uint8_t* xsrc[kRouterXCopies];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            xd[i] = *reinterpret_cast<const float4*>(xrow + kk + 4 * i);
-            gd[i] = *reinterpret_cast<const float4*>(grow + kk + 4 * i);  // same address on every lane
-        }
+    for (int jj = 0; jj < kRouterXCopies; ++jj) {
+        const int r = kRouterRowsPerCopy * (kRouterXCopies * w + jj) + lane / kRouterPieces;
+        const int c = (lane % kRouterPieces) ^ (r & 15);
+        const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
+        xsrc[jj] = static_cast<const uint8_t*>(xv) + row * static_cast<int64_t>(H) * F::kElt + c * 16;
+    }
+    // gate copies: wave w fetches expert e's kK values of the chunk, one
+    // dword per lane per copy (inactive waves fetch a valid row, unused)
+    const float* gsrc = gate + static_cast<int64_t>(active ? e : E - 1) * H + lane;
+    auto issue_chunk = [&](int kc) {
+        uint8_t* slot = ring + (kc % kRouterSlots) * F::kSlotBytes;
+#pragma unroll
+        for (int jj = 0; jj < kRouterXCopies; ++jj)
+            __builtin_amdgcn_global_load_lds(APS_RGP(xsrc[jj] + static_cast<int64_t>(kc) * kRouterRowBytes),
+                                             APS_RLP(slot + (kRouterXCopies * w + jj) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int jj = 0; jj < F::kGateDma; ++jj)
+            __builtin_amdgcn_global_load_lds(APS_RGP(gsrc + kc * F::kK + jj * kWave),
+                                             APS_RLP(slot + F::kXBytes + w * F::kK * 4 + jj * 256), 4, 0, 0);
+    };
+    // chunk kc landed in this wave's view: wait for its copies (later chunks
+    // may stay in flight), then the barrier makes every wave's copies visible
+    auto chunk_ready = [&](int kc) {
+        const int later = NC - 1 - kc < kRouterSlots - 2 ? NC - 1 - kc : kRouterSlots - 2;
+        if (later >= 2) r_wait_vm<2 * F::kDma>();
+        else if (later == 1) r_wait_vm<F::kDma>();
+        else r_wait_vm<0>();
+        r_barrier();
+    };
+    auto load_block = [&](ru32x4_t (&xp)[F::kPieces], float& g0, float& g1, int kc, int bb) {
+        const uint8_t* slot = ring + (kc % kRouterSlots) * F::kSlotBytes;
+#pragma unroll
+        for (int p = 0; p < F::kPieces; ++p)
+            xp[p] = *reinterpret_cast<const ru32x4_t*>(slot + rpos(lane, bb * F::kPieces + p));
+        const float* gs = reinterpret_cast<const float*>(slot + F::kXBytes + w * F::kK * 4) + bb * kRouterBlk + (lane & 15);
+        g0 = gs[0];
+        g1 = gs[16];
     };
 
-    XStage<XBF16> st;
-    float4 gv;
-    st.load(x, row0, rows, H, 0);
-    gv = *reinterpret_cast<const float4*>(gsrc);
-    float acc = 0.0f;
-    for (int k0 = 0; k0 < H; k0 += kRouterKC) {
-        __syncthreads();  // previous chunk fully consumed
-        st.store(xs);
-        *reinterpret_cast<float4*>(&gs[threadIdx.x >> 6][(threadIdx.x & 63) * 4]) = gv;
-        __syncthreads();
-        if (k0 + kRouterKC < H) {
-            st.load(x, row0, rows, H, k0 + kRouterKC);
-            gv = *reinterpret_cast<const float4*>(gsrc + k0 + kRouterKC);
-        }
-        if (active) {
-            // 16 blocks of 16 steps; the LDS reads of block i+1 are issued
-            // before the FMAs of block i (ping-pong), pinned by sched_barrier
-            float4 xa[4], ga[4], xb[4], gb[4];
-            load_xg(xa, ga, 0);
 #pragma unroll
-            for (int blk = 0; blk < kRouterKC / 16; blk += 2) {
-                load_xg(xb, gb, 16 * blk + 16);
+    for (int c = 0; c < kRouterSlots - 1; ++c)
+        if (c < NC) issue_chunk(c);
+    chunk_ready(0);
+    if (kRouterSlots - 1 < NC) issue_chunk(kRouterSlots - 1);
+
+    float acc = 0.0f;
+    ru32x4_t xa[F::kPieces], xb[F::kPieces];
+    float ga0, ga1, gb0, gb1;
+    if (active) load_block(xa, ga0, ga1, 0, 0);
+    for (int kc = 0; kc < NC; ++kc) {
+        // register ping-pong: xa holds block bb, xb block bb + 1 (kBpc is even)
+#pragma unroll
+        for (int bb = 0; bb < F::kBpc; bb += 2) {
+            if (active) {
+                r_wait_lgkm0();
+                load_block(xb, gb0, gb1, kc, bb + 1);
                 __builtin_amdgcn_sched_barrier(0);
-                acc = fma16(acc, xa, ga);
+                acc = chain_block<XBF16>(acc, ga0, ga1, xa);
                 __builtin_amdgcn_sched_barrier(0);
-                if (blk + 2 < kRouterKC / 16) load_xg(xa, ga, 16 * blk + 32);
+            }
+            const bool last = bb + 2 == F::kBpc;
+            if (last && kc + 1 < NC) {
+                // chunk kc+1 opens next: this wave's reads of chunk kc are
+                // done once block bb+1 has landed; after the barrier chunk
+                // kc's slot is free for chunk kc + kRouterSlots
+                if (active) r_wait_lgkm0();
+                chunk_ready(kc + 1);
+                if (kc + kRouterSlots < NC) issue_chunk(kc + kRouterSlots);
+            }
+            if (active) {
+                r_wait_lgkm0();
+                if (!last) load_block(xa, ga0, ga1, kc, bb + 2);
+                else if (kc + 1 < NC) load_block(xa, ga0, ga1, kc + 1, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                acc = fma16(acc, xb, gb);
+                acc = chain_block<XBF16>(acc, gb0, gb1, xb);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -226,7 +326,8 @@ k_route_top2(const float* __restrict__ logits, int64_t rows, int E, uint8_t* __r
 hipError_t launch_router_logits(const void* x, bool x_bf16, const float* gate, int64_t rows,
                                 int hidden, int experts, float* logits, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    if (hidden % kRouterKC != 0 || experts <= 0) return hipErrorInvalidValue;
+    // whole chunks, and an even number of 32-step blocks
+    if (hidden % (x_bf16 ? RFmt<true>::kK : RFmt<false>::kK) != 0 || experts <= 0) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>(ceil_div(rows, kWave)),
                     static_cast<unsigned>(ceil_div(experts, kRouterExpertsPerBlock)));
     if (x_bf16)
