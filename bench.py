@@ -12,9 +12,11 @@ decoder layers would, so expert weights stream from HBM every step instead
 of sitting in the Infinity Cache.
 
 Prints ONE JSON line.  `roofline` covers the dominant kernel (the grouped
-w1||w3 + SwiGLU GEMM, k_ffn_up_bf16), timed with HIP events on the stream it
-is launched on; `cpu_baseline` times the CPU oracle (the reference CPU-path
-algorithm, src/layer.cu:113-148) on the host cores.
+w1||w3 + SwiGLU GEMM, k_ffn_up<Bf16Fmt>, or k_ffn_up<Fp8Fmt> for --config c5),
+timed with HIP events on the stream it is launched on; its `traffic` is the
+HBM bytes per launch measured with rocprofv3 counters (TRAFFIC_KIB below).
+`cpu_baseline` times the CPU oracle (the reference CPU-path algorithm,
+src/layer.cu:113-148) on the host cores for about --cpu-seconds.
 """
 from __future__ import annotations
 
@@ -37,6 +39,15 @@ PEAK_FP8 = 5.0e15        # MI355X dense fp8 MFMA, FLOP/s
 PEAK_F32 = 157.3e12
 PEAK_HBM = 8.0e12        # bytes/s
 LAYERS = 4
+COPY_PROBE_BYTES = 256 << 20
+# HBM bytes per launch of the roofline kernel, from two rocprofv3 counter runs
+# (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch, of `bench.py --config C
+# --steps 3 --warmup 1 --cpu-baseline skip --copy-probe`), each scaled by what
+# the counter reads for the 256 MiB copy probe: FETCH_SIZE 131088.5 KiB
+# (x 1.9997), WRITE_SIZE 262144 KiB (x 1.0).  Summary and commands:
+# profiles/moe_forward_hbm_traffic.md.  Re-measure when a GEMM kernel changes.
+TRAFFIC_KIB = {"c2": (114083.9, 7168.0), "c5": (89546.5, 14336.0)}
+FETCH_SCALE, WRITE_SCALE = 262144.0 / 131088.5, 1.0
 
 
 def parse():
@@ -46,7 +57,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5"])
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
-    ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU baseline: repeat full-batch runs until this much time is spent (at least 2 runs)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run one 256 MiB device-to-device copy before the steps (scale reference for the "
+                         "FETCH_SIZE / WRITE_SIZE counter passes)")
     return ap.parse_args()
 
 
@@ -95,6 +110,13 @@ def main():
             layers.append(moe.register_moe_weights_gpu(*lists, compute_dtype=tdt))
         del lists, scales
     torch.cuda.synchronize()
+
+    if args.copy_probe:
+        src = torch.full((COPY_PROBE_BYTES,), 7, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     L = capi.lib()
     lay = layers[0].layout(T)
@@ -204,7 +226,9 @@ def main():
     kname = "k_ffn_up<Fp8Fmt>" if fp8 else ("k_ffn_up<Bf16Fmt>" if bf16 else "k_ffn_up_f32")
     roofline = {"bound": "mfma", "kernel": kname,
                 "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
-                "frac": achieved / peak, "traffic": None,
+                "frac": achieved / peak,
+                "traffic": (TRAFFIC_KIB[args.config][0] * FETCH_SCALE + TRAFFIC_KIB[args.config][1] * WRITE_SCALE) * 1024
+                if args.config in TRAFFIC_KIB else None,
                 "flops_per_launch": flops_up, "launch_us": mean_t["ffn_up"] * 1e6}
 
     # ---- CPU baseline: the reference CPU-path algorithm on the host cores ----
@@ -213,15 +237,16 @@ def main():
         import oracle
         runs = []
         oracle.moe_forward(inp.x[:256], inp.gate, inp.w1, inp.w3, inp.w2)  # warm-up
-        for _ in range(args.cpu_runs):
+        while len(runs) < 2 or sum(runs) < args.cpu_seconds:
             t = time.perf_counter()
             oracle.moe_forward(inp.x, inp.gate, inp.w1, inp.w3, inp.w2)
             runs.append(time.perf_counter() - t)
-        med = statistics.median(runs)
-        cpu = {"value": T / med, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
-               "sample": f"full {args.config} batch ({T} tokens), values upcast to fp32, reference CPU-path "
-                         f"order (router, route, per-expert gather/FFN/scatter-add), 1 warm-up + median of "
-                         f"{args.cpu_runs} runs ({med:.2f} s each)"}
+        total = sum(runs)
+        cpu = {"value": T * len(runs) / total, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
+               "sample": f"{len(runs)} runs of the full {args.config} batch ({T} tokens each, {total:.1f} s in "
+                         f"all, median {statistics.median(runs):.2f} s), values upcast to fp32, reference "
+                         f"CPU-path order (router, route, per-expert gather/FFN/scatter-add), after a 256-token "
+                         f"warm-up"}
 
     line = {
         "metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1,
