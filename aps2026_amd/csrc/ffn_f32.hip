@@ -11,7 +11,7 @@
 // rounded to float afterwards).  They are SIMT kernels: each thread owns a
 // 4 x 4 block of outputs per operand and walks k in order; operand tiles are
 // staged k-major in LDS so the inner step is three ds_read_b128 + 32 FMAs.
-// This is the exactness path; the throughput path is
+// This is the exactness path (config C1, fp32); the throughput path is
 // the bf16 MFMA kernel.
 #include "common.hpp"
 

@@ -1,7 +1,7 @@
 // fp8 e4m3 quantisation for the fp8 expert path, and its weight packing.
 //
-// The reference has no fp8 path; this is the library's own format (BASELINE
-// config C5): weights e4m3 with one fp32 scale per output channel, x and the
+// The reference has no fp8 path; this is the library's own format (config
+// C5, 8192 tokens with fp8 experts): weights e4m3 with one fp32 scale per output channel, x and the
 // SwiGLU activations quantised per row at run time:
 //   scale = amax(|row|) / 448 (1 if the row is all zero),
 //   code  = e4m3(v / scale), round to nearest even, saturating at +-448

@@ -181,7 +181,7 @@ def make_moe_inputs(T: int, H: int = HIDDEN, E: int = NUM_EXPERTS, F: int = FFN,
                      packed=packed, zipf=zipf, seed=seed)
 
 
-# The BASELINE configs that exercise the MoE block itself.
+# The benchmark configs that exercise the MoE block itself.
 CONFIGS = {
     # C1: fp32, CPU-runnable, 512 tokens, unbiased router, seed 0.
     "c1": dict(T=512, dtype="f32", zipf=None),

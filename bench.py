@@ -4,7 +4,7 @@
 
 One step = one full MoE block (router GEMM, quantised top-2, dispatch,
 grouped w1||w3 + SwiGLU, grouped w2, combine) over one batch of synthetic
-tokens already resident in HBM.  Workload (default): BASELINE config C2 --
+tokens already resident in HBM.  Workload (default): benchmark config C2 --
 4096 tokens, hidden 4096, 16 experts top-2, expert FFN 448, bf16, router bias
 giving Zipf(1.1) expert loads.  Steps rotate over LAYERS distinct device
 copies of the expert weights (4 x 176 MB > the 256 MB MALL), as consecutive

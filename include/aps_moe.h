@@ -61,7 +61,7 @@ typedef enum aps_dtype {
  *   APS_DTYPE_F32  - fp32 FMA-chain kernels, accumulation order identical to
  *                    the reference (k ascending), src_dtype must be F32;
  *   APS_DTYPE_BF16 - bf16 MFMA kernels, fp32 accumulate; src F32 or BF16;
- *   APS_DTYPE_E4M3 - fp8 MFMA kernels; src E4M3 codes
+ *   APS_DTYPE_E4M3 - fp8 MFMA kernels (config C5); src E4M3 codes
  *                    with per-output-channel fp32 scales (w1_scale[e],
  *                    w3_scale[e]: [ffn] device arrays, w2_scale[e]:
  *                    [hidden]); x (bf16) and the SwiGLU activations are
@@ -179,7 +179,7 @@ APS_API int aps_moe_ffn_down(uint64_t handle, const void* act, const float* act_
                              int64_t rows, const uint32_t* offsets, void* y_perm,
                              void* stream);
 
-/* ---- fp8 stages (no reference counterpart) --------- */
+/* ---- fp8 stages (config C5; no reference counterpart) ------------------ */
 
 /* Per-row e4m3 quantisation: scale[r] = amax(|src[r]|) / 448 (1 for a zero
  * row), dst[r][k] = e4m3(src[r][k] / scale[r]) rounded to nearest even and

@@ -196,7 +196,7 @@ def dequantise_rows_e4m3(codes: np.ndarray, scale: np.ndarray) -> np.ndarray:
 
 
 def fp8_ffn_rows(x_rows: np.ndarray, experts: np.ndarray, w1, w3, w2):
-    """The fp8 path's expert FFN for n (row, expert) pairs (BASELINE C5):
+    """The fp8 path's expert FFN for n (row, expert) pairs (config C5, fp8 experts):
     x rows quantised per row to e4m3, the dequantised values through the
     gate/up GEMMs and SiLU (fp32), the activations rounded to bf16 and
     quantised per row to e4m3, then the w2 GEMM on their dequantised values.

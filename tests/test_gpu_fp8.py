@@ -1,4 +1,4 @@
-"""GPU parity of the fp8 e4m3 path against the CPU oracle.
+"""GPU parity of the fp8 e4m3 path (config C5: 8192 tokens, fp8 experts) against the CPU oracle.
 
 Bars: routing indices, counts, offsets and permutation bit-exact; the
 quantised operands the kernels consume (x and the SwiGLU activations, codes

@@ -1,6 +1,6 @@
 """GPU parity of the HIP MoE path against the CPU oracle, through the C ABI.
 
-Bars:
+Bars (the tolerances stated for this path):
   routing indices, per-expert counts, offsets and permutation: bit-exact
   fp32 path (config C1): output within 1e-5 relative, normwise per row
   bf16 path (config C2): output within 2e-2 relative, normwise per row
