@@ -97,6 +97,27 @@ __device__ inline void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
 }
 
+// s_waitcnt lgkmcnt(n) alone.
+template <int N>
+__device__ inline void wait_lgkm_n() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (N << 8) | (0x3 << 14));
+}
+
+// wait_vm_lgkm0<n> for a value n in {0, 4, ..., 20} known only after
+// unrolling (the s_waitcnt operand must be an immediate); other values wait
+// for everything.
+__device__ inline void wait_vm_lgkm0_upto20(int n) {
+    switch (n) {
+        case 20: wait_vm_lgkm0<20>(); break;
+        case 16: wait_vm_lgkm0<16>(); break;
+        case 12: wait_vm_lgkm0<12>(); break;
+        case 8: wait_vm_lgkm0<8>(); break;
+        case 4: wait_vm_lgkm0<4>(); break;
+        default: wait_vm_lgkm0<0>(); break;
+    }
+}
+
 // s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left at their maximum).
 __device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14)); }
 
@@ -118,6 +139,15 @@ struct Bf16Fmt {
     __device__ static f32x16_t mma(const frag_t& a, const frag_t& b, f32x16_t c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
+    // The register-resident w2 kernel pins its operands: accumulators in
+    // VGPRs, the resident act fragments (second operand) in AGPRs, which
+    // the MFMA reads directly.  Left to the allocator, the 224 act registers
+    // plus 128 accumulators overflow the VGPR file and every step shuffles
+    // operands between the two files.
+    static constexpr bool kPinned = true;
+    __device__ static void mma_pinned(f32x16_t& c, const frag_t& b, const frag_t& a) {
+        asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(b), "a"(a));
+    }
 };
 
 struct Fp8Fmt {
@@ -134,6 +164,8 @@ struct Fp8Fmt {
     __device__ static f32x16_t mma(const frag_t& a, const frag_t& b, f32x16_t c) {
         return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
     }
+    static constexpr bool kPinned = false;   // 128 act registers: the allocator copes
+    __device__ static void mma_pinned(f32x16_t& c, const frag_t& b, const frag_t& a) { c = mma(b, a, c); }
 };
 
 // ---------------------------------------------------------------------------
@@ -548,6 +580,354 @@ k_ffn_down(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint32_
     else ffn_down_block<false, Fmt>(ring, act, act_row_bytes, w2, y, H, KT, sa, s2, u);
 }
 
+// ---------------------------------------------------------------------------
+// w2 with the act operand resident in registers.  K = F is short (448 bf16,
+// 512 padded fp8), so a 256-position row tile of act fits the four waves'
+// VGPRs (64 positions per wave: 224 VGPRs in bf16, 128 in fp8).  A block
+// loads its row tile once and then streams w2 column blocks (128 hidden
+// columns, KT images of 16 KB) through a four-slot LDS ring; every B byte
+// feeds 256 positions (256 FLOP per LDS byte in bf16), so the loop is
+// MFMA-bound where the streamed-A engine above is load-bound.  After a
+// column block the tile is written through LDS as 16-byte row chunks while
+// the ring already holds the next column block's first stages.
+//   Work: each expert's positions form 256-row tiles; the H / 128 column
+// blocks of a tile are split into S contiguous segments, S = the largest
+// count that keeps tiles x S within the grid (about one block per CU).
+// Logical blocks run expert-major, then segment, then tile, and XCD x takes
+// a contiguous slice, so the blocks reading one w2 column range of an
+// expert share an L2.
+template <class Fmt>
+struct DownAr;
+template <>
+struct DownAr<Bf16Fmt> { static constexpr int kKtMax = 7; };    // F <= 448
+template <>
+struct DownAr<Fp8Fmt> { static constexpr int kKtMax = 4; };     // F padded to <= 512
+
+constexpr int kArRows = 256;                 // positions per block (4 waves x 64)
+constexpr int kArSlots = 4;                  // w2 ring: 4 images of 16 KB
+constexpr int kArPitch = 136;                // bf16 per staged y row (128 + 8)
+constexpr int kArAStage = kArRows * kRowBytes;  // 32 KB: one act stage of the row tile
+
+template <bool kFp8>
+struct ArLds {
+    uint8_t ring[kArSlots][kImageBytes];             // 64 KB
+    uint8_t stage[kArRows * kArPitch * 2];           // 68 KB: the y tile, or two act stages
+    float scl[kFp8 ? 32 * 128 : 4];                  // fp8: w2 column scales of the block's range
+};
+
+struct ArWork {
+    int expert, nb0, nb1;
+    uint32_t m0, end;
+};
+
+__device__ inline bool locate_ar(const uint32_t* __restrict__ offsets, int E, int NB, ArWork& u) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t lo = lane < E ? offsets[lane] : 0u;
+    uint32_t hi = __shfl_down(lo, 1);
+    if (lane == E - 1) hi = offsets[E];
+    const uint32_t cnt = lane < E ? hi - lo : 0u;
+    const int r256 = static_cast<int>((cnt + kArRows - 1) / kArRows);
+    int tiles = r256;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) tiles += __shfl_xor(tiles, d);
+    if (tiles == 0) return false;
+    const int G = static_cast<int>(gridDim.x);
+    int S = G / tiles;
+    S = S < 1 ? 1 : (S > NB ? NB : S);
+    const int total = tiles * S;
+    const int per = G / kXcds;
+    const int b = blockIdx.x;
+    const int t = (b % kXcds) * per + b / kXcds;
+    if (t >= total) return false;
+    int incl = r256 * S;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d);
+        if (lane >= d) incl += v;
+    }
+    const uint64_t m = __ballot(lane < E && incl > t);
+    const int e = __ffsll(static_cast<unsigned long long>(m)) - 1;
+    const int before = e > 0 ? __shfl(incl, e - 1) : 0;
+    const int i = t - before;
+    const int er = __shfl(r256, e);
+    const int seg = i / er, tile = i - seg * er;
+    // wave-uniform by construction; readfirstlane lets them live in SGPRs
+    // (the y buffer resource must be scalar)
+    u.expert = __builtin_amdgcn_readfirstlane(e);
+    u.m0 = __builtin_amdgcn_readfirstlane(__shfl(lo, e) + static_cast<uint32_t>(tile) * kArRows);
+    u.end = __builtin_amdgcn_readfirstlane(__shfl(hi, e));
+    u.nb0 = __builtin_amdgcn_readfirstlane(seg * NB / S);
+    u.nb1 = __builtin_amdgcn_readfirstlane((seg + 1) * NB / S);
+    return true;
+}
+
+// y-tile stores through a buffer resource: rows past the expert's end fall
+// outside num_records and the hardware drops them, so every thread issues
+// the same number of stores (the vmcnt arithmetic below relies on it).
+__device__ inline __amdgpu_buffer_rsrc_t y_rsrc(bf16_t* y, uint32_t m0, uint32_t end, int H, bool live) {
+    const uint32_t rows = live ? (end - m0 < kArRows ? end - m0 : kArRows) : 0u;
+    return __builtin_amdgcn_make_buffer_rsrc(y + static_cast<int64_t>(m0) * H, 0,
+                                             static_cast<int>(rows * static_cast<uint32_t>(H) * 2u), 0x00020000);
+}
+
+// 16-byte chunks c0 .. c0 + N - 1 of this thread's share of the staged y
+// tile: chunk c is tile row (tid + 256 c) / 16, column chunk (tid + 256 c) % 16.
+template <int N>
+__device__ inline void read_y_chunks(const bf16_t* stage, int c0, int tid, u32x4_t (&v)[N]) {
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+        const int id = tid + 256 * (c0 + c);
+        v[c] = *reinterpret_cast<const u32x4_t*>(stage + (id >> 4) * kArPitch + (id & 15) * 8);
+    }
+}
+template <int N>
+__device__ inline void write_y_chunks(__amdgpu_buffer_rsrc_t rs, int H, int nb, int c0, int tid, const u32x4_t (&v)[N]) {
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+        const int id = tid + 256 * (c0 + c);
+        __builtin_amdgcn_raw_buffer_store_b128(v[c], rs, (id >> 4) * H * 2 + nb * 256 + (id & 15) * 16, 0, 0);
+    }
+}
+
+// KT (k stages of 128 bytes) is a template argument so that the resident act
+// fragments take exactly KT x 2 x kSub registers.  With KT >= 4 (the
+// production shapes: F = 448 bf16, 512 fp8) the y tile of column block u-1
+// leaves during the first four k stages of column block u, 4 chunks per
+// stage, so the stores stream under MFMA work instead of stalling the ring.
+//
+// Schedule.  B fragments are read two MFMA steps ahead (three register
+// sets).  Stage g+1's ring barrier (stage_ready) sits at step kSub-2 of stage
+// g, just before its first fragments are read, and refills the slot of
+// stage g-1 with stage g+3... (g+1)+2.  Per step: wait for this step's
+// fragments, [barrier], [read this step's share of the staged y tile],
+// read the fragments of step + 2, MFMAs, [store the y share].
+template <class Fmt, int KT>
+__global__ void __launch_bounds__(256, 1)
+k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint32_t* __restrict__ offsets,
+              const uint8_t* __restrict__ w2, bf16_t* __restrict__ y, int H, int E,
+              const float* __restrict__ sa, const float* __restrict__ s2) {
+    constexpr bool kFp8 = Fmt::kElt == 1;
+    constexpr bool kOverlap = KT >= 4;
+    constexpr int KTM = KT;
+    constexpr int kSub = Fmt::kSub;
+    constexpr int kLoads = kFp8 ? 8 : 4;       // ds_read_b128 per fragment set
+    static_assert(kSub >= 2, "two steps per stage");
+    __shared__ __align__(16) ArLds<kFp8> lds;
+    ArWork u;
+    if (!locate_ar(offsets, E, H / 128, u)) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int aR = wave * 64;
+    const int NB = H / 128;
+    const int nunits = u.nb1 - u.nb0;
+    const int nstages = nunits * KT;
+    bf16_t* stage = reinterpret_cast<bf16_t*>(lds.stage);
+    const __amdgpu_buffer_rsrc_t ys = y_rsrc(y, u.m0, u.end, H, true);
+    const __amdgpu_buffer_rsrc_t ynull = y_rsrc(y, u.m0, u.end, H, false);
+
+    // w2 ring: stage g = (unit g / KT, k stage g % KT); wave w copies bytes
+    // [4 KB w, 4 KB w + 4 KB) of the 16 KB image, verbatim (pre-swizzled).
+    const uint8_t* bsrc = w2 + (static_cast<int64_t>(u.expert) * NB + u.nb0) * KT * kImageBytes + wave * 4096 + lane * 16;
+    auto issue_b = [&](int g) {
+        const uint8_t* src = bsrc + static_cast<int64_t>(g) * kImageBytes;
+        uint8_t* dst = lds.ring[g % kArSlots] + wave * 4096;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dma16(src + c * 1024, dst + c * 1024);
+    };
+    // y chunks issued by the overlap schedule at k stage k of a column block
+    auto stores_at = [](int k) { return kOverlap && (k + KTM) % KTM < 4 ? 4 : 0; };
+    // Stage g (k stage kt) landed for every wave.  Issued after stage g's
+    // copies (at stage_ready(g-2)): stage g+1's copies, if any, and the y
+    // chunks of k stages kt-2, kt-1 (bf16: the stores of a stage precede its
+    // stage_ready) or kt-3, kt-2 (fp8: they follow it).  Stages 0..2 wait for
+    // everything.  Then stage g-2's slot takes stage g+2.
+    auto stage_ready = [&](int g, int kt) {
+        const int later = g + 1 < nstages ? 1 : 0;
+        const int kS = kFp8 ? stores_at(kt - 2) + stores_at(kt - 3) : stores_at(kt - 1) + stores_at(kt - 2);
+        wait_vm_lgkm0_upto20(g < 3 ? 0 : 4 * later + kS);
+        raw_barrier();
+        if (g + 2 < nstages) issue_b(g + 2);
+    };
+    if (nstages > 0) issue_b(0);
+    if (nstages > 1) issue_b(1);
+
+    // fp8 scales: the block's w2 column scales into LDS, its 2 x 32 row scales per lane
+    float rs[2] = {1.0f, 1.0f};
+    if constexpr (kFp8) {
+        const float* src = s2 + static_cast<int64_t>(u.expert) * H + u.nb0 * 128;
+        for (int t = tid; t < nunits * 32; t += 256)
+            *reinterpret_cast<float4*>(lds.scl + 4 * t) = *reinterpret_cast<const float4*>(src + 4 * t);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            uint32_t p = u.m0 + aR + 32 * i + (lane & 31);
+            p = p < u.end ? p : u.end - 1;
+            rs[i] = sa[p];
+        }
+    }
+
+    // ---- the row tile of act into registers, one 32 KB stage at a time ----
+    typename Fmt::frag_t areg[KTM][2][kSub];
+    {
+        const uint8_t* asrc[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int row = slot_row(s, wave, lane);
+            uint32_t p = u.m0 + row;
+            p = p < u.end ? p : u.end - 1;
+            asrc[s] = act + static_cast<int64_t>(p) * act_row_bytes + slot_chunk(row, lane) * 16;
+        }
+        auto issue_a = [&](int kt) {
+            uint8_t* st = lds.stage + (kt & 1) * kArAStage;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) dma16(asrc[s] + kt * kRowBytes, st + (32 * s + 8 * wave) * kRowBytes);
+        };
+        issue_a(0);
+#pragma unroll
+        for (int kt = 0; kt < KTM; ++kt) {
+            if (kt < KT) {
+                if (kt + 1 < KT) {
+                    issue_a(kt + 1);
+                    wait_vm_lgkm0<8>();
+                } else {
+                    wait_vm_lgkm0<0>();
+                }
+                raw_barrier();
+                const uint8_t* st = lds.stage + (kt & 1) * kArAStage;
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int kk = 0; kk < kSub; ++kk) areg[kt][i][kk] = Fmt::load(st, aR + 32 * i + (lane & 31), kk, lane);
+                wait_lgkm0();
+                raw_barrier();  // slot kt & 1 takes stage kt + 2; the last barrier frees the y stage
+            }
+        }
+    }
+
+    typename Fmt::frag_t bf[3][4];
+    auto load_b = [&](typename Fmt::frag_t (&f)[4], int g, int kk) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f[j] = Fmt::load(lds.ring[g % kArSlots], 32 * j + (lane & 31), kk, lane);
+    };
+    if (nstages > 0) stage_ready(0, 0);
+    for (int ui = 0; ui < nunits; ++ui) {
+        const int nb = u.nb0 + ui;
+        const int g0 = ui * KT;
+        f32x16_t acc[2][4];
+        zero_acc(acc);
+        if constexpr (Fmt::kPinned) asm volatile("s_nop 4");  // VALU write -> MFMA srcC (hidden in asm)
+        const __amdgpu_buffer_rsrc_t prev = ui > 0 ? ys : ynull;  // unit 0 stores nothing, same count
+        load_b(bf[0], g0, 0);
+        load_b(bf[1], g0, 1);
+#pragma unroll
+        for (int kt = 0; kt < KTM; ++kt) {
+            if (kt < KT) {
+                const int g = g0 + kt;
+#pragma unroll
+                for (int s = 0; s < kSub; ++s) {
+                    const int q = kt * kSub + s;                      // step within the column block
+                    const bool next1 = s + 1 < kSub || kt + 1 < KT;   // step q+1 exists
+                    const bool next2 = s + 2 < kSub || kt + 1 < KT;   // step q+2 exists
+                    if (next1) wait_lgkm_n<kLoads>();
+                    else wait_lgkm0();
+                    if (s == kSub - 2 && g + 1 < nstages) stage_ready(g + 1, (kt + 1) % KTM);
+                    const bool st = kOverlap && s == 0 && kt < 4;
+                    u32x4_t yv[4];
+                    if (st) read_y_chunks<4>(stage, 4 * kt, tid, yv);
+                    if (next2) {
+                        const int s2_ = (s + 2) % kSub;
+                        load_b(bf[(q + 2) % 3], s + 2 < kSub ? g : g + 1, s2_);
+                    }
+                    APS_PIN();
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) Fmt::mma_pinned(acc[i][j], bf[q % 3][j], areg[kt][i][s]);
+                    APS_PIN();
+                    if (st) {
+                        // the previous column block's y chunks 4kt .. 4kt+3
+                        write_y_chunks<4>(prev, H, nb - 1, 4 * kt, tid, yv);
+                        APS_PIN();
+                    }
+                }
+            }
+        }
+
+        // epilogue: scales (fp8), bf16, staged in LDS
+        if constexpr (Fmt::kPinned) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");  // MFMA write -> VALU read
+        if (kOverlap) raw_barrier();  // every thread has read the previous tile out of the stage
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = aR + i * 32 + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float o[4];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) o[v] = acc[i][j][4 * q + v];
+                    const int col = 32 * j + 8 * q + 4 * (lane >> 5);
+                    if constexpr (kFp8) {
+                        const float4 a = *reinterpret_cast<const float4*>(lds.scl + ui * 128 + col);
+                        o[0] = o[0] * rs[i] * a.x; o[1] = o[1] * rs[i] * a.y;
+                        o[2] = o[2] * rs[i] * a.z; o[3] = o[3] * rs[i] * a.w;
+                    }
+                    const u32x2_t v = {pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
+                    *reinterpret_cast<u32x2_t*>(stage + row * kArPitch + col) = v;
+                }
+        }
+        wait_lgkm0();
+        raw_barrier();
+        if (!kOverlap || ui + 1 == nunits) {
+            // no later column block to hide under: store the tile now
+            u32x4_t yv[16];
+            read_y_chunks<16>(stage, 0, tid, yv);
+            write_y_chunks<16>(ys, H, nb, 0, tid, yv);
+            if (!kOverlap) {
+                wait_lgkm0();
+                raw_barrier();  // the stage is read out before the next epilogue
+            }
+        }
+    }
+}
+
+int num_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// The register-resident w2 kernel for KT k stages, or null when KT is past
+// the register budget (the streamed kernel serves those shapes).
+typedef void (*down_ar_fn)(const uint8_t*, int64_t, const uint32_t*, const uint8_t*, bf16_t*, int, int,
+                           const float*, const float*);
+template <class Fmt>
+down_ar_fn down_ar_kernel(int KT) {
+    switch (KT) {
+        case 1: return k_ffn_down_ar<Fmt, 1>;
+        case 2: return k_ffn_down_ar<Fmt, 2>;
+        case 3: return k_ffn_down_ar<Fmt, 3>;
+        case 4: return k_ffn_down_ar<Fmt, 4>;
+        case 5: return DownAr<Fmt>::kKtMax >= 5 ? k_ffn_down_ar<Fmt, (DownAr<Fmt>::kKtMax >= 5 ? 5 : 1)> : nullptr;
+        case 6: return DownAr<Fmt>::kKtMax >= 6 ? k_ffn_down_ar<Fmt, (DownAr<Fmt>::kKtMax >= 6 ? 6 : 1)> : nullptr;
+        case 7: return DownAr<Fmt>::kKtMax >= 7 ? k_ffn_down_ar<Fmt, (DownAr<Fmt>::kKtMax >= 7 ? 7 : 1)> : nullptr;
+        default: return nullptr;
+    }
+}
+
+// Grid of the register-resident w2 kernel: about one block per CU, at least
+// one per row tile, a multiple of the XCD count.
+dim3 grid_ar(int64_t rows, int experts) {
+    const int64_t tiles = max_row_tiles(2 * rows, kArRows, experts);
+    const int64_t g = tiles > num_cus() ? tiles : num_cus();
+    return dim3(static_cast<unsigned>(ceil_div(g, kXcds) * kXcds));
+}
+
 // Upper bound on the work-list length for A = 2 * rows positions.
 int64_t max_blocks(int64_t rows, int nblk, int experts, bool all_tall) {
     if (all_tall) return max_row_tiles(2 * rows, 256, experts) * nblk;
@@ -577,6 +957,12 @@ hipError_t launch_ffn_down_bf16(const bf16_t* act, const uint32_t* offsets, cons
                                 hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (hidden % 128 != 0 || ffn % 64 != 0) return hipErrorInvalidValue;
+    if (auto kern = down_ar_kernel<Bf16Fmt>(ffn / 64)) {
+        hipLaunchKernelGGL(kern, grid_ar(rows, experts), dim3(256), 0, s,
+                           reinterpret_cast<const uint8_t*>(act), static_cast<int64_t>(ffn) * 2, offsets,
+                           reinterpret_cast<const uint8_t*>(w2), y, hidden, experts, nullptr, nullptr);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_ffn_down<Bf16Fmt>, grid_of(max_blocks(rows, hidden / 128, experts, APS_DOWN_TALL)),
                        dim3(256), 0, s, reinterpret_cast<const uint8_t*>(act), static_cast<int64_t>(ffn) * 2,
                        offsets, reinterpret_cast<const uint8_t*>(w2), y, hidden, ffn / 64, experts, nullptr,
@@ -602,6 +988,11 @@ hipError_t launch_ffn_down_fp8(const uint8_t* actq, const float* act_scale, cons
     if (rows <= 0) return hipSuccess;
     if (hidden % 128 != 0 || ffn % 64 != 0) return hipErrorInvalidValue;
     const int kpad = static_cast<int>(ceil_div(ffn, 128) * 128);
+    if (auto kern = down_ar_kernel<Fp8Fmt>(kpad / 128)) {
+        hipLaunchKernelGGL(kern, grid_ar(rows, experts), dim3(256), 0, s, actq,
+                           static_cast<int64_t>(kpad), offsets, w2, y, hidden, experts, act_scale, w2_scale);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_ffn_down<Fp8Fmt>, grid_of(max_blocks(rows, hidden / 128, experts, APS_DOWN_TALL)),
                        dim3(256), 0, s, actq, static_cast<int64_t>(kpad), offsets, w2, y, hidden, kpad / 128,
                        experts, act_scale, w2_scale);
