@@ -23,6 +23,33 @@ using bf16_t = uint16_t;            // raw bfloat16 bits in memory
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// q = sign(l) * floorf(|l| / Q + 0.5f) * Q with every step rounded on its own
+// (the _rn intrinsics keep the compiler from contracting the multiply into a
+// later add).  Reference src/layer.cu:72-77, src/tensor.cu:1300-1306.
+__device__ inline float route_quantise(float l) {
+    const float r = __fmul_rn(floorf(__fadd_rn(__fdiv_rn(fabsf(l), kRouterQuantum), 0.5f)), kRouterQuantum);
+    return l < 0.0f ? -r : r;
+}
+
+// Greedy top-2 over the quantised logits q[0..E-1]: a later expert replaces
+// the incumbent only when it is larger by more than the tie epsilon
+// (reference src/layer.cu:78-87, src/tensor.cu:1307-1330).
+template <int EMAX>
+__device__ inline void route_greedy_top2(const float (&q)[EMAX], int E, int& first, int& second) {
+    int best = -1;
+    float bv = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+        if (e < E && (best < 0 || q[e] > __fadd_rn(bv, kRouterTieEps))) { best = e; bv = q[e]; }
+    first = best;
+    best = -1;
+    bv = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+        if (e < E && e != first && (best < 0 || q[e] > __fadd_rn(bv, kRouterTieEps))) { best = e; bv = q[e]; }
+    second = best;
+}
+
 // Upper bound on sum_e ceil(count_e / bm) over E experts with sum count_e = n.
 __host__ __device__ inline int64_t max_row_tiles(int64_t n, int64_t bm, int64_t E) {
     return ceil_div(n, bm) + E;

@@ -265,15 +265,6 @@ k_router_logits(const void* __restrict__ xv, const float* __restrict__ gate, int
     if (active && row < rows) logits[row * E + e] = acc;
 }
 
-// q = sign(l) * floorf(|l| / Q + 0.5f) * Q with every step rounded on its own
-// (the _rn intrinsics keep the compiler from contracting the multiply into a
-// later add).  src/layer.cu:72-77, src/tensor.cu:1300-1306.
-__device__ inline float quantise(float l) {
-    const float r = __fmul_rn(floorf(__fadd_rn(__fdiv_rn(fabsf(l), kRouterQuantum), 0.5f)),
-                              kRouterQuantum);
-    return l < 0.0f ? -r : r;
-}
-
 // One thread per token; one 64-thread workgroup per 64-token tile.  The
 // token's E logits are loaded up front (independent loads, one round trip),
 // then quantised and scanned twice.  Writes routes and the tile's per-expert
@@ -291,23 +282,8 @@ k_route_top2(const float* __restrict__ logits, int64_t rows, int E, uint8_t* __r
 #pragma unroll
         for (int e = 0; e < EMAX; ++e) q[e] = e < E ? logits[t * E + e] : 0.0f;
 #pragma unroll
-        for (int e = 0; e < EMAX; ++e) q[e] = quantise(q[e]);
-        // greedy scan: a later expert replaces the incumbent only when it is
-        // larger by more than the tie epsilon (src/layer.cu:78-87)
-        int best = -1;
-        float bv = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EMAX; ++e) {
-            if (e < E && (best < 0 || q[e] > __fadd_rn(bv, kRouterTieEps))) { best = e; bv = q[e]; }
-        }
-        first = best;
-        best = -1;
-        bv = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EMAX; ++e) {
-            if (e < E && e != first && (best < 0 || q[e] > __fadd_rn(bv, kRouterTieEps))) { best = e; bv = q[e]; }
-        }
-        second = best;
+        for (int e = 0; e < EMAX; ++e) q[e] = route_quantise(q[e]);
+        route_greedy_top2<EMAX>(q, E, first, second);
         routes[2 * t] = static_cast<uint8_t>(first);
         routes[2 * t + 1] = static_cast<uint8_t>(second);
     }
