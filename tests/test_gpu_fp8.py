@@ -140,6 +140,20 @@ def test_fp8_ragged_small(gpu_device, T):
     w.release()
 
 
+@pytest.mark.parametrize("F", [128, 256, 384, 448, 640])
+def test_fp8_ffn_widths_cover_each_w2_kernel(gpu_device, F):
+    # w2 k stages of 128 fp8: 1..4 select the register-resident kernel, 5 the streamed one
+    note(f"fp8 T=700 H=512 E=16 F={F}")
+    inp = synth.make_moe_inputs(T=700, H=512, E=16, F=F, dtype="fp8", seed=70 + F, name="fp8-widths")
+    w, out, plan = run_block(inp, gpu_device)
+    ref = oracle_routing(inp)
+    y_gpu, got = check_common(inp, out, plan, ref)
+    toks = np.unique(np.concatenate([np.arange(24), np.random.default_rng(F).choice(inp.T, 96, replace=False)]))
+    e_y, e_o = check_ffn(inp, y_gpu, got, ref, toks)
+    assert e_y <= TOL_FP8 and e_o <= TOL_FP8
+    w.release()
+
+
 def test_fp8_staged_entry_points_are_rejected(gpu_device):
     inp = synth.make_moe_inputs(T=8, H=1024, E=16, F=448, dtype="fp8", seed=3, name="fp8-err")
     w = fp8_weights(inp, gpu_device)

@@ -183,6 +183,24 @@ def test_ragged_rows_small_shapes(gpu_device, T, dtype):
     w.release()
 
 
+@pytest.mark.parametrize("F", [192, 256, 320, 384, 448, 512])
+def test_ffn_widths_cover_each_w2_kernel(gpu_device, F):
+    # F / 64 k stages of w2: 3..7 select the register-resident kernel (4..7
+    # with stores spread over the next column block), 8 the streamed one
+    note(f"bf16 T=700 H=512 E=16 F={F}: every w2 kernel shape vs the oracle")
+    inp = synth.make_moe_inputs(T=700, H=512, E=16, F=F, dtype="bf16", seed=40 + F)
+    w = weights_for(inp, gpu_device)
+    x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+    out = moe.moe_forward_gpu(x, gate, w, out_dtype=torch.float32)
+    plan = w.plan_views(inp.T)
+    torch.cuda.synchronize()
+    ref = oracle.reference_path(inp.x, inp.gate, inp.w1, inp.w3, inp.w2)
+    check_plan(plan, ref, inp.T)
+    assert rowwise_err(bf16_to_np(plan["y"]), ref["y"]).max() <= TOL_BF16
+    assert rowwise_err(out.cpu().numpy(), ref["out"]).max() <= TOL_BF16
+    w.release()
+
+
 def test_empty_batch(gpu_device):
     note("T=0")
     inp = synth.make_moe_inputs(T=0, H=256, E=16, F=64, dtype="bf16", seed=1)
