@@ -182,6 +182,8 @@ int check_x_dtype(const WeightSet& w, int32_t x_dtype) {
     return APS_OK;
 }
 
+// Routing (from `logits`; nullptr when the router kernel already wrote the
+// routes and tile histogram into the workspace), dispatch, FFN and combine.
 int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const float* logits, int64_t rows,
                         void* out, int32_t out_dtype, char* ws, const aps_moe_ws_layout& L,
                         hipStream_t s) {
@@ -196,7 +198,7 @@ int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const 
         APS_HIP(aps::launch_to_bf16(static_cast<const float*>(x), xb, rows * w.H, s), "x to bf16 launch");
         x = xb;
     }
-    APS_HIP(aps::launch_route_top2(logits, rows, w.E, routes, tiles, s), "route_top2 launch");
+    if (logits) APS_HIP(aps::launch_route_top2(logits, rows, w.E, routes, tiles, s), "route_top2 launch");
     APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, w.E, counts, offsets, arows, rpos, s),
             "dispatch launch");
     if (w.compute == APS_DTYPE_E4M3) {
@@ -349,8 +351,8 @@ int aps_router_logits(const void* x, int32_t x_dtype, const float* gate, int64_t
     if (x_dtype != APS_DTYPE_F32 && x_dtype != APS_DTYPE_BF16)
         return fail(APS_ERR_DTYPE, "router x dtype %d not supported", x_dtype);
     if (rows > 0 && (!x || !gate || !logits)) return fail(APS_ERR_ARG, "router: NULL pointer");
-    APS_HIP(aps::launch_router_logits(x, x_dtype == APS_DTYPE_BF16, gate, rows, hidden, num_experts,
-                                      logits, static_cast<hipStream_t>(stream)),
+    APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, hidden, num_experts, logits, nullptr,
+                               nullptr, static_cast<hipStream_t>(stream)),
             "router_logits launch");
     return APS_OK;
 }
@@ -548,10 +550,14 @@ int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float
     if (!gate) return fail(APS_ERR_ARG, "forward: NULL gate");
     char* ws = static_cast<char*>(workspace);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    // logits, routes and the tile histogram in one kernel; the grouped path
+    // then starts at the dispatch
     float* logits = reinterpret_cast<float*>(ws + L.logits);
-    APS_HIP(aps::launch_router_logits(x, x_dtype == APS_DTYPE_BF16, gate, rows, w->H, w->E, logits, s),
-            "router_logits launch");
-    return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, logits, rows, out, out_dtype, ws, L, s);
+    auto* routes = reinterpret_cast<uint8_t*>(ws + L.routes);
+    auto* tiles = reinterpret_cast<uint32_t*>(ws + L.tile_counts);
+    APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, w->H, w->E, logits, routes, tiles, s),
+            "router launch");
+    return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, nullptr, rows, out, out_dtype, ws, L, s);
 }
 
 // Dense FFN of a single-expert weight set: offsets {0, rows} and the

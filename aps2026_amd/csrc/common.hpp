@@ -50,6 +50,22 @@ __device__ inline void route_greedy_top2(const float (&q)[EMAX], int E, int& fir
     second = best;
 }
 
+// Tile histogram word of expert e for the 64-token tile of this wave: byte q
+// counts the routes to e of tokens 16q .. 16q+15 (at most 16 each), so a word
+// sums to the tile's count with (w * 0x01010101) >> 24.  The router writes the
+// bytes one 16-token workgroup at a time.
+__device__ inline uint32_t tile_quarter_counts(int first, int second, int e) {
+    const uint64_t m0 = __ballot(first == e), m1 = __ballot(second == e);
+    uint32_t word = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint64_t qm = 0xFFFFull << (16 * q);
+        word |= static_cast<uint32_t>(__popcll(m0 & qm) + __popcll(m1 & qm)) << (8 * q);
+    }
+    return word;
+}
+__host__ __device__ inline uint32_t tile_word_total(uint32_t w) { return (w * 0x01010101u) >> 24; }
+
 // Upper bound on sum_e ceil(count_e / bm) over E experts with sum count_e = n.
 __host__ __device__ inline int64_t max_row_tiles(int64_t n, int64_t bm, int64_t E) {
     return ceil_div(n, bm) + E;
@@ -97,8 +113,11 @@ __device__ inline RowTile wave_find_tile(int tile, int bm, uint32_t lo, uint32_t
 
 // ---- launchers (defined in the .hip files) --------------------------------
 
-hipError_t launch_router_logits(const void* x, bool x_bf16, const float* gate, int64_t rows,
-                                int hidden, int experts, float* logits, hipStream_t s);
+// Router GEMM; with routes != nullptr also the top-2 routes and the tile
+// histogram (tile_counts), in the same kernel.
+hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t rows, int hidden,
+                         int experts, float* logits, uint8_t* routes, uint32_t* tile_counts,
+                         hipStream_t s);
 hipError_t launch_route_top2(const float* logits, int64_t rows, int experts, uint8_t* routes,
                              uint32_t* tile_counts, hipStream_t s);
 hipError_t launch_tile_hist(const uint8_t* routes, int64_t rows, int experts,

@@ -7,7 +7,8 @@
 // tokens in ascending token order.
 //
 // gfx950 design: the routing kernel already produced a per-64-token-tile
-// histogram (wave ballots, no atomics).  Here each wave owns one tile:
+// histogram (one word per tile and expert, one byte per 16-token quarter).
+// Here each wave owns one tile:
 //   1. lane e sums expert e's counts over all tiles (total) and over the
 //      tiles before its own (prefix) -- a handful of L2-resident loads;
 //   2. a wave scan over lanes turns totals into offsets;
@@ -41,7 +42,7 @@ k_tile_hist(const uint8_t* __restrict__ routes, int64_t rows, int E,
     }
     uint32_t mine = 0;
     for (int e = 0; e < E; ++e) {
-        const uint32_t c = __popcll(__ballot(first == e)) + __popcll(__ballot(second == e));
+        const uint32_t c = tile_quarter_counts(first, second, e);
         if (lane == e) mine = c;
     }
     if (tile < ntiles && lane < E) tile_counts[tile * E + lane] = mine;
@@ -63,13 +64,16 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
     uint32_t total = 0, before = 0;
     if (lane < E) {
         for (int64_t j0 = 0; j0 < ntiles; j0 += 32) {
+            // unconditional loads (index clamped), so that all 32 are in
+            // flight before the first use
             uint32_t c[32];
 #pragma unroll
-            for (int i = 0; i < 32; ++i) c[i] = j0 + i < ntiles ? tile_counts[(j0 + i) * E + lane] : 0u;
+            for (int i = 0; i < 32; ++i) c[i] = tile_counts[(j0 + i < ntiles ? j0 + i : ntiles - 1) * E + lane];
 #pragma unroll
             for (int i = 0; i < 32; ++i) {
-                total += c[i];
-                before += j0 + i < tile ? c[i] : 0u;
+                const uint32_t n = j0 + i < ntiles ? tile_word_total(c[i]) : 0u;
+                total += n;
+                before += j0 + i < tile ? n : 0u;
             }
         }
     }

@@ -1,274 +1,344 @@
-// Router: logits GEMM (bit-exact fp32 FMA chains) and quantised greedy top-2.
+// Router: logits GEMM (bit-exact fp32 FMA chains), quantised greedy top-2 and
+// the per-tile expert histogram, in one kernel.
 //
 // Reference: k_matmul_transposed_narrow (src/tensor.cu:2943-3006) computes
 // each logit as ONE fp32 accumulator walked over k = 0..H-1 with FMA, and
-// k_moe_top2 (src/tensor.cu:1293-1331) quantises and greedy-selects.  The
-// reference's own logs show that a last-ulp change upstream flips experts, so
-// the chain order is fixed: no split-K, no tree reduction over k.
+// k_moe_top2 (src/tensor.cu:1293-1331) quantises and greedy-selects.  A
+// last-ulp change of a logit can flip an expert, so the chain order is fixed:
+// no split-K, no tree reduction over k.
 //
-// gfx950 mapping.  The parallelism is T*E independent chains of length H.
-// One lane owns one chain: a wavefront is 64 tokens x 1 expert, a workgroup
-// 64 tokens x 4 experts (four waves sharing the x tile), grid [token tiles] x
-// [E/4].  At T = 4096, E = 16 that is one wave per SIMD, so the time is the
-// length of one dependent chain.  Measured on gfx950 (cycles per step):
-// dependent v_fmac_f32_dpp alone 6.1; with the bf16 -> fp32 conversion
-// interleaved 9.2; with the LDS operand reads 10.8; with the ring barrier
-// 12.4.  The design keeps everything else off the chain:
-//  * x streams into a two-slot LDS ring straight from global memory
-//    (global_load_lds_dwordx4; no VGPR staging, no conversion pass).  A slot
-//    holds 512 bytes of each of the 64 token rows, in 16-byte pieces XOR-
-//    swizzled by row so that the 16 lanes of an LDS phase, each reading its
-//    own row, hit 16 distinct 4-bank groups.  The copy of chunk c+1 is in
-//    flight while chunk c (256 bf16 steps, ~1 us) is consumed.
-//  * The gate chunk of the block's 4 experts rides in the same slot.  Lane
-//    j of every 16-lane row reads gate value j of a 16-step group, and the
-//    FMA takes it through DPP row_newbcast:j, which hands lane j's value to
-//    the whole row: a broadcast that costs no LDS bandwidth and no scalar-
-//    cache latency (scalar gate loads miss the scalar cache once per 64 B
-//    and stall the chain on L2 latency).
-//  * bf16 -> fp32 is exact (a shift or a mask).  The chain is one asm
-//    stream in which the conversion for step j+2 sits behind the FMA of
-//    step j; the FMA is v_fmac_f32_dpp(acc, gate_k, x_k), k ascending, as in
-//    the reference (the product is commutative, so operand order does not
-//    change a bit).
-//  * Operand reads for block b+1 (32 steps) are issued before block b's
-//    FMAs; the ring barrier for chunk c sits at the last block of chunk c-1,
-//    so the first reads of a chunk are also issued ahead.
-//  * 72 KB of LDS per workgroup: two workgroups per CU (two chains per SIMD
-//    once T*E exceeds 64 chains per SIMD, T > 4096 at E = 16).
-// With tiles % 8 == 0 the expert groups of a token tile land on one XCD
-// (workgroups are dealt round-robin over the 8 XCDs), so x is fetched from
-// HBM once per XCD L2.
+// gfx950 mapping.  There are T*E independent chains of length H and one lane
+// owns one chain.  A wavefront is 4 tokens x 16 experts: each 16-lane row is
+// one token and lane j of the row is expert j (E <= 16; for E <= 32 / 64 a
+// token spans 2 / 4 rows, R = rows per token).  A workgroup is 16 tokens
+// (4 R waves), so at T = 4096, E = 16 every SIMD runs one wave and the time
+// is the length of one dependent chain.
+//  * x is the broadcast operand.  Lane i of a row holds x[t][8i .. 8i+7] of a
+//    128-step window (one 16-byte load per lane, straight to registers) and
+//    v_fmac_f32_dpp ... row_newbcast:i hands element m of lane i to the whole
+//    row.  The bf16 -> fp32 conversion (a shift or a mask, exact) costs 8
+//    VALU ops per 128 steps instead of one per step.
+//  * The gate is the per-lane operand.  128-step windows of every expert's
+//    gate row sit in LDS as [k/4][expert][4] fp32, so the 16 lanes of a row
+//    read 16 consecutive 16-byte pieces (no bank conflicts) and one
+//    ds_read_b128 feeds four steps.  Windows stream into a two-stage LDS ring
+//    with global_load_lds_dwordx4 (a stage is 32 KB: 512 steps of 16
+//    experts), shared by the workgroup's waves, one barrier per stage.  Gate
+//    reads run two 16-step blocks ahead of the FMAs.
+//  * Each FMA is v_fmac_f32_dpp(acc, x_k, gate_k), k ascending, as in the
+//    reference (the product is commutative, so the operand order changes no
+//    bit).
+//  * Measured on gfx950 (cycles per chain step, one wave per SIMD): the DPP
+//    chain with its gate in registers 5.65, with the gate read from LDS 7.65.
+//    A lane-per-token layout (x per lane from LDS and converted every step,
+//    gate broadcast) ran at 12.4.
+// After the chain a row holds its token's E logits.  Every lane gathers them
+// (ds_bpermute), quantises and runs the reference's greedy scan; the
+// workgroup's per-expert counts (one 16-token quarter of a 64-token tile)
+// become one byte of the tile histogram words that the dispatch reads.
 #include "common.hpp"
+
+#include <utility>
 
 namespace aps {
 namespace {
 
-constexpr int kRouterRowBytes = 512;        // bytes of one token row per chunk
-constexpr int kRouterSlots = 2;             // LDS ring depth (chunks)
-static_assert(kRouterSlots >= 2 && kRouterSlots <= 4, "chunk_ready() waits for at most two later chunks");
-constexpr int kRouterPieces = kRouterRowBytes / 16;          // 16-byte pieces per row
-constexpr int kRouterRowsPerCopy = kWave / kRouterPieces;    // rows per 1 KB copy
-constexpr int kRouterXCopies = kRouterPieces / 4;            // x copies per wave per chunk
-constexpr int kRouterExpertsPerBlock = 4;   // one wave per expert
-constexpr int kRouterBlk = 32;              // chain steps per register block
+constexpr int kRWin = 128;                // chain steps per window (one x load per lane)
+constexpr int kRStageBytes = 32 * 1024;   // gate bytes per ring stage
+constexpr int kRTokens = 16;              // tokens per workgroup: a quarter of a routing tile
+static_assert(kTileTokens == 4 * kRTokens, "tile histogram words hold four quarter-tile bytes");
 
 typedef uint32_t ru32x4_t __attribute__((ext_vector_type(4)));
+typedef float rf32x4_t __attribute__((ext_vector_type(4)));
 
 #define APS_RGP(p) ((const __attribute__((address_space(1))) void*)(p))
 #define APS_RLP(p) ((__attribute__((address_space(3))) void*)(p))
 
-template <bool XBF16>
-struct RFmt {
-    static constexpr int kElt = XBF16 ? 2 : 4;
-    static constexpr int kK = kRouterRowBytes / kElt;                 // k per chunk (256 / 128)
-    static constexpr int kBpc = kK / kRouterBlk;                      // blocks per chunk (8 / 4)
-    static constexpr int kPieces = kRouterBlk * kElt / 16;            // 16-B x pieces per block (4 / 8)
-    static constexpr int kXBytes = kWave * kRouterRowBytes;           // 32 KB
-    static constexpr int kGBytes = kRouterExpertsPerBlock * kK * 4;   // 4 KB / 2 KB
-    static constexpr int kSlotBytes = kXBytes + kGBytes;
-    static constexpr int kGateDma = kK / kWave;                       // dword copies per wave (4 / 2)
-    static constexpr int kDma = kRouterXCopies + kGateDma;            // copies per wave per chunk
-};
-
-// LDS byte offset of 16-byte piece c of token row r (0..63).
-__device__ inline int rpos(int r, int c) { return r * kRouterRowBytes + ((c ^ (r & 15)) << 4); }
-
-__device__ inline void r_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14)); }
 template <int N>
 __device__ inline void r_wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
+__device__ inline void r_wait_vm0() { r_wait_vm<0>(); }
 __device__ inline void r_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// ---- the chain: 32 steps per asm block --------------------------------------
-// %0 acc; bf16: %1..%4 temporaries, %5 / %6 gate groups (steps 0-15 / 16-31),
-// %7..%22 the 16 words of bf16 pairs.  Step 2i takes the low half of word i
-// (shift), step 2i+1 the high half (mask).
-#define APS_STR_(x) #x
-#define APS_STR(x) APS_STR_(x)
-#define APS_F(T, G, J) "v_fmac_f32_dpp %0, " G ", " T " row_newbcast:" APS_STR(J) " row_mask:0xf bank_mask:0xf\n\t"
-#define APS_LO(T, W) "v_lshlrev_b32 " T ", 16, " W "\n\t"
-#define APS_HI(T, W) "v_and_b32 " T ", 0xffff0000, " W "\n\t"
-// Steps 4q .. 4q+3 (words W0 = 2q, in %1 / %2, and W1 = 2q+1) and the
-// conversion of the next word WN into %1 / %2.
-#define APS_QUAD(G, J, W1, WN)                                                          \
-    APS_F("%1", G, J) APS_LO("%3", W1) APS_F("%2", G, J##_1) APS_HI("%4", W1)           \
-    APS_F("%3", G, J##_2) APS_LO("%1", WN) APS_F("%4", G, J##_3) APS_HI("%2", WN)
-#define APS_QUAD_LAST(G, J, W1)                                                         \
-    APS_F("%1", G, J) APS_LO("%3", W1) APS_F("%2", G, J##_1) APS_HI("%4", W1)           \
-    APS_F("%3", G, J##_2) APS_F("%4", G, J##_3)
-// DPP lane numbers of the four steps of each quad
-#define APS_J0 0
-#define APS_J0_1 1
-#define APS_J0_2 2
-#define APS_J0_3 3
-#define APS_J4 4
-#define APS_J4_1 5
-#define APS_J4_2 6
-#define APS_J4_3 7
-#define APS_J8 8
-#define APS_J8_1 9
-#define APS_J8_2 10
-#define APS_J8_3 11
-#define APS_J12 12
-#define APS_J12_1 13
-#define APS_J12_2 14
-#define APS_J12_3 15
-
-__device__ inline float chain32(float acc, float g0, float g1, const ru32x4_t (&xp)[4]) {
-    float t0, t1, t2, t3;
-    asm volatile(
-        "s_nop 1\n\t"  // DPP source written by a VALU copy needs two wait states
-        APS_LO("%1", "%7") APS_HI("%2", "%7")
-        APS_QUAD("%5", APS_J0, "%8", "%9") APS_QUAD("%5", APS_J4, "%10", "%11")
-        APS_QUAD("%5", APS_J8, "%12", "%13") APS_QUAD("%5", APS_J12, "%14", "%15")
-        APS_QUAD("%6", APS_J0, "%16", "%17") APS_QUAD("%6", APS_J4, "%18", "%19")
-        APS_QUAD("%6", APS_J8, "%20", "%21") APS_QUAD_LAST("%6", APS_J12, "%22")
-        : "+v"(acc), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
-        : "v"(g0), "v"(g1),
-          "v"(xp[0][0]), "v"(xp[0][1]), "v"(xp[0][2]), "v"(xp[0][3]),
-          "v"(xp[1][0]), "v"(xp[1][1]), "v"(xp[1][2]), "v"(xp[1][3]),
-          "v"(xp[2][0]), "v"(xp[2][1]), "v"(xp[2][2]), "v"(xp[2][3]),
-          "v"(xp[3][0]), "v"(xp[3][1]), "v"(xp[3][2]), "v"(xp[3][3]));
-    return acc;
-}
-
-// fp32 x: 16 steps, %0 acc, %1 gate group, %2..%17 the x values.
-#define APS_F4(J, A, B, C, D) APS_F(A, "%1", J) APS_F(B, "%1", J##_1) APS_F(C, "%1", J##_2) APS_F(D, "%1", J##_3)
-__device__ inline float chain16_f32(float acc, float g, const ru32x4_t& a, const ru32x4_t& b,
-                                    const ru32x4_t& c, const ru32x4_t& d) {
-    asm volatile(
-        "s_nop 1\n\t"
-        APS_F4(APS_J0, "%2", "%3", "%4", "%5") APS_F4(APS_J4, "%6", "%7", "%8", "%9")
-        APS_F4(APS_J8, "%10", "%11", "%12", "%13") APS_F4(APS_J12, "%14", "%15", "%16", "%17")
-        : "+v"(acc)
-        : "v"(g), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]),
-          "v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]), "v"(d[0]), "v"(d[1]), "v"(d[2]), "v"(d[3]));
-    return acc;
-}
-
-template <bool XBF16>
-__device__ inline float chain_block(float acc, float g0, float g1, const ru32x4_t (&xp)[RFmt<XBF16>::kPieces]) {
-    if constexpr (XBF16) {
-        return chain32(acc, g0, g1, xp);
-    } else {
-        acc = chain16_f32(acc, g0, xp[0], xp[1], xp[2], xp[3]);
-        return chain16_f32(acc, g1, xp[4], xp[5], xp[6], xp[7]);
+// ---- the chain: 16 steps per asm block ---------------------------------------
+// Step s = 0..15: acc = fma(x_s, g_s, acc), where x_s is element s % 8 of lane
+// L0 (s < 8) or L1 (s >= 8) of the row, broadcast by DPP row_newbcast, and g_s
+// this lane's gate value (g[s / 4][s % 4]).  Block b opens with the four gate
+// reads of block b + 2 and then waits until 8 reads remain in flight: LDS
+// reads complete in order, so that completes block b's own four (blocks b+1
+// and b+2 stay in flight).  Measured on gfx950, the reads in one burst at the
+// head of the block ran 7% faster than spread between the FMA groups.
+// Operands: %0 acc; %1..%4 the next reads' destinations (early clobber: the
+// data lands after the statement); %5..%12 x elements; %13..%28 gate values;
+// %29 the lane's LDS address; %30..%33 the read offsets.
+#define APS_RF(XI, GI, L) "v_fmac_f32_dpp %0, %" #XI ", %" #GI " row_newbcast:" #L " row_mask:0xf bank_mask:0xf\n\t"
+#define APS_RG(L, X0, X1, X2, X3, G0, G1, G2, G3) APS_RF(X0, G0, L) APS_RF(X1, G1, L) APS_RF(X2, G2, L) APS_RF(X3, G3, L)
+#define APS_RBODY(L0, L1)                        \
+    APS_RG(L0, 5, 6, 7, 8, 13, 14, 15, 16)       \
+    APS_RG(L0, 9, 10, 11, 12, 17, 18, 19, 20)    \
+    APS_RG(L1, 5, 6, 7, 8, 21, 22, 23, 24)       \
+    APS_RG(L1, 9, 10, 11, 12, 25, 26, 27, 28)
+#define APS_RREADS                                 \
+    "ds_read_b128 %1, %29 offset:%30\n\t"          \
+    "ds_read_b128 %2, %29 offset:%31\n\t"          \
+    "ds_read_b128 %3, %29 offset:%32\n\t"          \
+    "ds_read_b128 %4, %29 offset:%33\n\t"
+#define APS_RBLK(NAME, HEAD, L0, L1)                                                                      \
+    template <int OFF, int STRIDE>                                                                        \
+    __device__ inline float NAME(float acc, const float (&c)[8], const rf32x4_t (&g)[4], rf32x4_t (&gn)[4], \
+                                 uint32_t addr) {                                                         \
+        asm volatile(HEAD APS_RBODY(L0, L1)                                                               \
+                     : "+v"(acc), "=&v"(gn[0]), "=&v"(gn[1]), "=&v"(gn[2]), "=&v"(gn[3])                  \
+                     : "v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]), "v"(c[4]), "v"(c[5]), "v"(c[6]),       \
+                       "v"(c[7]), "v"(g[0][0]), "v"(g[0][1]), "v"(g[0][2]), "v"(g[0][3]), "v"(g[1][0]),   \
+                       "v"(g[1][1]), "v"(g[1][2]), "v"(g[1][3]), "v"(g[2][0]), "v"(g[2][1]), "v"(g[2][2]), \
+                       "v"(g[2][3]), "v"(g[3][0]), "v"(g[3][1]), "v"(g[3][2]), "v"(g[3][3]), "v"(addr),   \
+                       "n"(OFF), "n"(OFF + STRIDE), "n"(OFF + 2 * STRIDE), "n"(OFF + 3 * STRIDE));         \
+        return acc;                                                                                       \
     }
+// Block 0 of a window follows the VALU writes of its x elements: a DPP
+// source written by VALU needs two wait states (the reads provide them).
+APS_RBLK(rblk0, APS_RREADS "s_waitcnt lgkmcnt(8)\n\t", 0, 1)
+APS_RBLK(rblk1, APS_RREADS "s_waitcnt lgkmcnt(8)\n\t", 2, 3)
+APS_RBLK(rblk2, APS_RREADS "s_waitcnt lgkmcnt(8)\n\t", 4, 5)
+APS_RBLK(rblk3, APS_RREADS "s_waitcnt lgkmcnt(8)\n\t", 6, 7)
+APS_RBLK(rblk4, APS_RREADS "s_waitcnt lgkmcnt(8)\n\t", 8, 9)
+APS_RBLK(rblk5, APS_RREADS "s_waitcnt lgkmcnt(8)\n\t", 10, 11)
+APS_RBLK(rblk6, APS_RREADS "s_waitcnt lgkmcnt(8)\n\t", 12, 13)
+APS_RBLK(rblk7, APS_RREADS "s_waitcnt lgkmcnt(8)\n\t", 14, 15)
+// the last two blocks of a stage read nothing ahead
+APS_RBLK(rblk6_tail, "s_waitcnt lgkmcnt(4)\n\t", 12, 13)
+APS_RBLK(rblk7_tail, "s_waitcnt lgkmcnt(0)\n\t", 14, 15)
+
+// Block b of a stage of NB blocks (NB a multiple of 8): the FMAs of block b,
+// with the reads of block b + 2 (offsets OFF + m STRIDE) when it exists.
+template <int B, int NB, int OFF, int STRIDE>
+__device__ inline float rblock(float acc, const float (&c)[8], const rf32x4_t (&g)[4], rf32x4_t (&gn)[4],
+                               uint32_t addr) {
+    constexpr int Q = B % 8;
+    if constexpr (B == NB - 2) return rblk6_tail<0, 0>(acc, c, g, gn, addr);
+    else if constexpr (B == NB - 1) return rblk7_tail<0, 0>(acc, c, g, gn, addr);
+    else if constexpr (Q == 0) return rblk0<OFF, STRIDE>(acc, c, g, gn, addr);
+    else if constexpr (Q == 1) return rblk1<OFF, STRIDE>(acc, c, g, gn, addr);
+    else if constexpr (Q == 2) return rblk2<OFF, STRIDE>(acc, c, g, gn, addr);
+    else if constexpr (Q == 3) return rblk3<OFF, STRIDE>(acc, c, g, gn, addr);
+    else if constexpr (Q == 4) return rblk4<OFF, STRIDE>(acc, c, g, gn, addr);
+    else if constexpr (Q == 5) return rblk5<OFF, STRIDE>(acc, c, g, gn, addr);
+    else if constexpr (Q == 6) return rblk6<OFF, STRIDE>(acc, c, g, gn, addr);
+    else return rblk7<OFF, STRIDE>(acc, c, g, gn, addr);
 }
 
-template <bool XBF16>
-__global__ void __launch_bounds__(256, 2)
-k_router_logits(const void* __restrict__ xv, const float* __restrict__ gate, int64_t rows,
-                int H, int E, float* __restrict__ logits) {
-    using F = RFmt<XBF16>;
-    // one LDS object: slot s = [x: 64 rows x 256 B][gate: 4 experts x kK floats]
-    __shared__ __align__(16) uint8_t ring[kRouterSlots * F::kSlotBytes];
+// x elements of one window as fp32, produced by asm so that the compiler can
+// neither recompute nor copy them next to a DPP read.  bf16: element 2p is
+// the low half of word p (shift), 2p+1 the high half (mask); both exact.
+__device__ inline void r_elements(float (&c)[8], const ru32x4_t (&w)[1]) {
+    asm volatile(
+        "v_lshlrev_b32 %0, 16, %8\n\t"
+        "v_and_b32 %1, 0xffff0000, %8\n\t"
+        "v_lshlrev_b32 %2, 16, %9\n\t"
+        "v_and_b32 %3, 0xffff0000, %9\n\t"
+        "v_lshlrev_b32 %4, 16, %10\n\t"
+        "v_and_b32 %5, 0xffff0000, %10\n\t"
+        "v_lshlrev_b32 %6, 16, %11\n\t"
+        "v_and_b32 %7, 0xffff0000, %11\n\t"
+        : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(c[4]), "=&v"(c[5]), "=&v"(c[6]), "=&v"(c[7])
+        : "v"(w[0][0]), "v"(w[0][1]), "v"(w[0][2]), "v"(w[0][3]));
+}
+__device__ inline void r_elements(float (&c)[8], const ru32x4_t (&w)[2]) {
+    asm volatile(
+        "v_mov_b32 %0, %8\n\t"
+        "v_mov_b32 %1, %9\n\t"
+        "v_mov_b32 %2, %10\n\t"
+        "v_mov_b32 %3, %11\n\t"
+        "v_mov_b32 %4, %12\n\t"
+        "v_mov_b32 %5, %13\n\t"
+        "v_mov_b32 %6, %14\n\t"
+        "v_mov_b32 %7, %15\n\t"
+        : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(c[4]), "=&v"(c[5]), "=&v"(c[6]), "=&v"(c[7])
+        : "v"(w[0][0]), "v"(w[0][1]), "v"(w[0][2]), "v"(w[0][3]), "v"(w[1][0]), "v"(w[1][1]), "v"(w[1][2]),
+          "v"(w[1][3]));
+}
 
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int e = blockIdx.y * kRouterExpertsPerBlock + w;
-    const bool active = e < E;  // wave-uniform
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kWave;
-    const int NC = H / F::kK;   // chunks
+// The four gate reads of one 16-step block (byte offsets OFF + m STRIDE from
+// the lane's LDS address), for the first two blocks of a stage.  Reads are
+// issued from asm and waited for inside the chain blocks: the compiler would
+// drain them before every block; the outputs are early-clobber since the data
+// lands after the statement.
+template <int OFF, int STRIDE>
+__device__ inline void r_gate_reads(rf32x4_t (&gd)[4], uint32_t addr) {
+    asm volatile(
+        "ds_read_b128 %0, %4 offset:%5\n\t"
+        "ds_read_b128 %1, %4 offset:%6\n\t"
+        "ds_read_b128 %2, %4 offset:%7\n\t"
+        "ds_read_b128 %3, %4 offset:%8"
+        : "=&v"(gd[0]), "=&v"(gd[1]), "=&v"(gd[2]), "=&v"(gd[3])
+        : "v"(addr), "n"(OFF), "n"(OFF + STRIDE), "n"(OFF + 2 * STRIDE), "n"(OFF + 3 * STRIDE));
+}
+template <int V>
+struct RInt {
+    static constexpr int value = V;
+};
 
-    // x copies: copy j of a chunk fills x bytes [1024 j, 1024 j + 1024) = rows
-    // R j .. R j + R - 1 (R = kRouterRowsPerCopy); wave w issues copies
-    // X w .. X w + X - 1 (X = kRouterXCopies).  Lane i lands at piece
-    // i % kRouterPieces of row R j + i / kRouterPieces and fetches the
-    // logical piece that rpos() places there.  Rows past the end re-read the
-    // last row.
-    const uint8_t* xsrc[kRouterXCopies];
+// One workgroup = 16 tokens x 16 R expert lanes.  logits [rows][E] always;
+// routes [rows][2] and the tile histogram when routes != nullptr.  A ring
+// stage holds GW windows; H is a multiple of GW * 128, so every stage is full
+// and the step sequence has no run-time bounds (the compiler can then count
+// the LDS reads in flight instead of draining them).
+template <bool XBF16, int R, int GW>
+__global__ void __launch_bounds__(256 * R)
+k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, int E,
+         float* __restrict__ logits, uint8_t* __restrict__ routes, uint8_t* __restrict__ tile_bytes) {
+    constexpr int kGW = GW;                    // windows per ring stage
+    constexpr int kWinBytes = 8 * 1024 * R;    // 32 (k/4) x 16 R experts x 16 B
+    constexpr int kElt = XBF16 ? 2 : 4;
+    constexpr int kXv = XBF16 ? 1 : 2;         // 16-byte x loads per lane per window
+    constexpr int kStageBytes = kGW * kWinBytes;
+    static_assert(kStageBytes <= kRStageBytes, "stage geometry");
+    // two LDS objects, so that the compiler sees the stage being filled and
+    // the stage being read as distinct memory
+    __shared__ __align__(16) uint8_t ring0[kStageBytes];
+    __shared__ __align__(16) uint8_t ring1[kStageBytes];
+    __shared__ uint32_t cnt[16 * R];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gr = 4 * w + (lane >> 4);        // row of the workgroup, 0 .. 16R-1
+    const int e = (gr % R) * 16 + (lane & 15); // this lane's expert
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kRTokens + gr / R;
+    const int NW = H / kRWin;
+    const int NG = NW / kGW;
+    if (tid < 16 * R) cnt[tid] = 0u;
+
+    // x: lane i of a row reads elements 8i .. 8i+7 of every window of its
+    // token (rows past the end re-read the last row; their results are
+    // dropped)
+    const uint8_t* xsrc = static_cast<const uint8_t*>(xv) +
+                          ((t < rows ? t : rows - 1) * static_cast<int64_t>(H) + 8 * (lane & 15)) * kElt;
+    // gate copies: copy i of a stage (i = 0 .. 2 kGW - 1) is instruction
+    // a = w + 4R i of the stage and fills bytes [a KB, a KB + 1 KB): window
+    // i / 2 of the stage, piece (w + 4R (i % 2)) * 64 + lane of the window,
+    // i.e. k/4 = piece / 16R and expert piece % 16R.  Padding experts read
+    // row E-1 (unused).
+    const float* gsrc[2];
 #pragma unroll
-    for (int jj = 0; jj < kRouterXCopies; ++jj) {
-        const int r = kRouterRowsPerCopy * (kRouterXCopies * w + jj) + lane / kRouterPieces;
-        const int c = (lane % kRouterPieces) ^ (r & 15);
-        const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
-        xsrc[jj] = static_cast<const uint8_t*>(xv) + row * static_cast<int64_t>(H) * F::kElt + c * 16;
+    for (int p = 0; p < 2; ++p) {
+        const int piece = (w + 4 * R * p) * 64 + lane;
+        const int ge = piece % (16 * R);
+        gsrc[p] = gate + static_cast<int64_t>(ge < E ? ge : E - 1) * H + 4 * (piece / (16 * R));
     }
-    // gate copies: wave w fetches expert e's kK values of the chunk, one
-    // dword per lane per copy (inactive waves fetch a valid row, unused)
-    const float* gsrc = gate + static_cast<int64_t>(active ? e : E - 1) * H + lane;
-    auto issue_chunk = [&](int kc) {
-        uint8_t* slot = ring + (kc % kRouterSlots) * F::kSlotBytes;
+    auto issue_gate = [&](auto par, int g) {
+        uint8_t* slot = decltype(par)::value ? ring1 : ring0;
+        const int v0 = g * kGW;
 #pragma unroll
-        for (int jj = 0; jj < kRouterXCopies; ++jj)
-            __builtin_amdgcn_global_load_lds(APS_RGP(xsrc[jj] + static_cast<int64_t>(kc) * kRouterRowBytes),
-                                             APS_RLP(slot + (kRouterXCopies * w + jj) * 1024), 16, 0, 0);
-#pragma unroll
-        for (int jj = 0; jj < F::kGateDma; ++jj)
-            __builtin_amdgcn_global_load_lds(APS_RGP(gsrc + kc * F::kK + jj * kWave),
-                                             APS_RLP(slot + F::kXBytes + w * F::kK * 4 + jj * 256), 4, 0, 0);
+        for (int i = 0; i < 2 * kGW; ++i)
+            __builtin_amdgcn_global_load_lds(APS_RGP(gsrc[i & 1] + (v0 + i / 2) * kRWin),
+                                             APS_RLP(slot + (w + 4 * R * i) * 1024), 16, 0, 0);
     };
-    // chunk kc landed in this wave's view: wait for its copies (later chunks
-    // may stay in flight), then the barrier makes every wave's copies visible
-    auto chunk_ready = [&](int kc) {
-        const int later = NC - 1 - kc < kRouterSlots - 2 ? NC - 1 - kc : kRouterSlots - 2;
-        if (later >= 2) r_wait_vm<2 * F::kDma>();
-        else if (later == 1) r_wait_vm<F::kDma>();
-        else r_wait_vm<0>();
-        r_barrier();
-    };
-    auto load_block = [&](ru32x4_t (&xp)[F::kPieces], float& g0, float& g1, int kc, int bb) {
-        const uint8_t* slot = ring + (kc % kRouterSlots) * F::kSlotBytes;
+    ru32x4_t xr[2][kGW][kXv];
+    auto issue_x = [&](ru32x4_t (&dst)[kGW][kXv], int g) {
+        const int v0 = g * kGW;
 #pragma unroll
-        for (int p = 0; p < F::kPieces; ++p)
-            xp[p] = *reinterpret_cast<const ru32x4_t*>(slot + rpos(lane, bb * F::kPieces + p));
-        const float* gs = reinterpret_cast<const float*>(slot + F::kXBytes + w * F::kK * 4) + bb * kRouterBlk + (lane & 15);
-        g0 = gs[0];
-        g1 = gs[16];
-    };
-
+        for (int wi = 0; wi < kGW; ++wi)
 #pragma unroll
-    for (int c = 0; c < kRouterSlots - 1; ++c)
-        if (c < NC) issue_chunk(c);
-    chunk_ready(0);
-    if (kRouterSlots - 1 < NC) issue_chunk(kRouterSlots - 1);
+            for (int p = 0; p < kXv; ++p)
+                dst[wi][p] = *reinterpret_cast<const ru32x4_t*>(xsrc + (v0 + wi) * kRWin * kElt + p * 16);
+    };
+    // gate values of block b (window b / 8, steps 16 (b % 8) .. +15) of a
+    // stage: piece (4 (b % 8) + m) * 16R + e of window b / 8, i.e. byte
+    // gate_off(b) + m * kGateStride from the lane's address
+    const uint32_t gaddr0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(APS_RLP(ring0))) + e * 16;
+    const uint32_t gaddr1 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(APS_RLP(ring1))) + e * 16;
+    constexpr int kGateStride = 16 * R * 16;  // bytes per k/4 row of a window
+    constexpr auto gate_off = [](int b) constexpr { return (b / 8) * kWinBytes + 4 * (b % 8) * kGateStride; };
+    auto load_gate = [&](rf32x4_t (&gd)[4], uint32_t addr, auto bq) {
+        constexpr int b = decltype(bq)::value;
+        r_gate_reads<gate_off(b), kGateStride>(gd, addr);
+    };
 
     float acc = 0.0f;
-    ru32x4_t xa[F::kPieces], xb[F::kPieces];
-    float ga0, ga1, gb0, gb1;
-    if (active) load_block(xa, ga0, ga1, 0, 0);
-    for (int kc = 0; kc < NC; ++kc) {
-        // register ping-pong: xa holds block bb, xb block bb + 1 (kBpc is even)
+    auto run_stage = [&](auto par, int g) {
+        constexpr int P = decltype(par)::value;
+        constexpr int nb = 8 * kGW;
+        // this stage's x elements, then the next stage's x loads (the x
+        // registers of this stage are free once converted)
+        float c[kGW][8];
 #pragma unroll
-        for (int bb = 0; bb < F::kBpc; bb += 2) {
-            if (active) {
-                r_wait_lgkm0();
-                load_block(xb, gb0, gb1, kc, bb + 1);
-                __builtin_amdgcn_sched_barrier(0);
-                acc = chain_block<XBF16>(acc, ga0, ga1, xa);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            const bool last = bb + 2 == F::kBpc;
-            if (last && kc + 1 < NC) {
-                // chunk kc+1 opens next: this wave's reads of chunk kc are
-                // done once block bb+1 has landed; after the barrier chunk
-                // kc's slot is free for chunk kc + kRouterSlots
-                if (active) r_wait_lgkm0();
-                chunk_ready(kc + 1);
-                if (kc + kRouterSlots < NC) issue_chunk(kc + kRouterSlots);
-            }
-            if (active) {
-                r_wait_lgkm0();
-                if (!last) load_block(xa, ga0, ga1, kc, bb + 2);
-                else if (kc + 1 < NC) load_block(xa, ga0, ga1, kc + 1, 0);
-                __builtin_amdgcn_sched_barrier(0);
-                acc = chain_block<XBF16>(acc, gb0, gb1, xb);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
+        for (int wi = 0; wi < kGW; ++wi) r_elements(c[wi], xr[P][wi]);
+        if (g + 1 < NG) issue_x(xr[P ^ 1], g + 1);
+        const uint32_t gaddr = P ? gaddr1 : gaddr0;
+        rf32x4_t gs[3][4];
+        load_gate(gs[0], gaddr, RInt<0>{});
+        load_gate(gs[1], gaddr, RInt<1>{});
+        rf32x4_t spare[4];  // destinations of the last two blocks' (absent) reads
+        auto step = [&](auto bq) {
+            constexpr int b = decltype(bq)::value;
+            if constexpr (b + 2 < nb)
+                acc = rblock<b, nb, gate_off(b + 2), kGateStride>(acc, c[b / 8], gs[b % 3], gs[(b + 2) % 3], gaddr);
+            else
+                acc = rblock<b, nb, 0, kGateStride>(acc, c[b / 8], gs[b % 3], spare, gaddr);
+        };
+        [&]<int... B>(std::integer_sequence<int, B...>) { (step(RInt<B>{}), ...); }(
+            std::make_integer_sequence<int, 8 * kGW>{});
+        // the next stage's gate and x have landed (every copy, in order);
+        // after the barrier all waves see the gate and this stage's slot is
+        // free for stage g + 2.  Unconditional, so that on every path the x
+        // registers are complete before their next use.
+        r_wait_vm0();
+        r_barrier();
+        if (g + 2 < NG) issue_gate(par, g + 2);
+    };
+
+    // stage 0 needs its gate and x; stage 1's gate copies (the last 2 kGW
+    // per wave) may stay in flight.  With a single stage the second slot is
+    // filled with stage 0 again (unused), so the wait is the same on every
+    // path and the compiler sees the x registers complete.
+    issue_gate(RInt<0>{}, 0);
+    issue_x(xr[0], 0);
+    issue_gate(RInt<1>{}, NG > 1 ? 1 : 0);
+    r_wait_vm<2 * kGW>();
+    r_barrier();
+    for (int g = 0; g < NG; g += 2) {
+        run_stage(RInt<0>{}, g);
+        if (g + 1 < NG) run_stage(RInt<1>{}, g + 1);
     }
-    const int64_t row = row0 + lane;
-    if (active && row < rows) logits[row * E + e] = acc;
+
+    const bool valid = t < rows;
+    if (valid && e < E) logits[t * E + e] = acc;
+    if (routes == nullptr) return;  // kernel-uniform
+
+    // top-2 of the token: its 16 R logits sit in lanes base .. base + 16R - 1
+    const float q = route_quantise(acc);
+    const int base = lane & ~(16 * R - 1);
+    float qs[16 * R];
+#pragma unroll
+    for (int k = 0; k < 16 * R; ++k) qs[k] = __shfl(q, base + k);
+    int first, second;
+    route_greedy_top2<16 * R>(qs, E, first, second);
+    if (valid && lane == base) {
+        routes[2 * t] = static_cast<uint8_t>(first);
+        routes[2 * t + 1] = static_cast<uint8_t>(second);
+    }
+    if (valid && e < E && (e == first || e == second)) atomicAdd(&cnt[e], 1u);
+    __syncthreads();
+    if (tid < E) {
+        // byte (blockIdx % 4) of word [tile][expert]; the last workgroup also
+        // zeroes the bytes of quarters past the end
+        const int sub = blockIdx.x % 4;
+        uint8_t* word = tile_bytes + (static_cast<int64_t>(blockIdx.x / 4) * E + tid) * 4;
+        word[sub] = static_cast<uint8_t>(cnt[tid]);
+        if (blockIdx.x == gridDim.x - 1)
+            for (int s2 = sub + 1; s2 < 4; ++s2) word[s2] = 0;
+    }
 }
 
-// One thread per token; one 64-thread workgroup per 64-token tile.  The
+// Top-2 from logits given by the caller (the reference's k_moe_top2 stage):
+// one thread per token, one 64-thread workgroup per 64-token tile.  The
 // token's E logits are loaded up front (independent loads, one round trip),
-// then quantised and scanned twice.  Writes routes and the tile's per-expert
-// histogram (popcounts of wave ballots: no atomics, deterministic).
+// then quantised and scanned twice.  Writes routes and, when asked, the
+// tile's histogram words (popcounts of wave ballots: no atomics).
 template <int EMAX>
 __global__ void __launch_bounds__(64)
 k_route_top2(const float* __restrict__ logits, int64_t rows, int E, uint8_t* __restrict__ routes,
@@ -290,7 +360,7 @@ k_route_top2(const float* __restrict__ logits, int64_t rows, int E, uint8_t* __r
     if (tile_counts) {
         uint32_t mine = 0;
         for (int e = 0; e < E; ++e) {
-            const uint32_t c = __popcll(__ballot(first == e)) + __popcll(__ballot(second == e));
+            const uint32_t c = tile_quarter_counts(first, second, e);
             if (lane == e) mine = c;
         }
         if (lane < E) tile_counts[tile * E + lane] = mine;
@@ -299,19 +369,33 @@ k_route_top2(const float* __restrict__ logits, int64_t rows, int E, uint8_t* __r
 
 }  // namespace
 
-hipError_t launch_router_logits(const void* x, bool x_bf16, const float* gate, int64_t rows,
-                                int hidden, int experts, float* logits, hipStream_t s) {
+hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t rows, int hidden,
+                         int experts, float* logits, uint8_t* routes, uint32_t* tile_counts,
+                         hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    // whole chunks, and an even number of 32-step blocks
-    if (hidden % (x_bf16 ? RFmt<true>::kK : RFmt<false>::kK) != 0 || experts <= 0) return hipErrorInvalidValue;
-    const dim3 grid(static_cast<unsigned>(ceil_div(rows, kWave)),
-                    static_cast<unsigned>(ceil_div(experts, kRouterExpertsPerBlock)));
-    if (x_bf16)
-        hipLaunchKernelGGL(k_router_logits<true>, grid, dim3(256), 0, s, x, gate, rows, hidden,
-                           experts, logits);
-    else
-        hipLaunchKernelGGL(k_router_logits<false>, grid, dim3(256), 0, s, x, gate, rows, hidden,
-                           experts, logits);
+    if (hidden <= 0 || hidden % (2 * kRWin) != 0 || experts <= 0 || experts > kMaxExperts)
+        return hipErrorInvalidValue;
+    if (routes && (experts < 2 || !tile_counts)) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(ceil_div(rows, kRTokens)));
+    auto* tb = reinterpret_cast<uint8_t*>(tile_counts);
+#define APS_ROUTER_LAUNCH(XB, R, GW)                                                                    \
+    hipLaunchKernelGGL((k_router<XB, R, GW>), grid, dim3(256 * R), 0, s, x, gate, rows, hidden, experts, \
+                       logits, routes, tb)
+    // windows per stage: 512 steps of 16 R experts (32 KB) when H allows
+    const int R = experts <= 16 ? 1 : experts <= 32 ? 2 : 4;
+    const bool wide = hidden % (4 * kRWin) == 0;
+    if (x_bf16) {
+        if (R == 1 && wide) APS_ROUTER_LAUNCH(true, 1, 4);
+        else if (R == 1) APS_ROUTER_LAUNCH(true, 1, 2);
+        else if (R == 2) APS_ROUTER_LAUNCH(true, 2, 2);
+        else APS_ROUTER_LAUNCH(true, 4, 1);
+    } else {
+        if (R == 1 && wide) APS_ROUTER_LAUNCH(false, 1, 4);
+        else if (R == 1) APS_ROUTER_LAUNCH(false, 1, 2);
+        else if (R == 2) APS_ROUTER_LAUNCH(false, 2, 2);
+        else APS_ROUTER_LAUNCH(false, 4, 1);
+    }
+#undef APS_ROUTER_LAUNCH
     return hipGetLastError();
 }
 

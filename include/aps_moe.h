@@ -89,7 +89,8 @@ typedef struct aps_moe_ws_layout {
     size_t total_bytes;
     size_t logits;          /* f32 [rows][E]                        */
     size_t routes;          /* u8  [rows][2], slot 0 = first pick   */
-    size_t tile_counts;     /* u32 [ceil(rows/64)][E]               */
+    size_t tile_counts;     /* u32 [ceil(rows/64)][E]: byte q counts the
+                               routes of tokens 16q..16q+15 of a tile */
     size_t counts;          /* u32 [E]                              */
     size_t offsets;         /* u32 [E+1]                            */
     size_t assignment_rows; /* u32 [2*rows] position -> token       */

@@ -165,6 +165,34 @@ def test_c2_deterministic_and_entry_points_agree(gpu_device):
     w.release()
 
 
+@pytest.mark.parametrize("E", [2, 8, 16, 24, 32, 48, 64])
+@pytest.mark.parametrize("H", [256, 1280, 2048])
+def test_router_kernel_shapes(gpu_device, E, H):
+    """Every router kernel variant: 1, 2 or 4 rows of 16 lanes per token
+    (E <= 16 / 32 / 64), ring stages of 4, 2 or 1 windows of 128 steps, an
+    odd stage count (H = 1280), fp32 and bf16 x.  Logits bit-exact from the
+    staged entry point; logits, routes, counts and permutation bit-exact from
+    the fused forward, whose router also writes the routes and the tile
+    histogram.  T = 333 leaves a partial 16-token workgroup and a partial
+    64-token tile."""
+    T = 333
+    for dtype in ("f32", "bf16"):
+        note(f"router T={T} H={H} E={E} x {dtype}")
+        inp = synth.make_moe_inputs(T=T, H=H, E=E, F=64, dtype=dtype, seed=7 * E + H)
+        x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+        ref = oracle_routing(inp)
+        logits = torch.full((T, E), float("nan"), dtype=torch.float32, device=gpu_device)
+        moe.matmul_transposed_gpu(x, gate, logits)
+        w = weights_for(inp, gpu_device)
+        moe.moe_forward_gpu(x, gate, w)
+        plan = w.plan_views(T)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(logits.cpu().numpy().view(np.uint32), ref["logits"].view(np.uint32))
+        np.testing.assert_array_equal(plan["logits"].cpu().numpy().view(np.uint32), ref["logits"].view(np.uint32))
+        check_plan(plan, ref, T)
+        w.release()
+
+
 @pytest.mark.parametrize("T", [1, 2, 3, 63, 64, 65, 127, 129, 300])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_ragged_rows_small_shapes(gpu_device, T, dtype):
