@@ -163,3 +163,43 @@ def test_fp8_staged_entry_points_are_rejected(gpu_device):
     with pytest.raises(ValueError, match="fp8 weight sets run through"):
         moe.expert_ffn(w, x, off, rows)
     w.release()
+
+
+def test_quantiser_every_bf16_value_at_many_scales(gpu_device):
+    """Every finite bf16 value through aps_quantise_rows_e4m3 at 40 row scales
+    (amax from 2^-133, a subnormal scale, through 2^-80, the smallest scale of
+    the reciprocal path, up to 2^127): each row holds amax and 4095 values of
+    magnitude <= amax, so its scale is amax / 448.  Codes and scales must equal
+    the oracle's quantiser (IEEE division, nearest-even e4m3) bit for bit; this
+    pins the kernel's reciprocal-and-correction quotient, its IEEE fallback for
+    tiny scales and the hardware e4m3 conversion, -0 and subnormals included."""
+    from aps2026_amd import capi
+    note("quantiser: every bf16 value at 40 scales")
+    allv = synth.bf16_bits_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    allv = allv[np.isfinite(allv)]
+    exps = list(range(-133, -120, 3)) + list(range(-92, -76, 2)) + list(range(-60, 128, 7))
+    rows = []
+    for e in exps:
+        amax = np.float32(np.ldexp(np.float32(1.5), e)) if e < 127 else np.float32(np.ldexp(np.float32(1.0), 127))
+        amax = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(np.array([amax], np.float32)))[0]
+        vals = allv[np.abs(allv) <= amax]
+        per = 4095
+        for i in range(0, vals.size, per):
+            chunk = vals[i:i + per]
+            row = np.zeros(4096, np.float32)
+            row[0] = amax
+            row[1:1 + chunk.size] = chunk
+            rows.append(row)
+    x = np.stack(rows)
+    assert np.array_equal(synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(x)), x)  # exact bf16 values
+    want_q, want_s = oracle.quantise_rows_e4m3(x)
+    xd = to_dev_bf16(synth.f32_to_bf16_bits(x), gpu_device)
+    q = torch.empty((x.shape[0], 4096), dtype=torch.uint8, device=gpu_device)
+    s = torch.empty(x.shape[0], dtype=torch.float32, device=gpu_device)
+    rc = capi.lib().aps_quantise_rows_e4m3(xd.data_ptr(), 4096, 4096, q.data_ptr(), 4096, s.data_ptr(),
+                                           x.shape[0], None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    note(f"quantiser: {x.shape[0]} rows")
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), want_s.view(np.uint32))
+    np.testing.assert_array_equal(q.cpu().numpy(), want_q)
