@@ -497,6 +497,36 @@ int aps_moe_combine(const void* y_perm, int32_t y_dtype, const uint32_t* route_p
     return APS_OK;
 }
 
+static int layer_norm_common(float* x, const float* residual, const float* weight, const float* bias,
+                             int64_t rows, int32_t hidden, float eps, float* y, void* stream, const char* what) {
+    if (rows < 0 || hidden <= 0 || hidden % 256 != 0)
+        return fail(APS_ERR_SHAPE, "%s shape: rows %lld hidden %d (hidden must be a multiple of 256)", what,
+                    (long long)rows, hidden);
+    if (rows > 0 && (!x || !weight || !bias || !y)) return fail(APS_ERR_ARG, "%s: NULL pointer", what);
+    if (residual == nullptr && std::strcmp(what, "add layer norm") == 0)
+        return fail(APS_ERR_ARG, "%s: NULL residual", what);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) |
+                           reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
+                           reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+    if (!aligned) return fail(APS_ERR_ARG, "%s: arrays must be 16-byte aligned", what);
+    if (rows > 0 && (y == x || (residual && y == residual)))
+        return fail(APS_ERR_ARG, "%s: y must not alias x or the residual", what);
+    APS_HIP(aps::launch_layer_norm(x, residual, weight, bias, y, rows, hidden, eps, static_cast<hipStream_t>(stream)),
+            "layer norm launch");
+    return APS_OK;
+}
+
+int aps_layer_norm(const float* x, const float* weight, const float* bias, int64_t rows, int32_t hidden, float eps,
+                   float* y, void* stream) {
+    return layer_norm_common(const_cast<float*>(x), nullptr, weight, bias, rows, hidden, eps, y, stream,
+                             "layer norm");
+}
+
+int aps_add_layer_norm(float* x, const float* residual, const float* weight, const float* bias, int64_t rows,
+                       int32_t hidden, float eps, float* y, void* stream) {
+    return layer_norm_common(x, residual, weight, bias, rows, hidden, eps, y, stream, "add layer norm");
+}
+
 static int forward_common(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows, void* out,
                           int32_t out_dtype, void* workspace, size_t workspace_bytes,
                           const WeightSet** w_out, aps_moe_ws_layout* L) {

@@ -122,6 +122,10 @@ hipError_t launch_route_top2(const float* logits, int64_t rows, int experts, uin
                              uint32_t* tile_counts, hipStream_t s);
 hipError_t launch_tile_hist(const uint8_t* routes, int64_t rows, int experts,
                             uint32_t* tile_counts, hipStream_t s);
+// Decoder-layer LayerNorm (residual == nullptr: plain; else x += residual
+// in place first).  hidden % 256 == 0.
+hipError_t launch_layer_norm(float* x, const float* residual, const float* weight, const float* bias, float* y,
+                             int64_t rows, int hidden, float eps, hipStream_t s);
 hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_counts,
                                    int64_t rows, int experts, uint32_t* counts,
                                    uint32_t* offsets, uint32_t* assignment_rows,

@@ -181,10 +181,47 @@ def matmul_transposed_gpu(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor) -> 
     return c
 
 
-def _check_x(x: torch.Tensor, w: MoeWeights):
+NORM_EPS = 1.0e-5  # reference include/config.h:19
+
+
+def _check_ln(x, weight, bias, y, what, residual=None):
+    _require(x.dim() >= 1 and x.dtype == torch.float32 and x.is_contiguous(), f"{what} shape")
+    h = x.shape[-1]
+    for t in (weight, bias):
+        _require(t.dtype == torch.float32 and t.is_contiguous() and t.numel() == h, f"{what} shape")
+    _require(y.dtype == torch.float32 and y.is_contiguous() and y.numel() == x.numel(), f"{what} shape")
+    if residual is not None:
+        _require(residual.dtype == torch.float32 and residual.is_contiguous() and residual.numel() == x.numel(),
+                 f"{what} shape")
+    return x.numel() // h, h
+
+
+def layer_norm_gpu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float, y: torch.Tensor):
+    """y = LayerNorm(x) over the last dimension with the reference GPU kernel's
+    arithmetic (serial ascending sums, fused variance chain).  reference
+    include/tensor.h:86-87, src/tensor.cu:3262-3280."""
+    rows, h = _check_ln(x, weight, bias, y, "layer norm")
+    _call(capi.lib().aps_layer_norm(_ptr(x), _ptr(weight), _ptr(bias), rows, h, eps, _ptr(y), _stream(x.device)))
+    return y
+
+
+def add_layer_norm_gpu(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                       eps: float, y: torch.Tensor):
+    """x += residual in place, then y = LayerNorm(x).  reference
+    include/tensor.h:88-90, src/tensor.cu:3282-3295."""
+    rows, h = _check_ln(x, weight, bias, y, "add layer norm", residual)
+    _call(capi.lib().aps_add_layer_norm(_ptr(x), _ptr(residual), _ptr(weight), _ptr(bias), rows, h, eps, _ptr(y),
+                                        _stream(x.device)))
+    return y
+
+
+def _check_x(x: torch.Tensor, w: MoeWeights, allow_f32: bool = False):
+    """allow_f32: the fused entry points also take fp32 x with a bf16 weight
+    set (the reference's activations are fp32); the FFN then reads a bf16 copy."""
     _require(x.dim() == 2 and x.shape[1] == w.hidden and x.is_contiguous() and x.is_cuda,
              "grouped MoE shape or handle")
-    _require(x.dtype == w.x_dtype, f"x must be {w.x_dtype} for this weight set")
+    ok = x.dtype == w.x_dtype or (allow_f32 and x.dtype == torch.float32 and w.compute_dtype == torch.bfloat16)
+    _require(ok, f"x must be {w.x_dtype} for this weight set")
 
 
 def _out(x: torch.Tensor, w: MoeWeights, out: Optional[torch.Tensor], out_dtype: Optional[torch.dtype]):
@@ -200,7 +237,7 @@ def moe_forward_grouped_gpu(x: torch.Tensor, router: torch.Tensor, weights: MoeW
                             out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """reference include/tensor.h:146-147: routing from precomputed router
     logits [rows, E], then dispatch, grouped expert FFN and combine."""
-    _check_x(x, weights)
+    _check_x(x, weights, allow_f32=True)
     rows = x.shape[0]
     _require(router.dim() == 2 and tuple(router.shape) == (rows, weights.num_experts) and
              router.dtype == torch.float32 and router.is_contiguous(), "grouped MoE shape or handle")
@@ -217,7 +254,7 @@ def moe_forward_gpu(x: torch.Tensor, gate: torch.Tensor, weights: MoeWeights,
                     out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """Router GEMM + grouped path in one call (the GPU branch of
     PhiMoE::forward, reference src/layer.cu:113-121)."""
-    _check_x(x, weights)
+    _check_x(x, weights, allow_f32=True)
     _require(tuple(gate.shape) == (weights.num_experts, weights.hidden) and gate.dtype == torch.float32
              and gate.is_contiguous(), "router gate shape")
     out = _out(x, weights, out, out_dtype)

@@ -245,6 +245,24 @@ APS_API size_t aps_mlp_workspace_size(uint64_t handle, int64_t rows);
 APS_API int aps_mlp_forward(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows, void* out,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- decoder-layer LayerNorm (the MoE block's input) -------------------- */
+
+/* Replaces tensor_ops::layer_norm_gpu (reference include/tensor.h:86-87,
+ * src/tensor.cu:3262-3280, kernel src/tensor.cu:2121-2140): per row of
+ * `hidden` fp32 values, mean and variance as single fp32 chains in ascending
+ * order (sum += v; var = fma(v - mean, v - mean, var)), inv = 1 / sqrt(var /
+ * hidden + eps), y = fma((v - mean) * inv, weight, bias) -- the reference
+ * GPU kernel's arithmetic, bit for bit.  hidden % 256 == 0; arrays 16-byte
+ * aligned; y must not alias x. */
+APS_API int aps_layer_norm(const float* x, const float* weight, const float* bias, int64_t rows,
+                           int32_t hidden, float eps, float* y, void* stream);
+
+/* Replaces tensor_ops::add_layer_norm_gpu (reference include/tensor.h:88-90,
+ * src/tensor.cu:3282-3295, kernel src/tensor.cu:2144-2178): x += residual
+ * in place (one fp32 add per element), then y = LayerNorm(x) as above. */
+APS_API int aps_add_layer_norm(float* x, const float* residual, const float* weight, const float* bias,
+                               int64_t rows, int32_t hidden, float eps, float* y, void* stream);
+
 /* ---- diagnostics ------------------------------------------------------- */
 
 APS_API const char* aps_moe_last_error(void);

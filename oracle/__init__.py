@@ -55,6 +55,8 @@ def lib():
         L.oracle_bf16_to_f32.argtypes = [_u16p, _f32p, _i64]
         L.oracle_e4m3_to_f32.argtypes = [_u8p, _f32p, _i64]
         L.oracle_quantise_rows_e4m3.argtypes = [_f32p, _i64, _i32, _u8p, _f32p]
+        L.oracle_layer_norm.argtypes = [_f32p, ctypes.c_void_p, _i64, _i32, _f32p, _f32p, ctypes.c_float,
+                                        ctypes.c_void_p, _f32p, ctypes.c_void_p, ctypes.c_void_p]
         L.oracle_default_quantum.restype = ctypes.c_float
         L.oracle_default_tie_eps.restype = ctypes.c_float
         L.oracle_num_threads.restype = ctypes.c_int
@@ -228,3 +230,26 @@ def reference_path(x, gate, w1, w3, w2):
     out = combine(y, routes, pos)
     return dict(logits=logits, routes=routes, counts=counts, offsets=offsets,
                 assignment_rows=rows, route_positions=pos, y=y, out=out)
+
+
+def layer_norm(x: np.ndarray, weight: np.ndarray, bias: np.ndarray, eps: float = 1e-5,
+               residual: Optional[np.ndarray] = None):
+    """The decoder layer's LayerNorm with the reference GPU kernels' operation
+    order (moe_oracle.c, oracle_layer_norm).  With ``residual`` it is
+    add_layer_norm: v = x + residual.  Returns (y, v, mean, inv), all float32."""
+    x = _c(x, np.float32)
+    rows, h = x.shape
+    w = _c(weight, np.float32)
+    b = _c(bias, np.float32)
+    res = None if residual is None else _c(residual, np.float32)
+    if res is not None and res.shape != x.shape:
+        raise ValueError("add layer norm shape")
+    if w.shape != (h,) or b.shape != (h,):
+        raise ValueError("layer norm shape")
+    y = np.empty_like(x)
+    v = np.empty_like(x)
+    mean = np.empty(rows, np.float32)
+    inv = np.empty(rows, np.float32)
+    lib().oracle_layer_norm(x, None if res is None else res.ctypes.data, rows, h, w, b, np.float32(eps),
+                            v.ctypes.data, y, mean.ctypes.data, inv.ctypes.data)
+    return y, v, mean, inv

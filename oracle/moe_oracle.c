@@ -430,3 +430,48 @@ ORACLE_API void oracle_quantise_rows_e4m3(const float* src, int64_t rows, int32_
         }
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* LayerNorm of the decoder layer (the MoE block's input), GPU-path semantics:
+ * src/tensor.cu:2144-2178 (k_add_layer_norm: v = x + residual, written back
+ * to x), src/tensor.cu:2121-2140 (k_layer_norm), with ln_moments / ln_serial_sum
+ * / ln_serial_var / ln_write at src/tensor.cu:2056-2119 and 2032-2055:
+ *   sum  = fp32 adds of v[j], j ascending, +0 init      mean = sum / h
+ *   var  = fma(t, t, var), t = v[j] - mean, j ascending (nvcc contracts
+ *          `var += t * t`), +0 init
+ *   inv  = 1 / sqrtf(var / h + eps)     (IEEE division and square root)
+ *   y[j] = fma((v[j] - mean) * inv, w[j], b[j])   (`... * w + b` contracted)
+ * The CPU twin (src/tensor.cu:327-341) sums in the same order.  x_out
+ * (optional) receives v; residual may be NULL (plain LayerNorm).  mean_out and
+ * inv_out (optional) receive the row statistics. */
+ORACLE_API void oracle_layer_norm(const float* x, const float* residual, int64_t rows, int32_t h,
+                                  const float* w, const float* b, float eps, float* x_out, float* y,
+                                  float* mean_out, float* inv_out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * h;
+        const float* rr = residual ? residual + r * h : NULL;
+        float* vr = x_out ? x_out + r * h : NULL;
+        float sum = 0.0f;
+        for (int32_t j = 0; j < h; ++j) {
+            const float v = rr ? xr[j] + rr[j] : xr[j];
+            if (vr) vr[j] = v;
+            sum += v;
+        }
+        const float mean = sum / (float)h;
+        float var = 0.0f;
+        for (int32_t j = 0; j < h; ++j) {
+            const float v = rr ? xr[j] + rr[j] : xr[j];
+            const float t = v - mean;
+            var = fmaf(t, t, var);
+        }
+        const float inv = 1.0f / sqrtf(var / (float)h + eps);
+        if (mean_out) mean_out[r] = mean;
+        if (inv_out) inv_out[r] = inv;
+        for (int32_t j = 0; j < h; ++j) {
+            const float v = rr ? xr[j] + rr[j] : xr[j];
+            const float a = (v - mean) * inv;
+            y[r * h + j] = fmaf(a, w[j], b[j]);
+        }
+    }
+}

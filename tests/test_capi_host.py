@@ -12,7 +12,7 @@ from aps2026_amd import capi, moe
 def test_library_exports_every_declared_symbol():
     L = capi.lib()
     names = capi.declared_symbols()
-    assert len(names) == 20
+    assert len(names) == 22
     for n in names:
         assert hasattr(L, n), n
     assert L.aps_moe_abi_version() == 1
@@ -69,6 +69,11 @@ def test_stage_argument_checks():
     assert L.aps_router_logits(None, capi.DTYPE_F32, None, 8, 4096, 16, None, None) == capi.APS_ERR_ARG
     assert L.aps_router_logits(None, capi.DTYPE_F32, None, 0, 4096, 16, None, None) == capi.APS_OK
     assert L.aps_moe_route_top2(None, 8, 1, None, None) == capi.APS_ERR_SHAPE
+    assert L.aps_layer_norm(None, None, None, 8, 100, 1e-5, None, None) == capi.APS_ERR_SHAPE
+    assert L.aps_layer_norm(None, None, None, 8, 4096, 1e-5, None, None) == capi.APS_ERR_ARG
+    assert L.aps_layer_norm(None, None, None, 0, 4096, 1e-5, None, None) == capi.APS_OK
+    assert L.aps_add_layer_norm(None, None, None, None, -1, 4096, 1e-5, None, None) == capi.APS_ERR_SHAPE
+    assert "add layer norm shape" in capi.last_error()
     assert L.aps_moe_combine(None, capi.DTYPE_BF16, None, 8, 12, None, capi.DTYPE_BF16, None) == capi.APS_ERR_SHAPE
     assert L.aps_moe_combine(None, capi.DTYPE_E4M3, None, 8, 16, None, capi.DTYPE_BF16, None) == capi.APS_ERR_DTYPE
     assert L.aps_moe_dispatch(None, 8, 16, None, None, None, None, None, 0, None) == capi.APS_ERR_ARG

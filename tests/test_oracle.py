@@ -332,3 +332,105 @@ def test_fp8_ffn_matches_fp64_textbook_pipeline():
     err = np.linalg.norm(y - yt, axis=1) / np.linalg.norm(yt, axis=1)
     assert err.max() < 2e-2, err.max()
     assert np.abs(act_b - a).max() <= np.abs(a).max() * 2.0 ** -7
+
+
+# ---- LayerNorm of the decoder layer (the MoE input) -------------------------
+
+def _ln_params(h, seed=0):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal(h).astype(np.float32), rng.standard_normal(h).astype(np.float32))
+
+
+def test_layer_norm_constant_row_gives_bias():
+    """A constant row has mean = the constant (2048 / 4096 exactly here),
+    every deviation 0, so y = fma(0, w, b) = b whatever inv is."""
+    h = 4096
+    w, b = _ln_params(h)
+    x = np.full((2, h), 0.5, np.float32)
+    y, v, mean, inv = oracle.layer_norm(x, w, b)
+    assert np.array_equal(mean, np.float32([0.5, 0.5]))
+    np.testing.assert_array_equal(y, np.stack([b, b]))
+    assert np.array_equal(v, x)
+
+
+def test_layer_norm_mean_sums_in_ascending_order():
+    """[1e8, 1, -1e8, 0...] and [1e8, -1e8, 1, 0...] hold the same values; summed
+    left to right the first loses the 1 (1e8 + 1 rounds to 1e8) and the second
+    keeps it, so the means are 0 and 2^-12.  Any order-free sum gives both the
+    same mean."""
+    h = 4096
+    w, b = _ln_params(h, 1)
+    x = np.zeros((2, h), np.float32)
+    x[0, :3] = [1e8, 1.0, -1e8]
+    x[1, :3] = [1e8, -1e8, 1.0]
+    _, _, mean, _ = oracle.layer_norm(x, w, b)
+    assert mean[0] == 0.0 and mean[1] == np.float32(2.0 ** -12)
+
+
+def test_layer_norm_variance_is_a_fused_chain():
+    """Row [a, -a, c, -c, 0...] has mean 0 exactly.  The variance accumulated as
+    fma(t, t, var) and as var + RN(t * t) differ for these a, c (found by
+    search and re-derived here with exact rational IEEE arithmetic), and so do
+    the resulting inv; the oracle must give the fused one (nvcc contracts
+    `var += t * t`)."""
+    import math
+    from fractions import Fraction as Fr
+    f32, from_float = ieee32.f32, ieee32.from_float
+    h = 4096
+    a = np.uint32(1067587382).view(np.float32)
+    c = np.uint32(1070634225).view(np.float32)
+    ts = [from_float(float(v)) for v in (a, -a, c, -c)]
+    var_f, var_u = Fr(0), Fr(0)
+    for t in ts:
+        var_f = f32(t * t + var_f)
+        var_u = f32(var_u + f32(t * t))
+    assert var_f != var_u
+
+    def inv_of(var):
+        q = f32(f32(var / h) + from_float(float(np.float32(1e-5))))
+        s0 = np.float32(math.sqrt(float(q)))
+        cands = [np.nextafter(s0, np.float32(-1)), s0, np.nextafter(s0, np.float32(1e30))]
+        s = min((Fr(float(v)) for v in cands), key=lambda v: abs(v * v - q))
+        return f32(Fr(1) / s)
+
+    assert inv_of(var_f) != inv_of(var_u)
+    x = np.zeros((1, h), np.float32)
+    x[0, :4] = [a, -a, c, -c]
+    w, b = _ln_params(h, 2)
+    _, _, mean, inv = oracle.layer_norm(x, w, b)
+    assert mean[0] == 0.0
+    assert Fr(float(inv[0])) == inv_of(var_f)
+
+
+def test_layer_norm_unit_variance_closed_form():
+    """eps = 0 and a row of +-1: mean 0, var = h, inv = 1 exactly, so
+    y = fma(v, w, b) elementwise."""
+    h = 1024
+    rng = np.random.default_rng(3)
+    w, b = _ln_params(h, 3)
+    x = np.where(np.arange(h) % 2 == 0, 1.0, -1.0).astype(np.float32)[None, :]
+    y, _, mean, inv = oracle.layer_norm(x, w, b, eps=0.0)
+    assert mean[0] == 0.0 and inv[0] == 1.0
+    want = (x[0].astype(np.float64) * w + b).astype(np.float32)  # one rounding: fma
+    np.testing.assert_array_equal(y[0], want)
+
+
+def test_add_layer_norm_residual_and_fp64_bound():
+    """v = x + residual elementwise (one fp32 add each, returned as the updated
+    x); y within 1e-5 relative (normwise per row) of a float64 LayerNorm of v."""
+    rng = np.random.default_rng(4)
+    rows, h = 16, 4096
+    x = rng.standard_normal((rows, h)).astype(np.float32)
+    r = rng.standard_normal((rows, h)).astype(np.float32)
+    w, b = _ln_params(h, 4)
+    y, v, mean, inv = oracle.layer_norm(x, w, b, residual=r)
+    np.testing.assert_array_equal(v, x + r)
+    vd = v.astype(np.float64)
+    md = vd.mean(1, keepdims=True)
+    yd = (vd - md) / np.sqrt(((vd - md) ** 2).mean(1, keepdims=True) + 1e-5) * w + b
+    err = np.linalg.norm(y - yd, axis=1) / np.linalg.norm(yd, axis=1)
+    assert err.max() < 1e-5
+    # rows are independent: a permutation of the rows permutes the outputs
+    p = rng.permutation(rows)
+    y2, _, _, _ = oracle.layer_norm(x[p], w, b, residual=r[p])
+    np.testing.assert_array_equal(y2, y[p])
