@@ -228,6 +228,33 @@ void matmul_transposed_gpu(const Tensor& a, const Tensor& b, Tensor& c) {
     if (rc) throw_status(rc, "matmul_transposed_gpu");
 }
 
+void layer_norm_gpu(const Tensor& x, const Tensor& weight, const Tensor& bias, float eps, Tensor& y) {
+    const std::size_t h = x.size(x.ndim() - 1);
+    const std::size_t rows = x.size() / h;
+    if (weight.size() != h || bias.size() != h || y.size() != x.size())
+        throw std::invalid_argument("layer norm shape");
+    if (h % 256 != 0) throw std::invalid_argument("layer_norm_gpu: this build needs the last dimension % 256 == 0");
+    const float* dx = x.cuda_data();
+    const int rc = aps_layer_norm(dx, weight.cuda_data(), bias.cuda_data(), static_cast<int64_t>(rows),
+                                  static_cast<int32_t>(h), eps, y.cuda_data_write(), nullptr);
+    if (rc) throw_status(rc, "layer_norm_gpu");
+}
+
+void add_layer_norm_gpu(Tensor& x, const Tensor& residual, const Tensor& weight, const Tensor& bias, float eps,
+                        Tensor& y) {
+    const std::size_t h = x.size(x.ndim() - 1);
+    const std::size_t rows = x.size() / h;
+    if (residual.size() != x.size() || weight.size() != h || bias.size() != h || y.size() != x.size())
+        throw std::invalid_argument("add layer norm shape");
+    if (h % 256 != 0)
+        throw std::invalid_argument("add_layer_norm_gpu: this build needs the last dimension % 256 == 0");
+    x.cuda_data();  // upload if the host copy is the valid one, then write in place
+    const int rc = aps_add_layer_norm(x.cuda_data_write(), residual.cuda_data(), weight.cuda_data(),
+                                      bias.cuda_data(), static_cast<int64_t>(rows), static_cast<int32_t>(h), eps,
+                                      y.cuda_data_write(), nullptr);
+    if (rc) throw_status(rc, "add_layer_norm_gpu");
+}
+
 std::size_t register_moe_weights_gpu(const std::vector<const Tensor*>& w1, const std::vector<const Tensor*>& w2,
                                      const std::vector<const Tensor*>& w3, aps_dtype compute) {
     if (w1.size() != apss26::NUM_EXPERTS || w2.size() != apss26::NUM_EXPERTS || w3.size() != apss26::NUM_EXPERTS)

@@ -1,6 +1,6 @@
 // Model constants of the MoE block, under the reference's names
 // (include/config.h:5-27 of the reference: namespace apss26).  Only the
-// constants the MoE feed-forward path reads are kept here.
+// constants the MoE feed-forward path and its LayerNorm read are kept here.
 #pragma once
 
 #include <cstddef>
@@ -15,4 +15,6 @@ constexpr std::size_t EXPERT_INTERMEDIATE_SIZE = 448;
 // score is larger by more than ROUTER_TIE_EPS.
 constexpr float ROUTER_SCORE_QUANTUM = 1.0e-3f;
 constexpr float ROUTER_TIE_EPS = 2.0e-2f;
+// LayerNorm epsilon of the decoder layer (reference include/config.h:19).
+constexpr float NORM_EPS = 1.0e-5f;
 }  // namespace apss26

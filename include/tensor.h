@@ -103,4 +103,17 @@ std::size_t register_moe_weights_gpu(const std::vector<const Tensor*>& w1,
 // for a router of the wrong shape or an invalid handle.
 void moe_forward_grouped_gpu(const Tensor& x, const Tensor& router, std::size_t weights_handle, Tensor& out);
 
+// y = LayerNorm(x) over the last dimension (reference include/tensor.h:86-87,
+// src/tensor.cu:3262-3280): both row sums serial in ascending order, as the
+// reference GPU kernel.  y must already have x's size.  Throws
+// std::invalid_argument("layer norm shape") for mismatched sizes; this
+// build needs the last dimension to be a multiple of 256.
+void layer_norm_gpu(const Tensor& x, const Tensor& weight, const Tensor& bias, float eps, Tensor& y);
+
+// x += residual, then y = LayerNorm(x) (reference include/tensor.h:88-90,
+// src/tensor.cu:3282-3295).  Throws std::invalid_argument("add layer norm
+// shape") for mismatched sizes.
+void add_layer_norm_gpu(Tensor& x, const Tensor& residual, const Tensor& weight, const Tensor& bias, float eps,
+                        Tensor& y);
+
 }  // namespace tensor_ops

@@ -127,6 +127,21 @@ int main(int argc, char** argv) {
     Tensor logits({T, E});
     tensor_ops::matmul_transposed_gpu(x, gate, logits);
 
+    // --- decoder-layer LayerNorm: plain, and x += residual in place ----------
+    Tensor ln_w = random_tensor({H}, rng, 1.0f), ln_b = random_tensor({H}, rng, 0.1f);
+    Tensor resid = random_tensor({T, H}, rng, 1.0f);
+    Tensor ln_y({T, H}), ln_x = x, add_y({T, H});
+    tensor_ops::layer_norm_gpu(x, ln_w, ln_b, apss26::NORM_EPS, ln_y);
+    tensor_ops::add_layer_norm_gpu(ln_x, resid, ln_w, ln_b, apss26::NORM_EPS, add_y);
+    {
+        Tensor bad({T, H - 1});
+        expect_throw<std::invalid_argument>([&] { tensor_ops::layer_norm_gpu(x, ln_w, ln_b, 1e-5f, bad); },
+                                            "layer norm shape", "layer norm shape");
+        expect_throw<std::invalid_argument>(
+            [&] { tensor_ops::add_layer_norm_gpu(ln_x, bad, ln_w, ln_b, 1e-5f, add_y); }, "add layer norm shape",
+            "add layer norm shape");
+    }
+
     // --- Tensor synchronisation rules ----------------------------------------
     {
         Tensor t({4, 8});
@@ -183,6 +198,12 @@ int main(int argc, char** argv) {
     write_raw(dir, "y_bf16", y16);
     write_raw(dir, "mlp_y", ymlp);
     write_raw(dir, "logits", logits);
+    write_raw(dir, "ln_w", ln_w);
+    write_raw(dir, "ln_b", ln_b);
+    write_raw(dir, "resid", resid);
+    write_raw(dir, "ln_y", ln_y);
+    write_raw(dir, "ln_x", ln_x);
+    write_raw(dir, "add_y", add_y);
     std::printf("layer_check: %d failure(s)\n", g_failures);
     return g_failures ? 1 : 0;
 }

@@ -40,7 +40,9 @@ def run(tmp_path_factory, gpu_device):
 
     d = {"x": load("x", (T, H)), "gate": load("gate", (E, H)), "w1": load("w1", (E, F, H)),
          "w2": load("w2", (E, H, F)), "w3": load("w3", (E, F, H)), "y_f32": load("y_f32", (T, H)),
-         "y_bf16": load("y_bf16", (T, H)), "mlp_y": load("mlp_y", (T, H)), "logits": load("logits", (T, E))}
+         "y_bf16": load("y_bf16", (T, H)), "mlp_y": load("mlp_y", (T, H)), "logits": load("logits", (T, E)),
+         "ln_w": load("ln_w", (H,)), "ln_b": load("ln_b", (H,)), "resid": load("resid", (T, H)),
+         "ln_y": load("ln_y", (T, H)), "ln_x": load("ln_x", (T, H)), "add_y": load("add_y", (T, H))}
     d["ref"] = oracle.reference_path(d["x"], d["gate"], d["w1"], d["w3"], d["w2"])
     return d
 
@@ -62,3 +64,13 @@ def test_phimoe_bf16_within_tolerance(run):
     ref = run["ref"]["out"]
     err = np.linalg.norm(run["y_bf16"] - ref, axis=1) / np.maximum(np.linalg.norm(ref, axis=1), 1e-30)
     assert err.max() <= 2e-2, err.max()
+
+
+def test_layer_norm_ops_bit_exact(run):
+    """tensor_ops::layer_norm_gpu and add_layer_norm_gpu through the C++ API:
+    y, and the in-place x += residual, equal the oracle bit for bit."""
+    y, _, _, _ = oracle.layer_norm(run["x"], run["ln_w"], run["ln_b"], eps=1e-5)
+    assert np.array_equal(run["ln_y"].view(np.uint32), y.view(np.uint32))
+    y2, v, _, _ = oracle.layer_norm(run["x"], run["ln_w"], run["ln_b"], eps=1e-5, residual=run["resid"])
+    assert np.array_equal(run["ln_x"].view(np.uint32), v.view(np.uint32))
+    assert np.array_equal(run["add_y"].view(np.uint32), y2.view(np.uint32))
