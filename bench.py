@@ -2,6 +2,12 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 
+`--config c3` times the decoder layer's post-attention half instead:
+add_layer_norm (attention output += residual stream, LayerNorm with the
+reference kernel's serial sums) feeding the same MoE block, fp32 activations
+with bf16 experts (synthetic attention output; the attention itself is not
+built).
+
 One step = one full MoE block (router GEMM, quantised top-2, dispatch,
 grouped w1||w3 + SwiGLU, grouped w2, combine) over one batch of synthetic
 tokens already resident in HBM.  Workload (default): benchmark config C2 --
@@ -55,7 +61,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c5"])
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline: repeat full-batch runs until this much time is spent (at least 2 runs)")
@@ -76,7 +82,8 @@ def main():
     from aps2026_amd import capi, moe, synth
 
     dev = torch.device("cuda:0")
-    inp = synth.make_config(args.config)
+    c3 = args.config == "c3"
+    inp = synth.make_config("c2" if c3 else args.config)
     T, H, E, F = inp.T, inp.H, inp.E, inp.F
     A = 2 * T
     fp8 = inp.dtype == "fp8"
@@ -86,7 +93,15 @@ def main():
     def dev_bits(bits):
         return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(dev).view(torch.bfloat16)
 
-    if bf16:
+    if c3:
+        # residual stream and attention output, fp32 (the reference's activations)
+        g = torch.Generator(device="cpu").manual_seed(3)
+        resid = (0.5 * torch.randn(T, H, generator=g)).to(dev)
+        attn = (0.5 * torch.randn(T, H, generator=g)).to(dev)
+        ln_w = (1.0 + 0.05 * torch.randn(H, generator=g)).to(dev)
+        ln_b = (0.05 * torch.randn(H, generator=g)).to(dev)
+        x = torch.empty(T, H, dtype=torch.float32, device=dev)  # post-attention LayerNorm output
+    elif bf16:
         x = dev_bits(inp.packed["x_bf16"])
     else:
         x = torch.from_numpy(inp.x).to(dev)
@@ -125,11 +140,22 @@ def main():
     stream = torch.cuda.current_stream(dev)
     sptr = ctypes.c_void_p(stream.cuda_stream)
     xd = capi.DTYPE_BF16 if bf16 else capi.DTYPE_F32
+    if c3:
+        out = torch.empty((T, H), dtype=torch.float32, device=dev)
+        xd = capi.DTYPE_F32
     args_fwd = [(w.handle, ctypes.c_void_p(x.data_ptr()), xd, ctypes.c_void_p(gate.data_ptr()), T,
                  ctypes.c_void_p(out.data_ptr()), xd, ctypes.c_void_p(ws.data_ptr()), ws.numel(), sptr)
                 for w in layers]
+    if c3:
+        args_ln = (ctypes.c_void_p(attn.data_ptr()), ctypes.c_void_p(resid.data_ptr()),
+                   ctypes.c_void_p(ln_w.data_ptr()), ctypes.c_void_p(ln_b.data_ptr()), T, H,
+                   ctypes.c_float(moe.NORM_EPS), ctypes.c_void_p(x.data_ptr()), sptr)
 
     def step(i):
+        if c3:
+            rc = L.aps_add_layer_norm(*args_ln)
+            if rc:
+                raise RuntimeError(capi.last_error())
         rc = L.aps_moe_forward(*args_fwd[i % LAYERS])
         if rc:
             raise RuntimeError(capi.last_error())
@@ -168,13 +194,18 @@ def main():
                   "combine"]
     else:
         stages = ["router_logits", "route_top2", "dispatch", "ffn_up", "ffn_down", "combine"]
+    if c3:
+        stages = ["add_layer_norm"] + stages
+        L.aps_add_layer_norm(*args_ln)
+        xb = x.to(torch.bfloat16)  # the FFN's bf16 copy of the norm output (the fused path makes its own)
     times = {s: [] for s in stages}
     n_stage = max(args.steps, 10)
     for i in range(n_stage + 2):
         w = layers[i % LAYERS]
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
         ev[0].record(stream)
-        calls = [
+        calls = [lambda: L.aps_add_layer_norm(*args_ln)] if c3 else []
+        calls += [
             lambda: L.aps_router_logits(p(x), xd, p(gate), T, H, E, p(logits), sptr),
             lambda: L.aps_moe_route_top2(p(logits), T, E, p(routes), sptr),
             lambda: L.aps_moe_dispatch(p(routes), T, E, p(counts), p(offsets), p(arows), p(rpos), p(scratch),
@@ -187,12 +218,19 @@ def main():
                 lambda: L.aps_quantise_rows_e4m3(p(act), F, F, p(actq), kp, p(acts), A, sptr),
                 lambda: L.aps_moe_ffn_down_fp8(w.handle, p(actq), p(acts), T, p(offsets), p(y), sptr),
             ]
+        elif c3:
+            calls += [
+                lambda: L.aps_moe_ffn_up(w.handle, p(xb), capi.DTYPE_BF16, T, p(offsets), p(arows), p(act), None,
+                                         sptr),
+                lambda: L.aps_moe_ffn_down(w.handle, p(act), None, T, p(offsets), p(y), sptr),
+            ]
         else:
             calls += [
                 lambda: L.aps_moe_ffn_up(w.handle, p(x), xd, T, p(offsets), p(arows), p(act), None, sptr),
                 lambda: L.aps_moe_ffn_down(w.handle, p(act), None, T, p(offsets), p(y), sptr),
             ]
-        calls.append(lambda: L.aps_moe_combine(p(y), xd, p(rpos), T, H, p(out), xd, sptr))
+        calls.append(lambda: L.aps_moe_combine(p(y), capi.DTYPE_BF16 if c3 else xd, p(rpos), T, H, p(out),
+                                               capi.DTYPE_F32 if c3 else xd, sptr))
         for k, c in enumerate(calls):
             rc = c()
             if rc:
@@ -204,12 +242,14 @@ def main():
                 times[s].append(ev[k].elapsed_time(ev[k + 1]) * 1e-3)
     mean_t = {s: statistics.mean(v) for s, v in times.items()}
 
-    esz = 2 if bf16 else 4
+    esz = 2 if bf16 and not c3 else 4
     flops_up = 4.0 * A * H * F
     flops_down = 2.0 * A * F * H
     peak = PEAK_FP8 if fp8 else (PEAK_BF16 if bf16 else PEAK_F32)
     bytes_router = T * H * esz + E * H * 4 + T * E * 4
     bytes_combine = A * H * esz + T * H * esz + A * 4
+    if c3:  # bf16 expert outputs in, fp32 block output
+        bytes_combine = A * H * 2 + T * H * 4 + A * 4
     stage_report = {
         "router_logits": {"us": mean_t["router_logits"] * 1e6,
                           "GB_s": bytes_router / mean_t["router_logits"] / 1e9},
@@ -222,6 +262,10 @@ def main():
            if fp8 else {}),
         "grouped_gemm_total_TFLOP_s": (flops_up + flops_down) / (mean_t["ffn_up"] + mean_t["ffn_down"]) / 1e12,
     }
+    if c3:
+        # algorithmic bytes: attention output and residual read, both written (x += r and y)
+        stage_report["add_layer_norm"] = {"us": mean_t["add_layer_norm"] * 1e6,
+                                          "GB_s": 4.0 * T * H * 4 / mean_t["add_layer_norm"] / 1e9}
     achieved = flops_up / mean_t["ffn_up"]
     kname = "k_ffn_up<Fp8Fmt>" if fp8 else ("k_ffn_up<Bf16Fmt>" if bf16 else "k_ffn_up_f32")
     roofline = {"bound": "mfma", "kernel": kname,
@@ -233,7 +277,7 @@ def main():
 
     # ---- CPU baseline: the reference CPU-path algorithm on the host cores ----
     cpu = None
-    if args.cpu_baseline == "auto":
+    if args.cpu_baseline == "auto" and not c3:
         import oracle
         runs = []
         oracle.moe_forward(inp.x[:256], inp.gate, inp.w1, inp.w3, inp.w2)  # warm-up
@@ -253,8 +297,10 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8" if fp8 else ("bf16" if bf16 else "f32"), "data": "synthetic (seeded PCG64 normals, random-init weights)",
-        "config": {"workload": f"{args.config}: MoE FFN block, {T} tokens, hidden {H}, {E} experts top-2, "
-                               f"ffn {F}, {inp.dtype}" + (", Zipf(1.1) expert loads" if inp.zipf else ""),
+        "config": {"workload": (f"c3: decoder post-attention half, add_layer_norm (fp32) + MoE FFN block, {T} "
+                                f"tokens, hidden {H}, {E} experts top-2, ffn {F}, bf16 experts" if c3 else
+                                f"{args.config}: MoE FFN block, {T} tokens, hidden {H}, {E} experts top-2, "
+                                f"ffn {F}, {inp.dtype}" + (", Zipf(1.1) expert loads" if inp.zipf else "")),
                    "tokens": T, "hidden": H, "experts": E, "ffn": F, "layers_rotated": LAYERS},
         "roofline": roofline,
         "cpu_baseline": cpu,
