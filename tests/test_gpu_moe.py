@@ -279,9 +279,9 @@ def test_argument_errors_on_device(gpu_device):
     inp = synth.make_moe_inputs(T=16, H=256, E=16, F=64, dtype="bf16", seed=2)
     w = weights_for(inp, gpu_device)
     gate = torch.from_numpy(inp.gate).to(gpu_device)
-    xf = torch.zeros((16, 256), dtype=torch.float32, device=gpu_device)
+    xh = torch.zeros((16, 256), dtype=torch.float16, device=gpu_device)
     with pytest.raises(ValueError):
-        moe.moe_forward_gpu(xf, gate, w)           # x dtype does not match bf16 weights
+        moe.moe_forward_gpu(xh, gate, w)           # x dtype does not match bf16 weights
     x = x_for(inp, gpu_device)
     out = torch.empty((16, 256), dtype=torch.bfloat16, device=gpu_device)
     L = capi.lib()
