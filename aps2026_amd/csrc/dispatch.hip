@@ -56,25 +56,71 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
     const int lane = threadIdx.x & 63;
     const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     const int64_t ntiles = (rows + kWave - 1) / kWave;
-    if (tile >= ntiles) return;  // wave-uniform
 
-    // 1. per-expert totals and the prefix before this tile (lane = expert).
-    //    Loads go out 32 tiles at a time (independent), so the wave waits a
-    //    handful of L2 round trips rather than one per tile.
+    // The lane's token's two routes (index clamped so that the loads are
+    // unconditional), issued first: their latency overlaps the histogram
+    // loads below.
+    const int64_t t = tile * kWave + lane;
+    const int64_t tc = t < rows ? t : rows - 1;
+    const int r0 = routes[2 * tc], r1 = routes[2 * tc + 1];
+
+    // 1. per-expert totals and the prefix before each of the workgroup's
+    //    four tiles, with the histogram read once per workgroup: a load
+    //    instruction covers tpl = 64 / E consecutive tiles (lane = tile
+    //    offset x E + expert; tpl = 1 when E does not divide 64), and the
+    //    four waves take every fourth group of tpl tiles.  Lanes of one
+    //    expert are then summed with xor shuffles, the waves' sums in LDS.
+    //    (Each wave reading the whole histogram, one narrow load per tile,
+    //    was the kernel's main cost.)
+    __shared__ uint32_t part[4][5][kMaxExperts];
+    const int wave = threadIdx.x >> 6;
+    const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * 4;  // the workgroup's first tile
+    const int tpl = 64 % E == 0 ? 64 / E : 1;
+    const int ex = lane % E;  // this lane's expert in the histogram loads
+    const bool active = lane < tpl * E;
+    uint32_t tot = 0, bef0 = 0, bef1 = 0, bef2 = 0, bef3 = 0;
+    // eight loads in flight per batch: unconditional (index clamped), used
+    // only where the tile exists
+    for (int64_t j0 = static_cast<int64_t>(wave) * tpl; j0 < ntiles; j0 += 32 * tpl) {
+        uint32_t c[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t j = j0 + 4 * tpl * i + lane / E;
+            c[i] = tile_counts[(j < ntiles ? j : ntiles - 1) * E + ex];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t j = j0 + 4 * tpl * i + lane / E;
+            const uint32_t n = active && j < ntiles ? tile_word_total(c[i]) : 0u;
+            tot += n;
+            bef0 += j < tile0 ? n : 0u;
+            bef1 += j < tile0 + 1 ? n : 0u;
+            bef2 += j < tile0 + 2 ? n : 0u;
+            bef3 += j < tile0 + 3 ? n : 0u;
+        }
+    }
+    for (int d = E; d < 64 && tpl > 1; d <<= 1) {  // lanes e, e + E, e + 2E, ...
+        tot += __shfl_xor(tot, d);
+        bef0 += __shfl_xor(bef0, d);
+        bef1 += __shfl_xor(bef1, d);
+        bef2 += __shfl_xor(bef2, d);
+        bef3 += __shfl_xor(bef3, d);
+    }
+    if (lane < E) {
+        part[wave][0][lane] = tot;
+        part[wave][1][lane] = bef0;
+        part[wave][2][lane] = bef1;
+        part[wave][3][lane] = bef2;
+        part[wave][4][lane] = bef3;
+    }
+    __syncthreads();
+    if (tile >= ntiles) return;  // wave-uniform, after the workgroup's barrier
     uint32_t total = 0, before = 0;
     if (lane < E) {
-        for (int64_t j0 = 0; j0 < ntiles; j0 += 32) {
-            // unconditional loads (index clamped), so that all 32 are in
-            // flight before the first use
-            uint32_t c[32];
 #pragma unroll
-            for (int i = 0; i < 32; ++i) c[i] = tile_counts[(j0 + i < ntiles ? j0 + i : ntiles - 1) * E + lane];
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const uint32_t n = j0 + i < ntiles ? tile_word_total(c[i]) : 0u;
-                total += n;
-                before += j0 + i < tile ? n : 0u;
-            }
+        for (int w = 0; w < 4; ++w) {
+            total += part[w][0][lane];
+            before += part[w][1 + wave][lane];
         }
     }
     // 2. exclusive scan of totals over lanes 0..E-1
@@ -93,12 +139,8 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
     }
 
     // 3. stable rank of each lane's token inside this tile, per expert
-    const int64_t t = tile * kWave + lane;
-    int first = 255, second = 255;
-    if (t < rows) {
-        first = routes[2 * t];
-        second = routes[2 * t + 1];
-    }
+    const int first = t < rows ? r0 : 255;
+    const int second = t < rows ? r1 : 255;
     const uint64_t below = (1ull << lane) - 1ull;
     uint32_t p0 = 0, p1 = 0;
     for (int e = 0; e < E; ++e) {

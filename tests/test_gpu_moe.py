@@ -193,6 +193,23 @@ def test_router_kernel_shapes(gpu_device, E, H):
         w.release()
 
 
+@pytest.mark.parametrize("E,T", [(16, 20000), (24, 5000), (64, 9000), (2, 3000)])
+def test_dispatch_many_tiles(gpu_device, E, T):
+    """The staged dispatch on random routes over many 64-token tiles (more
+    than one batch of histogram loads per wave, partial last workgroup),
+    bit-exact against the oracle's stable counting sort."""
+    note(f"dispatch E={E} T={T}")
+    rng = np.random.default_rng(E * 1000 + T)
+    first = rng.integers(0, E, T)
+    second = (first + rng.integers(1, E, T)) % E
+    routes = np.stack([first, second], axis=1).astype(np.uint8)
+    want = oracle.dispatch(routes, E)
+    got = moe.dispatch(torch.from_numpy(routes).to(gpu_device), E)
+    torch.cuda.synchronize()
+    for g, w_ in zip(got, want):
+        np.testing.assert_array_equal(g.cpu().numpy().astype(np.uint32), w_)
+
+
 @pytest.mark.parametrize("T", [1, 2, 3, 63, 64, 65, 127, 129, 300])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_ragged_rows_small_shapes(gpu_device, T, dtype):
