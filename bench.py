@@ -17,6 +17,11 @@ copies of the expert weights (4 x 176 MB > the 256 MB MALL), as consecutive
 decoder layers would, so expert weights stream from HBM every step instead
 of sitting in the Infinity Cache.
 
+Timing: untimed steps run for --settle seconds (default 0.5) and then W
+warm-up steps, so that the K timed steps see the clocks of sustained work
+(from idle the first tens of milliseconds run slower); the timed region is
+bracketed by device synchronisation.
+
 Prints ONE JSON line.  `roofline` covers the dominant kernel (the grouped
 w1||w3 + SwiGLU GEMM, k_ffn_up<Bf16Fmt>, or k_ffn_up<Fp8Fmt> for --config c5),
 timed with HIP events on the stream it is launched on; its `traffic` is the
@@ -59,8 +64,12 @@ FETCH_SCALE, WRITE_SCALE = 262144.0 / 131088.5, 1.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle", type=float, default=0.5,
+                    help="seconds of untimed steps before the warm-up steps: the GPU raises its clocks over the "
+                         "first tens of milliseconds of sustained work (5 warm-up + 50 timed steps from idle "
+                         "read about 16%% slower than the steady state)")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c5"])
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -160,6 +169,13 @@ def main():
         if rc:
             raise RuntimeError(capi.last_error())
 
+    t_settle = time.perf_counter()
+    n_settle = 0
+    while time.perf_counter() - t_settle < args.settle:
+        for _ in range(LAYERS):
+            step(n_settle)
+            n_settle += 1
+        torch.cuda.synchronize()
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -294,7 +310,7 @@ def main():
 
     line = {
         "metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "steps": args.steps, "warmup": args.warmup, "settle_steps": n_settle, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8" if fp8 else ("bf16" if bf16 else "f32"), "data": "synthetic (seeded PCG64 normals, random-init weights)",
         "config": {"workload": (f"c3: decoder post-attention half, add_layer_norm (fp32) + MoE FFN block, {T} "
