@@ -102,11 +102,15 @@ def lib():
     L.aps_moe_ffn_down_fp8.argtypes = [u64, _c_vp, _c_vp, i64, _c_vp, _c_vp, _c_vp]
     L.aps_layer_norm.argtypes = [_c_vp, _c_vp, _c_vp, i64, i32, ctypes.c_float, _c_vp, _c_vp]
     L.aps_add_layer_norm.argtypes = [_c_vp, _c_vp, _c_vp, _c_vp, i64, i32, ctypes.c_float, _c_vp, _c_vp]
+    L.aps_gather_rows.argtypes = [_c_vp, i64, i64, _c_vp, i64, _c_vp, _c_vp]
+    L.aps_prefix_dedup.argtypes = [_c_vp, _c_vp, i64, i64, i64, _c_vp, _c_vp, _c_vp, _c_vp, i64,
+                                   ctypes.POINTER(i64)]
     for name in ("aps_moe_weights_register", "aps_moe_weights_release", "aps_moe_workspace_layout",
                  "aps_router_logits", "aps_moe_route_top2", "aps_moe_dispatch", "aps_moe_expert_ffn",
                  "aps_moe_combine", "aps_moe_forward_grouped", "aps_moe_forward", "aps_moe_ffn_up",
                  "aps_moe_ffn_down", "aps_mlp_forward", "aps_quantise_rows_e4m3", "aps_moe_ffn_up_fp8",
-                 "aps_moe_ffn_down_fp8", "aps_layer_norm", "aps_add_layer_norm"):
+                 "aps_moe_ffn_down_fp8", "aps_layer_norm", "aps_add_layer_norm", "aps_gather_rows",
+                 "aps_prefix_dedup"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

@@ -346,3 +346,100 @@ std::size_t register_dense(const Tensor& w1, const Tensor& w2, const Tensor& w3)
 }
 
 }  // namespace aps_cpp_detail
+
+// ---- row gather (reference src/tensor.cu:3379-3426) ------------------------
+
+namespace {
+
+// Grow-only device staging buffer of the std::vector overload, as the
+// reference's device_rows: the blocking upload on the default stream orders
+// it after every earlier gather that read it.
+struct RowStaging {
+    std::mutex mu;
+    std::uint32_t* ptr = nullptr;
+    std::size_t cap = 0;
+};
+RowStaging g_rows;
+
+std::vector<std::uint32_t> compact_rows(const std::vector<std::size_t>& rows, std::size_t* max_row) {
+    std::vector<std::uint32_t> c(rows.size());
+    std::size_t mx = 0;
+    for (std::size_t i = 0; i < rows.size(); ++i) {
+        if (rows[i] > 0xFFFFFFFFull) throw std::invalid_argument("gather_rows_gpu row index");
+        c[i] = static_cast<std::uint32_t>(rows[i]);
+        mx = std::max(mx, rows[i]);
+    }
+    *max_row = mx;
+    return c;
+}
+
+void gather_common(const Tensor& x, const std::uint32_t* drows, std::size_t count, std::size_t max_row, Tensor& out) {
+    if (count == 0) return;
+    const std::size_t h = x.ndim() ? x.size(x.ndim() - 1) : 0;
+    const std::size_t x_rows = h ? x.size() / h : 0;
+    if (out.size() != count * h) throw std::invalid_argument("gather_rows_gpu shape");
+    if (max_row >= x_rows) throw std::invalid_argument("gather_rows_gpu row index");
+    const int rc = aps_gather_rows(x.cuda_data(), static_cast<int64_t>(x_rows), static_cast<int64_t>(h), drows,
+                                   static_cast<int64_t>(count), out.cuda_data_write(), nullptr);
+    if (rc) throw_status(rc, "gather_rows_gpu");
+}
+
+}  // namespace
+
+namespace tensor_ops {
+
+void gather_rows_gpu(const Tensor& x, const std::vector<std::size_t>& rows, Tensor& out) {
+    if (rows.empty()) return;
+    std::size_t max_row = 0;
+    const std::vector<std::uint32_t> c = compact_rows(rows, &max_row);
+    std::lock_guard<std::mutex> lock(g_rows.mu);
+    if (g_rows.cap < c.size()) {
+        if (g_rows.ptr) hip_check(hipFree(g_rows.ptr), "hipFree row staging");
+        g_rows.ptr = nullptr;
+        g_rows.cap = 0;
+        hip_check(hipMalloc(&g_rows.ptr, c.size() * sizeof(std::uint32_t)), "hipMalloc row staging");
+        g_rows.cap = c.size();
+    }
+    hip_check(hipMemcpy(g_rows.ptr, c.data(), c.size() * sizeof(std::uint32_t), hipMemcpyHostToDevice),
+              "copy row indices");
+    gather_common(x, g_rows.ptr, c.size(), max_row, out);
+}
+
+RowIndexBuffer::RowIndexBuffer(const std::vector<std::size_t>& rows) : size_(rows.size()) {
+    if (size_ == 0) return;
+    const std::vector<std::uint32_t> c = compact_rows(rows, &max_row_);
+    hip_check(hipMalloc(&ptr_, size_ * sizeof(std::uint32_t)), "hipMalloc RowIndexBuffer");
+    hip_check(hipMemcpy(ptr_, c.data(), size_ * sizeof(std::uint32_t), hipMemcpyHostToDevice),
+              "copy RowIndexBuffer");
+}
+
+RowIndexBuffer::~RowIndexBuffer() {
+    if (ptr_) (void)hipFree(ptr_);
+}
+
+RowIndexBuffer::RowIndexBuffer(RowIndexBuffer&& other) noexcept
+    : ptr_(other.ptr_), size_(other.size_), max_row_(other.max_row_) {
+    other.ptr_ = nullptr;
+    other.size_ = 0;
+    other.max_row_ = 0;
+}
+
+RowIndexBuffer& RowIndexBuffer::operator=(RowIndexBuffer&& other) noexcept {
+    if (this != &other) {
+        if (ptr_) (void)hipFree(ptr_);
+        ptr_ = other.ptr_;
+        size_ = other.size_;
+        max_row_ = other.max_row_;
+        other.ptr_ = nullptr;
+        other.size_ = 0;
+        other.max_row_ = 0;
+    }
+    return *this;
+}
+
+void gather_rows_gpu(const Tensor& x, const RowIndexBuffer& rows, Tensor& out) {
+    if (rows.empty()) return;
+    gather_common(x, rows.data(), rows.size(), rows.max_row(), out);
+}
+
+}  // namespace tensor_ops

@@ -527,6 +527,37 @@ int aps_add_layer_norm(float* x, const float* residual, const float* weight, con
     return layer_norm_common(x, residual, weight, bias, rows, hidden, eps, y, stream, "add layer norm");
 }
 
+int aps_gather_rows(const float* x, int64_t x_rows, int64_t hidden, const uint32_t* rows, int64_t count, float* out,
+                    void* stream) {
+    if (x_rows < 0 || hidden < 0 || count < 0)
+        return fail(APS_ERR_SHAPE, "gather rows shape: x_rows %lld hidden %lld count %lld", (long long)x_rows,
+                    (long long)hidden, (long long)count);
+    if (count == 0 || hidden == 0) return APS_OK;
+    if (!rows || !out || (x_rows > 0 && !x)) return fail(APS_ERR_ARG, "gather rows: NULL pointer");
+    if (count * ((hidden + 1023) / 1024) > 0x7FFFFFFF)
+        return fail(APS_ERR_SHAPE, "gather rows shape: %lld rows of %lld values is past the grid limit",
+                    (long long)count, (long long)hidden);
+    APS_HIP(aps::launch_gather_rows(x, x_rows, hidden, rows, count, out, static_cast<hipStream_t>(stream)),
+            "gather rows launch");
+    return APS_OK;
+}
+
+int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int64_t batch, int64_t vocab_size,
+                     int64_t max_positions, uint32_t* token_node, uint32_t* node_token, uint32_t* node_depth,
+                     uint32_t* node_anc, int64_t anc_stride, int64_t* nodes) {
+    // reference src/model.cu:47-49: an empty batch is a std::runtime_error
+    if (batch <= 0) return fail(APS_ERR_SHAPE, "generate received an empty input batch");
+    if (!seq_offsets || !nodes) return fail(APS_ERR_ARG, "prefix dedup: NULL pointer");
+    if (seq_offsets[batch] > 0 && (!ids || !token_node || !node_token || !node_depth))
+        return fail(APS_ERR_ARG, "prefix dedup: NULL pointer");
+    std::string err;
+    const int rc = aps::prefix_dedup(ids, seq_offsets, batch, vocab_size, max_positions, token_node, node_token,
+                                     node_depth, node_anc, anc_stride, nodes, err);
+    if (rc == 1) return fail(APS_ERR_ARG, "%s", err.c_str());
+    if (rc != 0) return fail(APS_ERR_SHAPE, "prefix dedup: %s", err.c_str());
+    return APS_OK;
+}
+
 static int forward_common(uint64_t handle, const void* x, int32_t x_dtype, int64_t rows, void* out,
                           int32_t out_dtype, void* workspace, size_t workspace_bytes,
                           const WeightSet** w_out, aps_moe_ws_layout* L) {

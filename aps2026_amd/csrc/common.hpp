@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <string>
 
 namespace aps {
 
@@ -124,6 +125,17 @@ hipError_t launch_tile_hist(const uint8_t* routes, int64_t rows, int experts,
                             uint32_t* tile_counts, hipStream_t s);
 // Decoder-layer LayerNorm (residual == nullptr: plain; else x += residual
 // in place first).  hidden % 256 == 0.
+// Row gather out[i] = x[rows[i]] (fp32); rows past x_rows give zero rows.
+hipError_t launch_gather_rows(const float* x, int64_t x_rows, int64_t hidden, const uint32_t* rows, int64_t count,
+                              float* out, hipStream_t s);
+
+// Prefix-trie deduplication of a packed prompt batch (host code).  Returns 0,
+// 1 for the reference's std::invalid_argument conditions or 2 for other
+// invalid arguments, with a message in err.
+int prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int64_t batch, int64_t vocab, int64_t max_positions,
+                 uint32_t* token_node, uint32_t* node_token, uint32_t* node_depth, uint32_t* node_anc,
+                 int64_t anc_stride, int64_t* nodes_out, std::string& err);
+
 hipError_t launch_layer_norm(float* x, const float* residual, const float* weight, const float* bias, float* y,
                              int64_t rows, int hidden, float eps, hipStream_t s);
 hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_counts,

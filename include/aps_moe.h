@@ -263,6 +263,38 @@ APS_API int aps_layer_norm(const float* x, const float* weight, const float* bia
 APS_API int aps_add_layer_norm(float* x, const float* residual, const float* weight, const float* bias,
                                int64_t rows, int32_t hidden, float eps, float* y, void* stream);
 
+/* ---- prompt prefix deduplication (scope row f2) ------------------------- */
+
+/* Replaces tensor_ops::gather_rows_gpu (reference include/tensor.h:115-116 and
+ * 138, src/tensor.cu:3379-3386, 3420-3426, kernel k_gather_rows
+ * src/tensor.cu:2635-2642): out[i][:] = x[rows[i]][:] for i < count, fp32
+ * rows of `hidden` values; rows[] is device memory (the reference's
+ * RowIndexBuffer, or its std::vector overload after an upload).  An index
+ * >= x_rows gives a row of zeros (the reference does not check; the C++ and
+ * Python layers reject such indices before the call).  Any hidden; 16-byte
+ * accesses when hidden % 4 == 0 and x, out are 16-byte aligned. */
+APS_API int aps_gather_rows(const float* x, int64_t x_rows, int64_t hidden, const uint32_t* rows, int64_t count,
+                            float* out, void* stream);
+
+/* The prefix-trie deduplication of PhiTinyMoEModel::generate (reference
+ * src/model.cu:44-117), host code, synchronous.  Sequence b is
+ * ids[seq_offsets[b] .. seq_offsets[b+1]) (seq_offsets[0] == 0, batch + 1
+ * entries).  Writes, for the `*nodes` trie nodes (node ids in creation
+ * order, sequence by sequence, as the reference):
+ *   token_node[row]  node of packed token row `row` (seq_offsets[batch] entries)
+ *   node_token[n]    token id of node n            (capacity seq_offsets[batch])
+ *   node_depth[n]    depth = position of node n    (capacity seq_offsets[batch])
+ *   node_anc         optional (NULL to skip): [nodes][anc_stride], row n =
+ *                    its ancestor chain root .. n, then zeros; anc_stride >=
+ *                    the longest sequence.
+ * Errors (the reference's std::invalid_argument messages, APS_ERR_ARG):
+ * "empty input", "sequence is too long" (length > max_positions), "token out
+ * of vocabulary" (outside [0, vocab_size)); batch <= 0 gives APS_ERR_SHAPE
+ * "generate received an empty input batch" (a std::runtime_error there). */
+APS_API int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int64_t batch, int64_t vocab_size,
+                             int64_t max_positions, uint32_t* token_node, uint32_t* node_token, uint32_t* node_depth,
+                             uint32_t* node_anc, int64_t anc_stride, int64_t* nodes);
+
 /* ---- diagnostics ------------------------------------------------------- */
 
 APS_API const char* aps_moe_last_error(void);

@@ -1,6 +1,7 @@
 // Model constants of the MoE block, under the reference's names
 // (include/config.h:5-27 of the reference: namespace apss26).  Only the
-// constants the MoE feed-forward path and its LayerNorm read are kept here.
+// constants the MoE feed-forward path, its LayerNorm and the prompt prefix
+// deduplication read are kept here.
 #pragma once
 
 #include <cstddef>
@@ -17,4 +18,8 @@ constexpr float ROUTER_SCORE_QUANTUM = 1.0e-3f;
 constexpr float ROUTER_TIE_EPS = 2.0e-2f;
 // LayerNorm epsilon of the decoder layer (reference include/config.h:19).
 constexpr float NORM_EPS = 1.0e-5f;
+// Token ids and sequence lengths the prefix trie accepts (reference
+// include/config.h:7, 16).
+constexpr std::size_t VOCAB_SIZE = 32064;
+constexpr std::size_t MAX_POSITION_EMBEDDINGS = 4096;
 }  // namespace apss26

@@ -116,4 +116,39 @@ void layer_norm_gpu(const Tensor& x, const Tensor& weight, const Tensor& bias, f
 void add_layer_norm_gpu(Tensor& x, const Tensor& residual, const Tensor& weight, const Tensor& bias, float eps,
                         Tensor& y);
 
+// out[i][:] = x[rows[i]][:] over the last dimension of x (reference
+// include/tensor.h:115-116, src/tensor.cu:3379-3386): the index list is
+// uploaded through a blocking copy on the default stream, then one HIP
+// gather kernel.  out must hold rows.size() rows.  An index past the end of
+// x throws std::invalid_argument("gather_rows_gpu row index"), and a wrong
+// out size std::invalid_argument("gather_rows_gpu shape") (the reference
+// does not check either).
+void gather_rows_gpu(const Tensor& x, const std::vector<std::size_t>& rows, Tensor& out);
+
+// A row-index map uploaded to the device once and reused across many
+// gathers (reference include/tensor.h:119-137).
+class RowIndexBuffer {
+public:
+    RowIndexBuffer() = default;
+    explicit RowIndexBuffer(const std::vector<std::size_t>& rows);
+    ~RowIndexBuffer();
+    RowIndexBuffer(const RowIndexBuffer&) = delete;
+    RowIndexBuffer& operator=(const RowIndexBuffer&) = delete;
+    RowIndexBuffer(RowIndexBuffer&& other) noexcept;
+    RowIndexBuffer& operator=(RowIndexBuffer&& other) noexcept;
+    const std::uint32_t* data() const { return ptr_; }
+    std::size_t size() const { return size_; }
+    bool empty() const { return size_ == 0; }
+    std::size_t max_row() const { return max_row_; }  // largest index (0 when empty)
+
+private:
+    std::uint32_t* ptr_ = nullptr;
+    std::size_t size_ = 0;
+    std::size_t max_row_ = 0;
+};
+
+// The same gather from a device-resident index map (reference
+// include/tensor.h:138, src/tensor.cu:3420-3426); same checks as above.
+void gather_rows_gpu(const Tensor& x, const RowIndexBuffer& rows, Tensor& out);
+
 }  // namespace tensor_ops

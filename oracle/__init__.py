@@ -253,3 +253,50 @@ def layer_norm(x: np.ndarray, weight: np.ndarray, bias: np.ndarray, eps: float =
     lib().oracle_layer_norm(x, None if res is None else res.ctypes.data, rows, h, w, b, np.float32(eps),
                             v.ctypes.data, y, mean.ctypes.data, inv.ctypes.data)
     return y, v, mean, inv
+
+
+def prefix_dedup(input_ids, vocab_size: int = 32064, max_positions: int = 4096):
+    """Prefix trie of a prompt batch, pure Python (small and medium batches).
+
+    Restates PhiTinyMoEModel::generate (reference src/model.cu:44-117):
+    lengths checked first over the whole batch ("empty input", "sequence is
+    too long"), then one walk sequence by sequence with a dict from (parent,
+    token) to child; a new child gets the next node id and records its token,
+    depth and ancestor chain root .. node; "token out of vocabulary" is
+    raised at the first bad token of the walk.  An empty batch raises
+    RuntimeError("generate received an empty input batch") (src/model.cu:47-49).
+    Returns (token_node, node_token, node_depth, node_anc) as lists; node_anc
+    holds the chains without padding."""
+    if len(input_ids) == 0:
+        raise RuntimeError("generate received an empty input batch")
+    for seq in input_ids:
+        if len(seq) == 0:
+            raise ValueError("empty input")
+        if len(seq) > max_positions:
+            raise ValueError("sequence is too long")
+    children = {}
+    token_node, node_token, node_depth, node_anc = [], [], [], []
+    for seq in input_ids:
+        parent = -1
+        chain = []
+        for si, tok in enumerate(seq):
+            tok = int(tok)
+            if tok < 0 or tok >= vocab_size:
+                raise ValueError("token out of vocabulary")
+            key = (parent, tok)
+            node = children.get(key)
+            if node is None:
+                node = len(node_token)
+                children[key] = node
+                node_token.append(tok)
+                node_depth.append(si)
+                node_anc.append(chain + [node])
+            chain.append(node)  # chain = nodes of positions 0 .. si of this sequence
+            token_node.append(node)
+            parent = node
+    return token_node, node_token, node_depth, node_anc
+
+
+def gather_rows(x: np.ndarray, rows) -> np.ndarray:
+    """out[i] = x[rows[i]] (reference k_gather_rows, src/tensor.cu:2635-2642)."""
+    return np.ascontiguousarray(x[np.asarray(rows, dtype=np.int64)])

@@ -7,8 +7,9 @@
 // (expert 0 as a dense FFN) on the GPU, and writes inputs and outputs as
 // raw little-endian fp32 files into <out_dir> for tests/test_gpu_cpp_layer.py
 // to compare with the CPU oracle.  It also checks, in process, the
-// reference's exception types and messages and the Tensor host/device
-// synchronisation rules.  Exit status 0 means every in-process check passed.
+// reference's exception types and messages, the Tensor host/device
+// synchronisation rules, and the prompt prefix trie (a hand-worked batch)
+// and row gather (both overloads) of include/prefix.h and include/tensor.h.  Exit status 0 means every in-process check passed.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -20,6 +21,7 @@
 #include <vector>
 
 #include "../../include/layer.h"
+#include "../../include/prefix.h"
 
 namespace {
 
@@ -140,6 +142,43 @@ int main(int argc, char** argv) {
         expect_throw<std::invalid_argument>(
             [&] { tensor_ops::add_layer_norm_gpu(ln_x, bad, ln_w, ln_b, 1e-5f, add_y); }, "add layer norm shape",
             "add layer norm shape");
+    }
+
+    // --- prompt prefix dedup and the row gather --------------------------------
+    {
+        const PrefixTrie trie = build_prefix_trie({{1, 2, 3}, {1, 2, 4}, {5}, {1, 2, 3, 6}});
+        expect(trie.token_node == std::vector<std::size_t>({0, 1, 2, 0, 1, 3, 4, 0, 1, 2, 5}), "trie token_node");
+        expect(trie.node_token == std::vector<std::size_t>({1, 2, 3, 4, 5, 6}), "trie node_token");
+        expect(trie.node_depth == std::vector<std::size_t>({0, 1, 2, 2, 0, 3}), "trie node_depth");
+        expect(trie.max_len == 4 && trie.node_anc.size() == 6 * 4, "trie ancestor table size");
+        expect(std::vector<std::size_t>(trie.node_anc.begin() + 20, trie.node_anc.end()) ==
+                   std::vector<std::size_t>({0, 1, 2, 5}), "trie ancestor chain of node 5");
+        expect(std::vector<std::size_t>(trie.node_anc.begin() + 16, trie.node_anc.begin() + 20) ==
+                   std::vector<std::size_t>({4, 0, 0, 0}), "trie ancestor chain of node 4");
+        expect(trie.last_rows() == std::vector<std::size_t>({2, 3, 4, 5}), "trie last rows");
+        expect_throw<std::runtime_error>([] { build_prefix_trie({}); }, "generate received an empty input batch",
+                                         "empty batch");
+        expect_throw<std::invalid_argument>([] { build_prefix_trie({{1}, {}}); }, "empty input", "empty sequence");
+        expect_throw<std::invalid_argument>([] { build_prefix_trie({std::vector<int>(4097, 1)}); },
+                                            "sequence is too long", "long sequence");
+        expect_throw<std::invalid_argument>([] { build_prefix_trie({{1, 32064}}); }, "token out of vocabulary",
+                                            "token range");
+        // gather rows of x: the vector overload and a device index map
+        const std::vector<std::size_t> rows = {T - 1, 0, 5, 5, 17};
+        Tensor g1({rows.size(), H}), g2({rows.size(), H});
+        tensor_ops::gather_rows_gpu(x, rows, g1);
+        const tensor_ops::RowIndexBuffer rib(rows);
+        tensor_ops::gather_rows_gpu(x, rib, g2);
+        bool same = true;
+        for (std::size_t i = 0; i < rows.size(); ++i)
+            for (std::size_t k = 0; k < H; ++k)
+                same = same && g1.at(i, k) == x.at(rows[i], k) && g2.at(i, k) == x.at(rows[i], k);
+        expect(same, "gather_rows_gpu copies the indexed rows");
+        Tensor g3({2, H});
+        expect_throw<std::invalid_argument>([&] { tensor_ops::gather_rows_gpu(x, {0, T}, g3); },
+                                            "gather_rows_gpu row index", "gather index past the end");
+        expect_throw<std::invalid_argument>([&] { tensor_ops::gather_rows_gpu(x, {0, 1}, g1); },
+                                            "gather_rows_gpu shape", "gather output size");
     }
 
     // --- Tensor synchronisation rules ----------------------------------------

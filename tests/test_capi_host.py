@@ -12,7 +12,7 @@ from aps2026_amd import capi, moe
 def test_library_exports_every_declared_symbol():
     L = capi.lib()
     names = capi.declared_symbols()
-    assert len(names) == 22
+    assert len(names) == 24
     for n in names:
         assert hasattr(L, n), n
     assert L.aps_moe_abi_version() == 1
@@ -111,3 +111,11 @@ def test_mlp_entry_points_reject_bad_handles():
     L = capi.lib()
     assert L.aps_mlp_workspace_size(0, 16) == 0
     assert L.aps_mlp_forward(0, None, capi.DTYPE_F32, 16, None, None, 0, None) == capi.APS_ERR_HANDLE
+
+
+def test_gather_rows_argument_errors():
+    L = capi.lib()
+    assert L.aps_gather_rows(None, 4, 16, None, 0, None, None) == capi.APS_OK      # nothing to gather
+    assert L.aps_gather_rows(None, -1, 16, None, 1, None, None) == capi.APS_ERR_SHAPE
+    assert L.aps_gather_rows(None, 4, 16, None, 1, None, None) == capi.APS_ERR_ARG
+    assert "NULL" in capi.last_error()

@@ -3,8 +3,8 @@
 tests/cpp/layer_check (built by aps2026_amd/build.py) runs PhiMoE::forward in
 fp32 and bf16 compute, PhiMLP::forward (expert 0 as a dense FFN) and the
 router GEMM through the C++ classes on a small synthetic layer, checks the
-reference's exception types and messages and the Tensor synchronisation
-rules in process, and writes its inputs and outputs here; the outputs are
+reference's exception types and messages, the Tensor synchronisation
+rules, the prefix trie and the row gather in process, and writes its inputs and outputs here; the outputs are
 compared with the CPU oracle on those same inputs:
   * router logits and the fp32 MoE block: bit-exact (same arithmetic as the
     reference: FMA chains k ascending, exact SiLU, RN(0.5a + 0.5b) combine);

@@ -1,0 +1,109 @@
+"""Prefix deduplication of prompt batches (reference PhiTinyMoEModel::generate,
+src/model.cu:44-117): the oracle's trie pinned by what the mathematics fixes
+(a node is a distinct prefix, numbered by first appearance), hand-worked
+known answers, the C4 shape's node count, and the library's host entry point
+(aps_prefix_dedup, no GPU needed) bit for bit against the oracle, errors
+included."""
+import numpy as np
+import pytest
+
+import oracle
+from aps2026_amd import prefix
+
+
+def brute_force(input_ids):
+    """Nodes = distinct prefixes in order of first appearance (sequence by
+    sequence, position by position); independent of any trie."""
+    ids = {}
+    token_node = []
+    for seq in input_ids:
+        for si in range(len(seq)):
+            p = tuple(int(t) for t in seq[:si + 1])
+            if p not in ids:
+                ids[p] = len(ids)
+            token_node.append(ids[p])
+    order = sorted(ids, key=ids.get)
+    node_token = [p[-1] for p in order]
+    node_depth = [len(p) - 1 for p in order]
+    node_anc = [[ids[p[:k + 1]] for k in range(len(p))] for p in order]
+    return token_node, node_token, node_depth, node_anc
+
+
+def shared_prefix_batch(rng, groups, per_group, prefix_len, suffix_len, vocab=32064):
+    out = []
+    for _ in range(groups):
+        pre = rng.integers(0, vocab, prefix_len)
+        for _ in range(per_group):
+            out.append(np.concatenate([pre, rng.integers(0, vocab, suffix_len)]).tolist())
+    return out
+
+
+def c4_prompts(seed=0):
+    """C4: 16 prompts of 1024 ids, groups of 4 share a 512-token prefix."""
+    return shared_prefix_batch(np.random.default_rng(seed), 4, 4, 512, 512)
+
+
+def test_oracle_known_answer():
+    tn, nt, nd, na = oracle.prefix_dedup([[1, 2, 3], [1, 2, 4], [5], [1, 2, 3, 6]])
+    assert tn == [0, 1, 2, 0, 1, 3, 4, 0, 1, 2, 5]
+    assert nt == [1, 2, 3, 4, 5, 6]
+    assert nd == [0, 1, 2, 2, 0, 3]
+    assert na == [[0], [0, 1], [0, 1, 2], [0, 1, 3], [4], [0, 1, 2, 5]]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_oracle_against_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    vocab = [3, 5, 32064][seed % 3]          # tiny vocabularies force shared prefixes everywhere
+    batch = [rng.integers(0, vocab, rng.integers(1, 40)).tolist() for _ in range(rng.integers(1, 12))]
+    batch += shared_prefix_batch(rng, 2, 3, 7, 5, vocab)
+    rng.shuffle(batch)
+    assert oracle.prefix_dedup(batch) == brute_force(batch)
+
+
+def test_oracle_c4_node_count():
+    tn, nt, nd, na = oracle.prefix_dedup(c4_prompts())
+    assert len(tn) == 16 * 1024 and len(nt) == 4 * (512 + 4 * 512) == 10240
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_library_matches_oracle(seed):
+    rng = np.random.default_rng(100 + seed)
+    vocab = [4, 50, 32064, 7][seed]
+    batch = [rng.integers(0, vocab, rng.integers(1, 60)).tolist() for _ in range(rng.integers(1, 20))]
+    batch += shared_prefix_batch(rng, 3, 4, 11, 9, vocab)
+    plan = prefix.prefix_dedup(batch)
+    tn, nt, nd, na = oracle.prefix_dedup(batch)
+    assert plan.token_node.tolist() == tn
+    assert plan.node_token.tolist() == nt
+    assert plan.node_depth.tolist() == nd
+    assert plan.nodes == len(nt)
+    for n, chain in enumerate(na):
+        row = plan.node_anc[n]
+        assert row[:len(chain)].tolist() == chain and not row[len(chain):].any()
+    ends = np.cumsum([len(s) for s in batch]) - 1
+    assert plan.last_rows.tolist() == [tn[e] for e in ends]
+
+
+def test_library_c4():
+    batch = c4_prompts()
+    plan = prefix.prefix_dedup(batch, with_ancestors=False)
+    tn, nt, nd, _ = oracle.prefix_dedup(batch)
+    assert plan.nodes == 10240 and plan.node_anc is None
+    assert plan.token_node.tolist() == tn and plan.node_token.tolist() == nt and plan.node_depth.tolist() == nd
+
+
+@pytest.mark.parametrize("batch,exc,msg", [
+    ([], RuntimeError, "generate received an empty input batch"),
+    ([[1, 2], []], ValueError, "empty input"),
+    ([[1] * 4097], ValueError, "sequence is too long"),
+    ([[1, 2, 32064]], ValueError, "token out of vocabulary"),
+    ([[1, -3]], ValueError, "token out of vocabulary"),
+    # lengths are checked over the whole batch before the walk
+    ([[1, 99999], [2] * 4097], ValueError, "sequence is too long"),
+])
+def test_errors_match_the_reference(batch, exc, msg):
+    with pytest.raises(exc, match=msg):
+        oracle.prefix_dedup(batch)
+    with pytest.raises(exc, match=msg):
+        prefix.prefix_dedup(batch)
