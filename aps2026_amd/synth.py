@@ -197,3 +197,18 @@ def make_config(name: str, seed: int = 0, T: Optional[int] = None) -> MoeInputs:
     if T is not None:
         cfg["T"] = T
     return make_moe_inputs(seed=seed, name=name, **cfg)
+
+
+def c4_prompts(seed: int = 0, groups: int = 4, per_group: int = 4, prefix_len: int = 512,
+               suffix_len: int = 512, vocab: int = 32064) -> list:
+    """C4's prompt batch: groups x per_group prompts of prefix_len +
+    suffix_len random token ids, the prompts of a group sharing their first
+    prefix_len ids (default 16 prompts of 1024 ids, 4 groups sharing 512:
+    16,384 token rows, 10,240 prefix-trie nodes at seed 0)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(groups):
+        pre = rng.integers(0, vocab, prefix_len)
+        for _ in range(per_group):
+            out.append(np.concatenate([pre, rng.integers(0, vocab, suffix_len)]).tolist())
+    return out

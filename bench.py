@@ -6,7 +6,9 @@
 add_layer_norm (attention output += residual stream, LayerNorm with the
 reference kernel's serial sums) feeding the same MoE block, fp32 activations
 with bf16 experts (synthetic attention output; the attention itself is not
-built).
+built).  `--config c4` does the same on C4's 16 prompts x 1024 ids after
+the prompt prefix trie (host code) folds them into 10,240 rows, with the
+embedding gather of those rows in each step; its value counts prompt tokens.
 
 One step = one full MoE block (router GEMM, quantised top-2, dispatch,
 grouped w1||w3 + SwiGLU, grouped w2, combine) over one batch of synthetic
@@ -70,7 +72,7 @@ def parse():
                     help="seconds of untimed steps before the warm-up steps: the GPU raises its clocks over the "
                          "first tens of milliseconds of sustained work (5 warm-up + 50 timed steps from idle "
                          "read about 16%% slower than the steady state)")
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline: repeat full-batch runs until this much time is spent (at least 2 runs)")
@@ -91,9 +93,22 @@ def main():
     from aps2026_amd import capi, moe, synth
 
     dev = torch.device("cuda:0")
-    c3 = args.config == "c3"
+    c3 = args.config in ("c3", "c4")   # the decoder's post-attention half (c4: on deduplicated rows)
+    c4 = args.config == "c4"
     inp = synth.make_config("c2" if c3 else args.config)
     T, H, E, F = inp.T, inp.H, inp.E, inp.F
+    if c4:
+        # C4's prompt batch through the prefix trie (host code, the reference's
+        # CPU-side step): the layer's rows are the trie nodes
+        from aps2026_amd import prefix
+        prompts = synth.c4_prompts()
+        dedup_s = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            plan = prefix.prefix_dedup(prompts)
+            dedup_s.append(time.perf_counter() - t0)
+        prompt_tokens = int(plan.token_node.shape[0])
+        T = plan.nodes
     A = 2 * T
     fp8 = inp.dtype == "fp8"
     bf16 = inp.dtype in ("bf16", "fp8")        # x and outputs are bf16 on both MFMA paths
@@ -110,6 +125,12 @@ def main():
         ln_w = (1.0 + 0.05 * torch.randn(H, generator=g)).to(dev)
         ln_b = (0.05 * torch.randn(H, generator=g)).to(dev)
         x = torch.empty(T, H, dtype=torch.float32, device=dev)  # post-attention LayerNorm output
+        if c4:
+            # embedding table on the device; the node rows are gathered from it
+            # every step (the residual stream the first layer adds to)
+            gd = torch.Generator(device=dev).manual_seed(4)
+            emb = torch.randn((prefix.VOCAB_SIZE, H), generator=gd, device=dev)
+            node_rows = prefix.RowIndexBuffer(plan.node_token, dev)
     elif bf16:
         x = dev_bits(inp.packed["x_bf16"])
     else:
@@ -160,7 +181,15 @@ def main():
                    ctypes.c_void_p(ln_w.data_ptr()), ctypes.c_void_p(ln_b.data_ptr()), T, H,
                    ctypes.c_float(moe.NORM_EPS), ctypes.c_void_p(x.data_ptr()), sptr)
 
+    if c4:
+        args_gather = (ctypes.c_void_p(emb.data_ptr()), emb.shape[0], H, ctypes.c_void_p(node_rows.data.data_ptr()),
+                       T, ctypes.c_void_p(resid.data_ptr()), sptr)
+
     def step(i):
+        if c4:
+            rc = L.aps_gather_rows(*args_gather)
+            if rc:
+                raise RuntimeError(capi.last_error())
         if c3:
             rc = L.aps_add_layer_norm(*args_ln)
             if rc:
@@ -185,7 +214,8 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
-    tokens_per_s = T * args.steps / elapsed
+    # c4: prompt tokens served (the trie rows stand for all of them)
+    tokens_per_s = (prompt_tokens if c4 else T) * args.steps / elapsed
 
     # ---- per-stage timing with HIP events on the launch stream ------------
     def p(t):
@@ -211,7 +241,7 @@ def main():
     else:
         stages = ["router_logits", "route_top2", "dispatch", "ffn_up", "ffn_down", "combine"]
     if c3:
-        stages = ["add_layer_norm"] + stages
+        stages = (["gather_rows"] if c4 else []) + ["add_layer_norm"] + stages
         L.aps_add_layer_norm(*args_ln)
         xb = x.to(torch.bfloat16)  # the FFN's bf16 copy of the norm output (the fused path makes its own)
     times = {s: [] for s in stages}
@@ -220,7 +250,8 @@ def main():
         w = layers[i % LAYERS]
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
         ev[0].record(stream)
-        calls = [lambda: L.aps_add_layer_norm(*args_ln)] if c3 else []
+        calls = [lambda: L.aps_gather_rows(*args_gather)] if c4 else []
+        calls += [lambda: L.aps_add_layer_norm(*args_ln)] if c3 else []
         calls += [
             lambda: L.aps_router_logits(p(x), xd, p(gate), T, H, E, p(logits), sptr),
             lambda: L.aps_moe_route_top2(p(logits), T, E, p(routes), sptr),
@@ -282,6 +313,12 @@ def main():
         # algorithmic bytes: attention output and residual read, both written (x += r and y)
         stage_report["add_layer_norm"] = {"us": mean_t["add_layer_norm"] * 1e6,
                                           "GB_s": 4.0 * T * H * 4 / mean_t["add_layer_norm"] / 1e9}
+    if c4:
+        # gather: node rows read from the embedding table and written, plus the indices
+        stage_report["gather_rows"] = {"us": mean_t["gather_rows"] * 1e6,
+                                       "GB_s": (2.0 * T * H * 4 + T * 4) / mean_t["gather_rows"] / 1e9}
+        stage_report["prefix_dedup_host"] = {"ms": statistics.median(dedup_s) * 1e3, "prompt_tokens": prompt_tokens,
+                                             "nodes": T, "threads": 1}
     achieved = flops_up / mean_t["ffn_up"]
     kname = "k_ffn_up<Fp8Fmt>" if fp8 else ("k_ffn_up<Bf16Fmt>" if bf16 else "k_ffn_up_f32")
     roofline = {"bound": "mfma", "kernel": kname,
@@ -313,11 +350,17 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "settle_steps": n_settle, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8" if fp8 else ("bf16" if bf16 else "f32"), "data": "synthetic (seeded PCG64 normals, random-init weights)",
-        "config": {"workload": (f"c3: decoder post-attention half, add_layer_norm (fp32) + MoE FFN block, {T} "
+        "config": {"workload": (f"c4: 16 prompts x 1024 ids (groups of 4 share a 512-id prefix) deduplicated to "
+                                f"{T} prefix-trie rows; per step the embedding gather of those rows, then the "
+                                f"decoder post-attention half (add_layer_norm fp32 + MoE FFN block, hidden {H}, "
+                                f"{E} experts top-2, ffn {F}, bf16 experts) on them; value counts the "
+                                f"{prompt_tokens} prompt tokens; the trie itself is host code, timed in stages"
+                                if c4 else
+                                f"c3: decoder post-attention half, add_layer_norm (fp32) + MoE FFN block, {T} "
                                 f"tokens, hidden {H}, {E} experts top-2, ffn {F}, bf16 experts" if c3 else
                                 f"{args.config}: MoE FFN block, {T} tokens, hidden {H}, {E} experts top-2, "
                                 f"ffn {F}, {inp.dtype}" + (", Zipf(1.1) expert loads" if inp.zipf else "")),
-                   "tokens": T, "hidden": H, "experts": E, "ffn": F, "layers_rotated": LAYERS},
+                   "tokens": prompt_tokens if c4 else T, "rows": T, "hidden": H, "experts": E, "ffn": F, "layers_rotated": LAYERS},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "stages": stage_report,

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
-from aps2026_amd import prefix
+from aps2026_amd import prefix, synth
 
 
 def brute_force(input_ids):
@@ -40,7 +40,7 @@ def shared_prefix_batch(rng, groups, per_group, prefix_len, suffix_len, vocab=32
 
 def c4_prompts(seed=0):
     """C4: 16 prompts of 1024 ids, groups of 4 share a 512-token prefix."""
-    return shared_prefix_batch(np.random.default_rng(seed), 4, 4, 512, 512)
+    return synth.c4_prompts(seed)
 
 
 def test_oracle_known_answer():
