@@ -1,11 +1,12 @@
 // PhiMLP / PhiMoE over the C ABI (declared in include/layer.h).
 //
-// Reference: PhiMLP::forward (src/layer.cu:49-67), PhiMoE::PhiMoE
-// (src/layer.cu:94-111) and PhiMoE::forward (src/layer.cu:113-121, the GPU
+// Reference: PhiMLP::PhiMLP and forward (src/layer.cu:44-67), PhiMoE::PhiMoE
+// (src/layer.cu:94-111, the tensor names) and PhiMoE::forward (src/layer.cu:113-121, the GPU
 // branch: router GEMM, then moe_forward_grouped_gpu).
 #include "../../include/layer.h"
 
 #include <stdexcept>
+#include <string>
 #include <utility>
 
 namespace aps_cpp_detail {
@@ -18,6 +19,10 @@ PhiMLP::PhiMLP(Tensor w1, Tensor w2, Tensor w3) : w1_(std::move(w1)), w2_(std::m
         w2_.size(1) != w1_.size(0))
         throw std::invalid_argument("PhiMLP weight shapes");
 }
+
+PhiMLP::PhiMLP(const ModelLoader& loader, const std::string& prefix)
+    : PhiMLP(loader.load(prefix + ".w1.weight"), loader.load(prefix + ".w2.weight"),
+             loader.load(prefix + ".w3.weight")) {}
 
 void PhiMLP::forward(const Tensor& x, Tensor& y, bool use_gpu) const {
     if (!use_gpu) throw std::invalid_argument("PhiMLP::forward: the CPU path (use_gpu = false) is not provided");
@@ -41,6 +46,22 @@ PhiMoE::PhiMoE(Tensor gate, std::vector<PhiMLP> experts, aps_dtype compute)
     }
     gpu_weights_handle_ = tensor_ops::register_moe_weights_gpu(w1, w2, w3, compute);
 }
+
+namespace {
+std::vector<PhiMLP> load_experts(const ModelLoader& loader, const std::string& base) {
+    std::vector<PhiMLP> experts;
+    experts.reserve(apss26::NUM_EXPERTS);
+    for (std::size_t e = 0; e < apss26::NUM_EXPERTS; ++e)
+        experts.emplace_back(loader, base + ".experts." + std::to_string(e));
+    return experts;
+}
+std::string moe_base(std::size_t layer_idx) {
+    return "model.layers." + std::to_string(layer_idx) + ".block_sparse_moe";
+}
+}  // namespace
+
+PhiMoE::PhiMoE(const ModelLoader& loader, std::size_t layer_idx, aps_dtype compute)
+    : PhiMoE(loader.load(moe_base(layer_idx) + ".gate.weight"), load_experts(loader, moe_base(layer_idx)), compute) {}
 
 void PhiMoE::forward(const Tensor& x, Tensor& y, bool use_gpu) const {
     if (!use_gpu) throw std::invalid_argument("PhiMoE::forward: the CPU path (use_gpu = false) is not provided");

@@ -1,9 +1,9 @@
 // PhiMLP and PhiMoE layers over the C ABI (reference include/layer.h:23-43).
 //
-// The forward signatures are the reference's.  The constructors take the
-// weight tensors directly: the reference's constructors read the same
-// tensors from a ModelLoader by name (src/layer.cu:44-47, 94-111), and the
-// loader is not part of this library.  forward(..., use_gpu = true) runs the
+// The forward signatures are the reference's, and so are the ModelLoader
+// constructors (src/layer.cu:44-47, 94-111: the same tensor names); the
+// constructors that take the weight tensors directly serve callers without
+// a model.bin.  forward(..., use_gpu = true) runs the
 // HIP path; the reference's CPU branch (use_gpu = false) is not provided and
 // throws std::invalid_argument.
 #pragma once
@@ -11,13 +11,18 @@
 #include <cstddef>
 #include <vector>
 
+#include <string>
+
 #include "config.h"
+#include "model_loader.h"
 #include "tensor.h"
 
 class PhiMLP {
 public:
     // w1, w3: [F][H]; w2: [H][F] (nn.Linear layout).
     PhiMLP(Tensor w1, Tensor w2, Tensor w3);
+    // <prefix>.w1.weight, <prefix>.w2.weight, <prefix>.w3.weight
+    PhiMLP(const ModelLoader& loader, const std::string& prefix);
     // y = w2 . (silu(w1 . x) * (w3 . x)) row by row; y takes x's shape.  The
     // GPU path keeps the reference's fp32 arithmetic (src/layer.cu:49-67 with
     // matmul_pair_silu_gpu), so it matches the reference bit for bit.
@@ -37,6 +42,9 @@ public:
     // the expert FFN kernels: APS_DTYPE_F32 (the reference's arithmetic) or
     // APS_DTYPE_BF16 (MFMA, fp32 accumulate).  Routing is exact either way.
     PhiMoE(Tensor gate, std::vector<PhiMLP> experts, aps_dtype compute = APS_DTYPE_F32);
+    // model.layers.<layer_idx>.block_sparse_moe.gate.weight and
+    // ....experts.<e>.{w1,w2,w3}.weight for e < NUM_EXPERTS
+    PhiMoE(const ModelLoader& loader, std::size_t layer_idx, aps_dtype compute = APS_DTYPE_F32);
     // y [rows][H] = sum over the two routed experts of 0.5 * expert(x).
     void forward(const Tensor& x, Tensor& y, bool use_gpu = false) const;
 

@@ -300,3 +300,37 @@ def prefix_dedup(input_ids, vocab_size: int = 32064, max_positions: int = 4096):
 def gather_rows(x: np.ndarray, rows) -> np.ndarray:
     """out[i] = x[rows[i]] (reference k_gather_rows, src/tensor.cu:2635-2642)."""
     return np.ascontiguousarray(x[np.asarray(rows, dtype=np.int64)])
+
+
+def model_bin_index(data: bytes):
+    """The index of a model.bin image, pure Python (reference
+    src/model_loader.cu:14-31): u32 count, then per entry u32 name_len, the
+    name, u32 ndim, ndim u32 dims, u64 offset, u64 bytes, little-endian.
+    Returns {name: (shape, offset, bytes)} (first entry of a name wins);
+    raises RuntimeError("truncated model.bin") when the index runs past the
+    end."""
+    import struct
+    pos = 0
+
+    def take(fmt):
+        nonlocal pos
+        n = struct.calcsize(fmt)
+        if pos + n > len(data):
+            raise RuntimeError("truncated model.bin")
+        v = struct.unpack_from(fmt, data, pos)
+        pos += n
+        return v
+
+    (count,) = take("<I")
+    out = {}
+    for _ in range(count):
+        (name_len,) = take("<I")
+        if pos + name_len > len(data):
+            raise RuntimeError("truncated model.bin")
+        name = data[pos:pos + name_len].decode("utf-8", "surrogateescape")
+        pos += name_len
+        (ndim,) = take("<I")
+        shape = take(f"<{ndim}I") if ndim else ()
+        offset, nbytes = take("<QQ")
+        out.setdefault(name, (tuple(shape), offset, nbytes))
+    return out

@@ -1,6 +1,6 @@
 // GPU check of the C++ host API (include/tensor.h, include/layer.h).
 //
-//   layer_check <out_dir>
+//   layer_check <out_dir> [<model.bin>]
 //
 // Builds a small synthetic MoE layer (16 experts, H = 512, F = 128, 96
 // tokens), runs PhiMoE::forward in fp32 and bf16 compute and PhiMLP::forward
@@ -16,6 +16,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <fstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -84,14 +85,66 @@ void write_raw(const std::string& dir, const char* name, const Tensor& t) {
     std::fclose(f);
 }
 
+// Raw little-endian fields for hand-made model.bin files.
+void put_u32(std::string& b, uint32_t v) { b.append(reinterpret_cast<const char*>(&v), 4); }
+void put_u64(std::string& b, uint64_t v) { b.append(reinterpret_cast<const char*>(&v), 8); }
+std::string write_file(const std::string& path, const std::string& bytes) {
+    std::ofstream f(path, std::ios::binary);
+    f.write(bytes.data(), static_cast<std::streamsize>(bytes.size()));
+    return path;
+}
+
+// model.bin mode: PhiMoE(loader, 0) and PhiMLP(loader, <expert 0>) on the
+// tensor "x" of the file, fp32 compute, outputs written for the oracle
+// comparison; then the loader's error messages on hand-made files.
+int loader_check(const std::string& dir, const std::string& model) {
+    const ModelLoader loader(model);
+    expect(loader.has("x") && !loader.has("nope"), "ModelLoader::has");
+    const Tensor x = loader.load("x");
+    const PhiMoE moe(loader, 0);
+    Tensor y;
+    moe.forward(x, y, true);
+    const PhiMLP mlp(loader, "model.layers.0.block_sparse_moe.experts.0");
+    Tensor ymlp;
+    mlp.forward(x, ymlp, true);
+    write_raw(dir, "loader_y", y);
+    write_raw(dir, "loader_mlp_y", ymlp);
+    expect_throw<std::runtime_error>([&] { (void)loader.load("nope"); }, "missing tensor: nope", "missing tensor");
+    const std::string nofile = dir + "/absent.bin";
+    expect_throw<std::runtime_error>([&] { ModelLoader l(nofile); }, ("cannot open model: " + nofile).c_str(),
+                                     "cannot open");
+    const std::string trunc = write_file(dir + "/trunc.bin", std::string("\x01\x00", 2));
+    expect_throw<std::runtime_error>([&] { ModelLoader l(trunc); }, "truncated model.bin", "truncated index");
+    std::string b;
+    put_u32(b, 2);
+    put_u32(b, 1);
+    b += "b";
+    put_u32(b, 1);
+    put_u32(b, 3);
+    put_u64(b, 0);
+    put_u64(b, 8);  // 3 elements but 8 bytes
+    put_u32(b, 1);
+    b += "t";
+    put_u32(b, 1);
+    put_u32(b, 4);
+    put_u64(b, 4096);  // past the end of the file
+    put_u64(b, 16);
+    const ModelLoader bad(write_file(dir + "/bad.bin", b));
+    expect_throw<std::runtime_error>([&] { (void)bad.load("b"); }, "tensor is not float32: b", "not float32");
+    expect_throw<std::runtime_error>([&] { (void)bad.load("t"); }, "truncated tensor: t", "truncated tensor");
+    std::printf("layer_check (model.bin): %d failure(s)\n", g_failures);
+    return g_failures ? 1 : 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
-    if (argc != 2) {
-        std::fprintf(stderr, "usage: %s <out_dir>\n", argv[0]);
+    if (argc != 2 && argc != 3) {
+        std::fprintf(stderr, "usage: %s <out_dir> [<model.bin>]\n", argv[0]);
         return 2;
     }
     const std::string dir = argv[1];
+    if (argc == 3) return loader_check(dir, argv[2]);
     const std::size_t T = 96, H = 512, F = 128, E = apss26::NUM_EXPERTS;
     Rng rng(20260);
 

@@ -74,3 +74,52 @@ def test_layer_norm_ops_bit_exact(run):
     y2, v, _, _ = oracle.layer_norm(run["x"], run["ln_w"], run["ln_b"], eps=1e-5, residual=run["resid"])
     assert np.array_equal(run["ln_x"].view(np.uint32), v.view(np.uint32))
     assert np.array_equal(run["add_y"].view(np.uint32), y2.view(np.uint32))
+
+
+def test_layers_from_model_bin(tmp_path, gpu_device):
+    """The reference's constructors PhiMoE(loader, layer_idx) and
+    PhiMLP(loader, prefix) (src/layer.cu:44-47, 94-111) on a model.bin
+    written by aps2026_amd.model_loader: the fp32 block and the dense FFN
+    equal the oracle bit for bit; the check program also checks ModelLoader's
+    error messages on hand-made files."""
+    from aps2026_amd.model_loader import moe_layer_tensors, write_model_bin
+    rng = np.random.default_rng(11)
+    Tm = 64
+    x = rng.standard_normal((Tm, H)).astype(np.float32)
+    gate = (0.02 * rng.standard_normal((E, H))).astype(np.float32)
+    w1 = (0.02 * rng.standard_normal((E, F, H))).astype(np.float32)
+    w2 = (0.02 * rng.standard_normal((E, H, F))).astype(np.float32)
+    w3 = (0.02 * rng.standard_normal((E, F, H))).astype(np.float32)
+    tensors = moe_layer_tensors(0, gate, list(w1), list(w2), list(w3))
+    tensors["x"] = x
+    model = tmp_path / "model.bin"
+    write_model_bin(str(model), tensors)
+    print(f"running {BIN} (model.bin mode)", flush=True)
+    res = subprocess.run([BIN, str(tmp_path), str(model)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, f"layer_check failed:\n{res.stdout}\n{res.stderr}"
+    y = np.fromfile(tmp_path / "loader_y.f32", dtype=np.float32).reshape(Tm, H)
+    ymlp = np.fromfile(tmp_path / "loader_mlp_y.f32", dtype=np.float32).reshape(Tm, H)
+    ref = oracle.reference_path(x, gate, w1, w3, w2)
+    assert np.array_equal(y.view(np.uint32), ref["out"].view(np.uint32))
+    want = oracle.ffn_rows(x, np.zeros(Tm, np.int32), w1[:1], w3[:1], w2[:1])
+    assert np.array_equal(ymlp.view(np.uint32), want.view(np.uint32))
+
+
+def test_python_loader_to_device(tmp_path, gpu_device):
+    from aps2026_amd.model_loader import ModelLoader, write_model_bin
+    a = np.random.default_rng(2).standard_normal((33, 129)).astype(np.float32)
+    write_model_bin(str(tmp_path / "m.bin"), {"a": a})
+    t = ModelLoader(str(tmp_path / "m.bin")).load("a", device=gpu_device)
+    assert t.is_cuda and np.array_equal(t.cpu().numpy().view(np.uint32), a.view(np.uint32))
+
+
+def test_python_loader_load_all(tmp_path, gpu_device):
+    """load_all (reads overlapped with uploads through two pinned buffers)
+    returns every tensor intact, in order, for more tensors than buffers."""
+    from aps2026_amd.model_loader import ModelLoader, write_model_bin
+    rng = np.random.default_rng(5)
+    ts = {f"t{i}": rng.standard_normal((rng.integers(1, 300), 7)).astype(np.float32) for i in range(9)}
+    write_model_bin(str(tmp_path / "m.bin"), ts)
+    got = ModelLoader(str(tmp_path / "m.bin")).load_all(list(ts), device=gpu_device)
+    for (name, want), g in zip(ts.items(), got):
+        assert np.array_equal(g.cpu().numpy().view(np.uint32), want.view(np.uint32)), name
