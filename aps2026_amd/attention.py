@@ -1,0 +1,105 @@
+"""Rotary embedding and GQA tree attention over prefix-trie rows, over the C
+ABI (include/aps_moe.h).
+
+Reference API mirrored (file:line in the reference tree):
+  tensor_ops::apply_rope_tree_gpu   include/tensor.h:100-103, src/tensor.cu:3342-3359
+  tensor_ops::attention_tree_gpu    include/tensor.h:109-114, src/tensor.cu:3361-3377
+  rope_table                        src/tensor.cu:2703-2735 (host tables)
+
+Rows are the nodes of the prompts' prefix trie (aps2026_amd.prefix): a
+node's RoPE position is its depth and its keys are its ancestor chain, so
+attention needs no expansion back to token rows.  Shapes as the reference:
+q [rows, q_heads * 128], k and v [rows, kv_heads * 128], fp32, q_heads =
+4 kv_heads.  Errors raise ValueError with the reference's messages
+("attention_tree_gpu expects GQA-4").
+"""
+from __future__ import annotations
+
+from typing import Dict, Tuple, Union
+
+import numpy as np
+import torch
+
+from . import capi
+from .moe import _call, _ptr, _stream
+
+NUM_ATTENTION_HEADS = 16   # reference include/config.h:10
+NUM_KV_HEADS = 4           # include/config.h:11
+HEAD_DIM = 128             # include/config.h:12
+SLIDING_WINDOW = 2047      # include/config.h:17
+ROPE_THETA = 10000.0       # include/config.h:18
+
+_tables: Dict[Tuple[torch.device, int, int, float], Tuple[torch.Tensor, torch.Tensor]] = {}
+
+
+def rope_table(max_seq: int, head_dim: int = HEAD_DIM, theta: float = ROPE_THETA) -> Tuple[np.ndarray, np.ndarray]:
+    """(cos, sin) [max_seq, head_dim / 2], the reference's host tables."""
+    half = head_dim // 2
+    c = np.empty((max_seq, half), np.float32)
+    s = np.empty((max_seq, half), np.float32)
+    _call(capi.lib().aps_rope_table(max_seq, head_dim, theta, c.ctypes.data_as(capi._c_vp),
+                                    s.ctypes.data_as(capi._c_vp)))
+    return c, s
+
+
+def _device_table(device: torch.device, max_seq: int, head_dim: int, theta: float):
+    """Device copies of the tables, kept per device and grown on demand (the
+    reference keeps one static table, src/tensor.cu:2703-2712)."""
+    key = (device, head_dim, float(theta))
+    have = _tables.get(key)
+    if have is None or have[0].shape[0] < max_seq:
+        c, s = rope_table(max_seq, head_dim, theta)
+        have = (torch.from_numpy(c).to(device), torch.from_numpy(s).to(device))
+        _tables[key] = have
+    return have
+
+
+def _rows_u32(t: Union[torch.Tensor, np.ndarray], device) -> torch.Tensor:
+    if isinstance(t, torch.Tensor):
+        return t.to(device=device, dtype=torch.int32).contiguous()
+    return torch.from_numpy(np.ascontiguousarray(np.asarray(t, dtype=np.uint32)).view(np.int32)).to(device)
+
+
+def apply_rope_tree_gpu(q: torch.Tensor, k: torch.Tensor, row_pos, max_seq: int,
+                        q_heads: int = NUM_ATTENTION_HEADS, kv_heads: int = NUM_KV_HEADS,
+                        head_dim: int = HEAD_DIM, theta: float = ROPE_THETA) -> None:
+    """RoPE in place on q and k at each row's position (reference
+    src/tensor.cu:3342-3359)."""
+    rows = q.shape[0]
+    if q.numel() != rows * q_heads * head_dim or k.numel() != rows * kv_heads * head_dim:
+        raise ValueError("apply_rope_tree_gpu shape")
+    if q.dtype != torch.float32 or k.dtype != torch.float32 or not q.is_contiguous() or not k.is_contiguous():
+        raise ValueError("apply_rope_tree_gpu expects contiguous fp32 tensors")
+    pos = _rows_u32(row_pos, q.device)
+    if rows and int(pos.max().item()) >= max_seq:
+        raise ValueError("apply_rope_tree_gpu position past max_seq")
+    c, s = _device_table(q.device, max_seq, head_dim, theta)
+    _call(capi.lib().aps_rope_tree(_ptr(q), _ptr(k), _ptr(pos), rows, q_heads, kv_heads, head_dim, _ptr(c), _ptr(s),
+                                   c.shape[0], _stream(q.device)))
+
+
+def attention_tree_gpu(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor, row_pos, anc,
+                       anc_stride: int, q_heads: int = NUM_ATTENTION_HEADS, kv_heads: int = NUM_KV_HEADS,
+                       head_dim: int = HEAD_DIM, window: int = SLIDING_WINDOW) -> torch.Tensor:
+    """out = softmax attention of each row over its ancestor chain (reference
+    src/tensor.cu:3361-3377)."""
+    if q_heads != 4 * kv_heads:
+        raise ValueError("attention_tree_gpu expects GQA-4")
+    rows = q.shape[0]
+    for t, h in ((q, q_heads), (k, kv_heads), (v, kv_heads), (out, q_heads)):
+        if t.numel() != rows * h * head_dim or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("attention_tree_gpu shape")
+    pos = _rows_u32(row_pos, q.device)
+    a = _rows_u32(anc, q.device)
+    if rows:
+        if int(pos.max().item()) >= anc_stride or a.numel() < rows * anc_stride:
+            raise ValueError("attention_tree_gpu ancestor table")
+        # every key a row can see must be a row of this batch
+        used = a.view(rows, anc_stride).to(torch.int64) & 0xFFFFFFFF
+        cols = torch.arange(anc_stride, device=q.device)
+        live = cols[None, :] <= pos.to(torch.int64)[:, None]
+        if bool((used[live] >= rows).any()):
+            raise ValueError("attention_tree_gpu ancestor index")
+    _call(capi.lib().aps_attention_tree(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(pos), _ptr(a), anc_stride, rows,
+                                        q_heads, kv_heads, head_dim, window, _stream(q.device)))
+    return out

@@ -10,6 +10,7 @@
 //    performs no allocation and no host synchronisation;
 //  * errors are status codes plus a thread-local message instead of C++
 //    exceptions crossing the ABI.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -555,6 +556,56 @@ int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int64_t bat
                                      node_depth, node_anc, anc_stride, nodes, err);
     if (rc == 1) return fail(APS_ERR_ARG, "%s", err.c_str());
     if (rc != 0) return fail(APS_ERR_SHAPE, "prefix dedup: %s", err.c_str());
+    return APS_OK;
+}
+
+int aps_rope_table(int64_t max_seq, int32_t head_dim, float theta, float* cos_out, float* sin_out) {
+    if (max_seq < 0 || head_dim <= 0 || head_dim % 2 != 0)
+        return fail(APS_ERR_SHAPE, "rope table shape: max_seq %lld head_dim %d", (long long)max_seq, head_dim);
+    if (max_seq > 0 && (!cos_out || !sin_out)) return fail(APS_ERR_ARG, "rope table: NULL pointer");
+    // reference src/tensor.cu:2716-2725: float arithmetic through powf / cosf / sinf
+    const int32_t half = head_dim / 2;
+    for (int64_t p = 0; p < max_seq; ++p)
+        for (int32_t j = 0; j < half; ++j) {
+            const float ex = (-2.0f * static_cast<float>(j)) / static_cast<float>(head_dim);
+            const float inv = powf(theta, ex);
+            const float ang = static_cast<float>(p) * inv;
+            cos_out[p * half + j] = cosf(ang);
+            sin_out[p * half + j] = sinf(ang);
+        }
+    return APS_OK;
+}
+
+int aps_rope_tree(float* q, float* k, const uint32_t* row_pos, int64_t rows, int32_t q_heads, int32_t kv_heads,
+                  int32_t head_dim, const float* cos_table, const float* sin_table, int64_t max_seq, void* stream) {
+    if (rows < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || max_seq < 0)
+        return fail(APS_ERR_SHAPE, "rope shape: rows %lld heads %d/%d head_dim %d", (long long)rows, q_heads,
+                    kv_heads, head_dim);
+    if (rows == 0) return APS_OK;
+    if (!q || !k || !row_pos || !cos_table || !sin_table) return fail(APS_ERR_ARG, "rope: NULL pointer");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    APS_HIP(aps::launch_rope_tree(q, row_pos, rows, q_heads, head_dim, cos_table, sin_table, max_seq, s),
+            "rope launch");
+    APS_HIP(aps::launch_rope_tree(k, row_pos, rows, kv_heads, head_dim, cos_table, sin_table, max_seq, s),
+            "rope launch");
+    return APS_OK;
+}
+
+int aps_attention_tree(const float* q, const float* k, const float* v, float* out, const uint32_t* row_pos,
+                       const uint32_t* anc, int64_t anc_stride, int64_t rows, int32_t q_heads, int32_t kv_heads,
+                       int32_t head_dim, int32_t window, void* stream) {
+    // reference src/tensor.cu:3367-3368: "attention_tree_gpu expects GQA-4"
+    if (kv_heads <= 0 || q_heads != 4 * kv_heads)
+        return fail(APS_ERR_SHAPE, "attention_tree_gpu expects GQA-4");
+    if (rows < 0 || head_dim != 128 || anc_stride <= 0 || window <= 0)
+        return fail(APS_ERR_SHAPE, "attention tree shape: rows %lld head_dim %d (128 only) anc_stride %lld window %d",
+                    (long long)rows, head_dim, (long long)anc_stride, window);
+    if (rows == 0) return APS_OK;
+    if (!q || !k || !v || !out || !row_pos || !anc) return fail(APS_ERR_ARG, "attention tree: NULL pointer");
+    if ((reinterpret_cast<uintptr_t>(k) & 15u) != 0) return fail(APS_ERR_ARG, "attention tree: k must be 16-byte aligned");
+    APS_HIP(aps::launch_attention_tree(q, k, v, out, row_pos, anc, anc_stride, rows, q_heads, kv_heads, head_dim,
+                                       window, static_cast<hipStream_t>(stream)),
+            "attention tree launch");
     return APS_OK;
 }
 

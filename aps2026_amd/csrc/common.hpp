@@ -136,6 +136,16 @@ int prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int64_t batch, 
                  uint32_t* token_node, uint32_t* node_token, uint32_t* node_depth, uint32_t* node_anc,
                  int64_t anc_stride, int64_t* nodes_out, std::string& err);
 
+// RoPE in place on x [rows][heads][head_dim] at each row's position (pairs
+// j, j + head_dim / 2); rows whose position is >= max_seq are left as they are.
+hipError_t launch_rope_tree(float* x, const uint32_t* row_pos, int64_t rows, int heads, int head_dim,
+                            const float* cosv, const float* sinv, int64_t max_seq, hipStream_t s);
+
+// GQA-4 tree attention, head_dim 128 (the reference kernel's arithmetic).
+hipError_t launch_attention_tree(const float* q, const float* k, const float* v, float* out, const uint32_t* row_pos,
+                                 const uint32_t* anc, int64_t anc_stride, int64_t rows, int q_heads, int kv_heads,
+                                 int head_dim, int window_max, hipStream_t s);
+
 hipError_t launch_layer_norm(float* x, const float* residual, const float* weight, const float* bias, float* y,
                              int64_t rows, int hidden, float eps, hipStream_t s);
 hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_counts,

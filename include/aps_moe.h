@@ -295,6 +295,38 @@ APS_API int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int
                              int64_t max_positions, uint32_t* token_node, uint32_t* node_token, uint32_t* node_depth,
                              uint32_t* node_anc, int64_t anc_stride, int64_t* nodes);
 
+/* ---- attention over the prefix trie (scope row f4) --------------------- */
+
+/* The RoPE tables of the reference's rope_table (src/tensor.cu:2703-2735),
+ * host code: cos/sin [max_seq][head_dim / 2] with inv = powf(theta,
+ * (-2 j) / head_dim), cos = cosf(p * inv), sin = sinf(p * inv). */
+APS_API int aps_rope_table(int64_t max_seq, int32_t head_dim, float theta, float* cos_out, float* sin_out);
+
+/* Replaces tensor_ops::apply_rope_tree_gpu (reference include/tensor.h:
+ * 100-103, src/tensor.cu:3342-3359, kernel k_rope :2180-2197): in place on
+ * q [rows][q_heads][head_dim] and k [rows][kv_heads][head_dim], pair (j, j +
+ * head_dim / 2) rotated by the table row at row_pos[row]:
+ * x0' = fma(x0, c, -(x1 s)), x1' = fma(x1, c, x0 s).  cos_table / sin_table
+ * are device copies of aps_rope_table's output; rows whose position is >=
+ * max_seq are left unchanged. */
+APS_API int aps_rope_tree(float* q, float* k, const uint32_t* row_pos, int64_t rows, int32_t q_heads,
+                          int32_t kv_heads, int32_t head_dim, const float* cos_table, const float* sin_table,
+                          int64_t max_seq, void* stream);
+
+/* Replaces tensor_ops::attention_tree_gpu (reference include/tensor.h:
+ * 109-114, src/tensor.cu:3361-3377, kernel k_attention_tree_gqa4
+ * :2407-2633): for each row and query head, softmax attention over the keys
+ * anc[row][begin .. pos] (pos = row_pos[row], begin = max(0, pos + 1 -
+ * window); the reference's window is SLIDING_WINDOW = 2047), with the
+ * reference kernel's arithmetic.  q [rows][q_heads][128], k, v
+ * [rows][kv_heads][128], out [rows][q_heads][128], fp32; q_heads = 4 kv_heads
+ * ("attention_tree_gpu expects GQA-4"); head_dim 128; k 16-byte aligned.
+ * Ancestor entries must be < rows and positions < anc_stride (the kernel
+ * clamps them, for memory safety only). */
+APS_API int aps_attention_tree(const float* q, const float* k, const float* v, float* out, const uint32_t* row_pos,
+                               const uint32_t* anc, int64_t anc_stride, int64_t rows, int32_t q_heads,
+                               int32_t kv_heads, int32_t head_dim, int32_t window, void* stream);
+
 /* ---- diagnostics ------------------------------------------------------- */
 
 APS_API const char* aps_moe_last_error(void);

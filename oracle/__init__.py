@@ -58,6 +58,10 @@ def lib():
         L.oracle_layer_norm.argtypes = [_f32p, ctypes.c_void_p, _i64, _i32, _f32p, _f32p, ctypes.c_float,
                                         ctypes.c_void_p, _f32p, ctypes.c_void_p, ctypes.c_void_p]
         L.oracle_default_quantum.restype = ctypes.c_float
+        L.oracle_rope_table.argtypes = [_i64, _i32, ctypes.c_float, _f32p, _f32p]
+        L.oracle_rope_tree.argtypes = [_f32p, _u32p, _i64, _i32, _i32, _f32p, _f32p]
+        L.oracle_attention_tree.argtypes = [_f32p, _f32p, _f32p, _f32p, _u32p, _u32p, _i64, _i64, _i32, _i32,
+                                            _i32, _i32]
         L.oracle_default_tie_eps.restype = ctypes.c_float
         L.oracle_num_threads.restype = ctypes.c_int
         L.oracle_set_num_threads.argtypes = [ctypes.c_int]
@@ -333,4 +337,38 @@ def model_bin_index(data: bytes):
         shape = take(f"<{ndim}I") if ndim else ()
         offset, nbytes = take("<QQ")
         out.setdefault(name, (tuple(shape), offset, nbytes))
+    return out
+
+
+SLIDING_WINDOW = 2047   # reference include/config.h:17
+ROPE_THETA = 10000.0    # reference include/config.h:18
+
+
+def rope_table(max_seq: int, head_dim: int, theta: float = ROPE_THETA):
+    """(cos, sin) [max_seq, head_dim / 2] fp32 (reference src/tensor.cu:2703-2735)."""
+    half = head_dim // 2
+    c = np.empty((max_seq, half), np.float32)
+    sn = np.empty((max_seq, half), np.float32)
+    lib().oracle_rope_table(max_seq, head_dim, theta, c, sn)
+    return c, sn
+
+
+def rope_tree(x: np.ndarray, row_pos, heads: int, head_dim: int, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """RoPE of x [rows, heads * head_dim] at each row's position (reference
+    k_rope, src/tensor.cu:2180-2197); returns a new array."""
+    y = _c(x, np.float32).copy()
+    pos = _c(row_pos, np.uint32)
+    lib().oracle_rope_tree(y, pos, pos.shape[0], heads, head_dim, _c(cos, np.float32), _c(sin, np.float32))
+    return y
+
+
+def attention_tree(q, k, v, row_pos, anc, anc_stride: int, q_heads: int, kv_heads: int, head_dim: int,
+                   window_max: int = SLIDING_WINDOW) -> np.ndarray:
+    """GQA tree attention over ancestor chains (reference
+    k_attention_tree_gqa4, src/tensor.cu:2407-2633); out [rows, q_heads * head_dim]."""
+    pos = _c(row_pos, np.uint32)
+    rows = pos.shape[0]
+    out = np.empty((rows, q_heads * head_dim), np.float32)
+    lib().oracle_attention_tree(_c(q, np.float32), _c(k, np.float32), _c(v, np.float32), out, pos,
+                                _c(anc, np.uint32), anc_stride, rows, q_heads, kv_heads, head_dim, window_max)
     return out

@@ -475,3 +475,107 @@ ORACLE_API void oracle_layer_norm(const float* x, const float* residual, int64_t
         }
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* Tree attention of the prefix-deduplicated rows (scope row f4).
+ *
+ * RoPE table, reference src/tensor.cu:2703-2735 (host code, float
+ * arithmetic through std::pow / std::cos / std::sin on floats, i.e. glibc's
+ * powf / cosf / sinf):
+ *   inv = powf(theta, (-2.0f * j) / head_dim);  cos[p][j] = cosf(p * inv),
+ *   sin[p][j] = sinf(p * inv)                  (p * inv rounded to float)
+ * RoPE, src/tensor.cu:2180-2197 (k_rope), pair (j, j + half) of each head at
+ * the row's position:
+ *   x0' = fma(x0, c, -(x1 * s)),  x1' = fma(x1, c, x0 * s)
+ * (the reference's `x0 * c - x1 * s` and `x1 * c + x0 * s` as contracted by
+ * the LLVM rule that fuses the left product; which product nvcc fuses is not
+ * fixed by the source: parity unpinned at that last rounding).
+ * Attention, src/tensor.cu:2407-2633 (k_attention_tree_gqa4), per row, KV
+ * head kh and query head qh = 4 kh + g:
+ *   pos = row_pos[row]; begin = pos + 1 > window_max ? pos + 1 - window_max : 0
+ *   key w (0 <= w <= pos - begin) is row anc[row][begin + w]
+ *   a_j = fma chain over d = j, j + 4, ... ascending of q[d] * k[d]  (j < 4)
+ *   s_w = ((a_0 + a_1) + (a_2 + a_3)) * (1 / sqrtf(head_dim))
+ *   m = max_w s_w;  e_w = (float)exp((double)(s_w - m))
+ *   den = fp32 sum of e_w, w ascending;  p_w = e_w / den
+ *   out[d] = fma chain over w ascending of p_w * v[key w][d]
+ * exp is glibc's double exp here and ROCm's in the kernel (the reference:
+ * CUDA's): all within an ulp of double, so the float results agree except in
+ * the rare case of a double within an ulp of a float rounding boundary. */
+ORACLE_API void oracle_rope_table(int64_t max_seq, int32_t head_dim, float theta, float* cosv, float* sinv) {
+    const int32_t half = head_dim / 2;
+    for (int64_t p = 0; p < max_seq; ++p)
+        for (int32_t j = 0; j < half; ++j) {
+            volatile float ex = (-2.0f * (float)j) / (float)head_dim;
+            const float inv = powf(theta, ex);
+            volatile float ang = (float)p * inv;
+            cosv[p * half + j] = cosf(ang);
+            sinv[p * half + j] = sinf(ang);
+        }
+}
+
+ORACLE_API void oracle_rope_tree(float* x, const uint32_t* row_pos, int64_t rows, int32_t heads, int32_t head_dim,
+                                 const float* cosv, const float* sinv) {
+    const int32_t half = head_dim / 2;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r)
+        for (int32_t h = 0; h < heads; ++h) {
+            float* base = x + (r * heads + h) * (int64_t)head_dim;
+            const int64_t t = (int64_t)row_pos[r] * half;
+            for (int32_t j = 0; j < half; ++j) {
+                const float c = cosv[t + j], s = sinv[t + j];
+                const float x0 = base[j], x1 = base[j + half];
+                volatile float x1s = x1 * s, x0s = x0 * s;
+                base[j] = fmaf(x0, c, -x1s);
+                base[j + half] = fmaf(x1, c, x0s);
+            }
+        }
+}
+
+ORACLE_API void oracle_attention_tree(const float* q, const float* k, const float* v, float* out,
+                                      const uint32_t* row_pos, const uint32_t* anc, int64_t anc_stride, int64_t rows,
+                                      int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t window_max) {
+    volatile float root = sqrtf((float)head_dim);
+    const float scale = 1.0f / root;
+    const int32_t group = q_heads / kv_heads;
+#pragma omp parallel
+    {
+        float* e = (float*)malloc(sizeof(float) * (size_t)(window_max > 0 ? window_max : 1));
+#pragma omp for schedule(dynamic, 4)
+        for (int64_t row = 0; row < rows; ++row) {
+            const int64_t pos = row_pos[row];
+            const int64_t begin = pos + 1 > window_max ? pos + 1 - window_max : 0;
+            const int64_t window = pos - begin + 1;
+            const uint32_t* chain = anc + row * anc_stride + begin;
+            for (int32_t qh = 0; qh < q_heads; ++qh) {
+                const int32_t kh = qh / group;
+                const float* qv = q + (row * q_heads + qh) * (int64_t)head_dim;
+                float m = -3.402823466e+38F;
+                for (int64_t w = 0; w < window; ++w) {
+                    const float* kv = k + ((int64_t)chain[w] * kv_heads + kh) * head_dim;
+                    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int32_t d = 0; d < head_dim; ++d) a[d & 3] = fmaf(qv[d], kv[d], a[d & 3]);
+                    volatile float s01 = a[0] + a[1], s23 = a[2] + a[3];
+                    volatile float s = s01 + s23;
+                    e[w] = s * scale;
+                    m = fmaxf(m, e[w]);
+                }
+                float den = 0.0f;
+                for (int64_t w = 0; w < window; ++w) {
+                    volatile float t = e[w] - m;
+                    e[w] = (float)exp((double)t);
+                    den += e[w];
+                }
+                for (int64_t w = 0; w < window; ++w) e[w] = e[w] / den;
+                float* o = out + (row * q_heads + qh) * (int64_t)head_dim;
+                for (int32_t d = 0; d < head_dim; ++d) {
+                    float val = 0.0f;
+                    for (int64_t w = 0; w < window; ++w)
+                        val = fmaf(e[w], v[((int64_t)chain[w] * kv_heads + kh) * head_dim + d], val);
+                    o[d] = val;
+                }
+            }
+        }
+        free(e);
+    }
+}

@@ -1,0 +1,109 @@
+"""GPU parity of the tree attention row (reference apply_rope_tree_gpu and
+attention_tree_gpu, src/tensor.cu:3342-3377): RoPE and attention through the
+C ABI against the oracle bit for bit on prefix-trie batches (the reference's
+16 query / 4 KV heads, head_dim 128), with the sliding window exercised at
+its real size by a 2,100-token sequence and at a small size; node rows
+against token rows; the GQA-4 error."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from aps2026_amd import attention, prefix
+from tests.test_attention import trie_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def dev(a, d):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(d)
+
+
+def shared_batch(seed, groups=3, per=3, pre=40, suf=30):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(groups):
+        p = rng.integers(0, 32064, pre).tolist()
+        for _ in range(per):
+            out.append(p + rng.integers(0, 32064, rng.integers(1, suf)).tolist())
+    return out
+
+
+def test_rope_bit_exact(gpu_device):
+    note("rope tree")
+    batch = shared_batch(1) + [list(range(1, 300))]
+    plan, q, k, _ = trie_inputs(batch, q_heads=16, kv_heads=4, seed=1)
+    qd, kd = dev(q, gpu_device), dev(k, gpu_device)
+    attention.apply_rope_tree_gpu(qd, kd, plan.node_depth, max_seq=4096)
+    torch.cuda.synchronize()
+    c, s = oracle.rope_table(4096, 128)
+    np.testing.assert_array_equal(qd.cpu().numpy().view(np.uint32),
+                                  oracle.rope_tree(q, plan.node_depth, 16, 128, c, s).view(np.uint32))
+    np.testing.assert_array_equal(kd.cpu().numpy().view(np.uint32),
+                                  oracle.rope_tree(k, plan.node_depth, 4, 128, c, s).view(np.uint32))
+
+
+@pytest.mark.parametrize("window", [2047, 5])
+def test_attention_bit_exact(gpu_device, window):
+    note(f"attention tree window={window}")
+    batch = shared_batch(2 + window)
+    plan, q, k, v = trie_inputs(batch, q_heads=16, kv_heads=4, seed=window)
+    out = torch.empty((plan.nodes, 16 * 128), dtype=torch.float32, device=gpu_device)
+    attention.attention_tree_gpu(dev(q, gpu_device), dev(k, gpu_device), dev(v, gpu_device), out,
+                                 plan.node_depth, plan.node_anc, plan.max_len, window=window)
+    torch.cuda.synchronize()
+    want = oracle.attention_tree(q, k, v, plan.node_depth, plan.node_anc, plan.max_len, 16, 4, 128, window)
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_attention_long_sequence_sliding_window(gpu_device):
+    """One 2,100-token prompt: rows past position 2046 see exactly the last
+    2,047 keys (the reference's SLIDING_WINDOW)."""
+    note("attention tree 2100-token sequence")
+    batch = [list(np.random.default_rng(3).integers(0, 32064, 2100))]
+    plan, q, k, v = trie_inputs(batch, q_heads=4, kv_heads=1, seed=3)
+    rows = np.arange(plan.nodes - 64, plan.nodes)   # the last 64 rows: full windows
+    out = torch.empty((plan.nodes, 4 * 128), dtype=torch.float32, device=gpu_device)
+    attention.attention_tree_gpu(dev(q, gpu_device), dev(k, gpu_device), dev(v, gpu_device), out,
+                                 plan.node_depth, plan.node_anc, plan.max_len, q_heads=4, kv_heads=1)
+    torch.cuda.synchronize()
+    want = oracle.attention_tree(q[rows], k, v, plan.node_depth[rows], plan.node_anc[rows], plan.max_len, 4, 1, 128)
+    np.testing.assert_array_equal(out.cpu().numpy()[rows].view(np.uint32), want.view(np.uint32))
+
+
+def test_attention_nodes_equal_token_rows(gpu_device):
+    note("attention tree nodes vs token rows")
+    batch = shared_batch(4, groups=2, per=4, pre=60, suf=20)
+    plan, q, k, v = trie_inputs(batch, q_heads=16, kv_heads=4, seed=4)
+    tn = plan.token_node.astype(np.int64)
+    total = tn.shape[0]
+    tanc = np.zeros((total, plan.max_len), np.uint32)
+    tpos = np.zeros(total, np.uint32)
+    for off, ln in zip(plan.offsets, plan.seq_lens):
+        for si in range(ln):
+            tpos[off + si] = si
+            tanc[off + si, :si + 1] = np.arange(off, off + si + 1)
+    o_nodes = torch.empty((plan.nodes, 16 * 128), dtype=torch.float32, device=gpu_device)
+    o_toks = torch.empty((total, 16 * 128), dtype=torch.float32, device=gpu_device)
+    attention.attention_tree_gpu(dev(q, gpu_device), dev(k, gpu_device), dev(v, gpu_device), o_nodes,
+                                 plan.node_depth, plan.node_anc, plan.max_len)
+    attention.attention_tree_gpu(dev(q[tn], gpu_device), dev(k[tn], gpu_device), dev(v[tn], gpu_device), o_toks,
+                                 tpos, tanc, plan.max_len)
+    torch.cuda.synchronize()
+    assert torch.equal(o_toks.view(torch.int32), o_nodes[torch.from_numpy(tn).to(gpu_device)].view(torch.int32))
+
+
+def test_attention_errors(gpu_device):
+    x = torch.zeros((2, 5 * 128), dtype=torch.float32, device=gpu_device)
+    kv = torch.zeros((2, 128), dtype=torch.float32, device=gpu_device)
+    with pytest.raises(ValueError, match="expects GQA-4"):
+        attention.attention_tree_gpu(x, kv, kv, x.clone(), [0, 1], np.array([[0, 0], [0, 1]]), 2, q_heads=5,
+                                     kv_heads=1)
+    q = torch.zeros((2, 4 * 128), dtype=torch.float32, device=gpu_device)
+    with pytest.raises(ValueError, match="ancestor index"):
+        attention.attention_tree_gpu(q, kv, kv, q.clone(), [0, 1], np.array([[0, 0], [0, 7]]), 2, q_heads=4,
+                                     kv_heads=1)
