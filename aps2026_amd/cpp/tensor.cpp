@@ -443,3 +443,94 @@ void gather_rows_gpu(const Tensor& x, const RowIndexBuffer& rows, Tensor& out) {
 }
 
 }  // namespace tensor_ops
+
+// ---- tree attention (reference src/tensor.cu:2703-2735, 3342-3377) ----------
+
+namespace {
+
+// Device RoPE tables, one set per (device, head_dim, theta), grown on demand
+// (the reference keeps one static table).
+struct RopeTables {
+    std::mutex mu;
+    struct Entry {
+        int dev;
+        std::size_t half;
+        float theta;
+        std::size_t max_seq;
+        float* cosv;
+        float* sinv;
+    };
+    std::vector<Entry> entries;
+};
+RopeTables g_rope;
+
+RopeTables::Entry rope_tables(std::size_t max_seq, std::size_t head_dim, float theta) {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_rope.mu);
+    RopeTables::Entry* e = nullptr;
+    for (auto& x : g_rope.entries)
+        if (x.dev == dev && x.half == head_dim / 2 && x.theta == theta) e = &x;
+    if (e && e->max_seq >= max_seq) return *e;
+    const std::size_t half = head_dim / 2, n = max_seq * half;
+    std::vector<float> c(n ? n : 1), s(n ? n : 1);
+    const int rc = aps_rope_table(static_cast<int64_t>(max_seq), static_cast<int32_t>(head_dim), theta, c.data(),
+                                  s.data());
+    if (rc) throw_status(rc, "apply_rope_tree_gpu");
+    float *dc = nullptr, *ds = nullptr;
+    hip_check(hipMalloc(&dc, c.size() * sizeof(float)), "hipMalloc rope cosine");
+    hip_check(hipMalloc(&ds, s.size() * sizeof(float)), "hipMalloc rope sine");
+    hip_check(hipMemcpy(dc, c.data(), c.size() * sizeof(float), hipMemcpyHostToDevice), "copy rope cosine");
+    hip_check(hipMemcpy(ds, s.data(), s.size() * sizeof(float), hipMemcpyHostToDevice), "copy rope sine");
+    if (e) {
+        // the old tables may still be read by queued kernels: the legacy
+        // default stream orders this free after them
+        hip_check(hipDeviceSynchronize(), "rope table resize");
+        (void)hipFree(e->cosv);
+        (void)hipFree(e->sinv);
+        e->cosv = dc;
+        e->sinv = ds;
+        e->max_seq = max_seq;
+        return *e;
+    }
+    g_rope.entries.push_back({dev, half, theta, max_seq, dc, ds});
+    return g_rope.entries.back();
+}
+
+}  // namespace
+
+namespace tensor_ops {
+
+void apply_rope_tree_gpu(Tensor& q, Tensor& k, const std::uint32_t* row_pos, std::size_t rows, std::size_t max_seq,
+                         std::size_t q_heads, std::size_t kv_heads, std::size_t head_dim, float theta) {
+    if (q.size() != rows * q_heads * head_dim || k.size() != rows * kv_heads * head_dim || head_dim % 2 != 0)
+        throw std::invalid_argument("apply_rope_tree_gpu shape");
+    if (rows == 0) return;
+    const RopeTables::Entry t = rope_tables(max_seq, head_dim, theta);
+    q.cuda_data();
+    k.cuda_data();
+    const int rc = aps_rope_tree(q.cuda_data_write(), k.cuda_data_write(), row_pos, static_cast<int64_t>(rows),
+                                 static_cast<int32_t>(q_heads), static_cast<int32_t>(kv_heads),
+                                 static_cast<int32_t>(head_dim), t.cosv, t.sinv, static_cast<int64_t>(t.max_seq),
+                                 nullptr);
+    if (rc) throw_status(rc, "apply_rope_tree_gpu");
+}
+
+void attention_tree_gpu(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out, const std::uint32_t* row_pos,
+                        const std::uint32_t* anc, std::size_t anc_stride, std::size_t rows, std::size_t max_seq,
+                        std::size_t q_heads, std::size_t kv_heads, std::size_t head_dim) {
+    if (q_heads != 4 * kv_heads) throw std::invalid_argument("attention_tree_gpu expects GQA-4");
+    if (q.size() != rows * q_heads * head_dim || k.size() != rows * kv_heads * head_dim ||
+        v.size() != k.size() || out.size() != q.size())
+        throw std::invalid_argument("attention_tree_gpu shape");
+    (void)max_seq;  // the window is SLIDING_WINDOW; the ancestor stride bounds the chains
+    if (rows == 0) return;
+    const int rc = aps_attention_tree(q.cuda_data(), k.cuda_data(), v.cuda_data(), out.cuda_data_write(), row_pos, anc,
+                                      static_cast<int64_t>(anc_stride), static_cast<int64_t>(rows),
+                                      static_cast<int32_t>(q_heads), static_cast<int32_t>(kv_heads),
+                                      static_cast<int32_t>(head_dim), static_cast<int32_t>(apss26::SLIDING_WINDOW),
+                                      nullptr);
+    if (rc) throw_status(rc, "attention_tree_gpu");
+}
+
+}  // namespace tensor_ops

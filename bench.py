@@ -211,6 +211,18 @@ def main():
             gd = torch.Generator(device=dev).manual_seed(4)
             emb = torch.randn((prefix.VOCAB_SIZE, H), generator=gd, device=dev)
             node_rows = prefix.RowIndexBuffer(plan.node_token, dev)
+            # attention inputs (the q/k/v projections are not built: synthetic
+            # q, k, v of the reference's 16 query / 4 KV heads of 128)
+            from aps2026_amd import attention
+            qa = (0.5 * torch.randn((T, 16 * 128), generator=gd, device=dev)).contiguous()
+            ka = (0.5 * torch.randn((T, 4 * 128), generator=gd, device=dev)).contiguous()
+            va = torch.randn((T, 4 * 128), generator=gd, device=dev)
+            oa = torch.empty((T, 16 * 128), dtype=torch.float32, device=dev)
+            pos_d = attention._rows_u32(plan.node_depth, dev)
+            anc_d = attention._rows_u32(plan.node_anc, dev)
+            cos_d, sin_d = attention._device_table(dev, plan.max_len, 128, attention.ROPE_THETA)
+            windows = np.minimum(plan.node_depth.astype(np.int64) + 1, attention.SLIDING_WINDOW)
+            attn_flops = float(windows.sum()) * 16 * 128 * 4   # scores and values, 2 FLOP per FMA
     elif bf16:
         x = dev_bits(inp.packed["x_bf16"])
     else:
@@ -264,12 +276,20 @@ def main():
     if c4:
         args_gather = (ctypes.c_void_p(emb.data_ptr()), emb.shape[0], H, ctypes.c_void_p(node_rows.data.data_ptr()),
                        T, ctypes.c_void_p(resid.data_ptr()), sptr)
+        args_rope = (ctypes.c_void_p(qa.data_ptr()), ctypes.c_void_p(ka.data_ptr()), ctypes.c_void_p(pos_d.data_ptr()),
+                     T, 16, 4, 128, ctypes.c_void_p(cos_d.data_ptr()), ctypes.c_void_p(sin_d.data_ptr()),
+                     cos_d.shape[0], sptr)
+        args_attn = (ctypes.c_void_p(qa.data_ptr()), ctypes.c_void_p(ka.data_ptr()), ctypes.c_void_p(va.data_ptr()),
+                     ctypes.c_void_p(oa.data_ptr()), ctypes.c_void_p(pos_d.data_ptr()),
+                     ctypes.c_void_p(anc_d.data_ptr()), plan.max_len, T, 16, 4, 128, attention.SLIDING_WINDOW, sptr)
 
     def step(i):
         if c4:
-            rc = L.aps_gather_rows(*args_gather)
-            if rc:
-                raise RuntimeError(capi.last_error())
+            for fn, a in ((L.aps_gather_rows, args_gather), (L.aps_rope_tree, args_rope),
+                          (L.aps_attention_tree, args_attn)):
+                rc = fn(*a)
+                if rc:
+                    raise RuntimeError(capi.last_error())
         if c3:
             rc = L.aps_add_layer_norm(*args_ln)
             if rc:
@@ -321,7 +341,7 @@ def main():
     else:
         stages = ["router_logits", "route_top2", "dispatch", "ffn_up", "ffn_down", "combine"]
     if c3:
-        stages = (["gather_rows"] if c4 else []) + ["add_layer_norm"] + stages
+        stages = (["gather_rows", "rope", "attention_tree"] if c4 else []) + ["add_layer_norm"] + stages
         L.aps_add_layer_norm(*args_ln)
         xb = x.to(torch.bfloat16)  # the FFN's bf16 copy of the norm output (the fused path makes its own)
     times = {s: [] for s in stages}
@@ -330,7 +350,8 @@ def main():
         w = layers[i % LAYERS]
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
         ev[0].record(stream)
-        calls = [lambda: L.aps_gather_rows(*args_gather)] if c4 else []
+        calls = ([lambda: L.aps_gather_rows(*args_gather), lambda: L.aps_rope_tree(*args_rope),
+                  lambda: L.aps_attention_tree(*args_attn)] if c4 else [])
         calls += [lambda: L.aps_add_layer_norm(*args_ln)] if c3 else []
         calls += [
             lambda: L.aps_router_logits(p(x), xd, p(gate), T, H, E, p(logits), sptr),
@@ -397,6 +418,11 @@ def main():
         # gather: node rows read from the embedding table and written, plus the indices
         stage_report["gather_rows"] = {"us": mean_t["gather_rows"] * 1e6,
                                        "GB_s": (2.0 * T * H * 4 + T * 4) / mean_t["gather_rows"] / 1e9}
+        stage_report["rope"] = {"us": mean_t["rope"] * 1e6,
+                                "GB_s": 2.0 * T * 20 * 128 * 4 / mean_t["rope"] / 1e9}
+        stage_report["attention_tree"] = {"us": mean_t["attention_tree"] * 1e6,
+                                          "TFLOP_s": attn_flops / mean_t["attention_tree"] / 1e12,
+                                          "flops": attn_flops}
         stage_report["prefix_dedup_host"] = {"ms": statistics.median(dedup_s) * 1e3, "prompt_tokens": prompt_tokens,
                                              "nodes": T, "threads": 1}
     achieved = flops_up / mean_t["ffn_up"]
@@ -431,8 +457,10 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8" if fp8 else ("bf16" if bf16 else "f32"), "data": "synthetic (seeded PCG64 normals, random-init weights)",
         "config": {"workload": (f"c4: 16 prompts x 1024 ids (groups of 4 share a 512-id prefix) deduplicated to "
-                                f"{T} prefix-trie rows; per step the embedding gather of those rows, then the "
-                                f"decoder post-attention half (add_layer_norm fp32 + MoE FFN block, hidden {H}, "
+                                f"{T} prefix-trie rows; per step the embedding gather of those rows, RoPE and GQA "
+                                f"tree attention (16/4 heads of 128, synthetic q/k/v: the projections are not "
+                                f"built), then the decoder post-attention half (add_layer_norm fp32 + MoE FFN "
+                                f"block, hidden {H}, "
                                 f"{E} experts top-2, ffn {F}, bf16 experts) on them; value counts the "
                                 f"{prompt_tokens} prompt tokens; the trie itself is host code, timed in stages"
                                 if c4 else

@@ -1,7 +1,7 @@
 // Model constants of the MoE block, under the reference's names
 // (include/config.h:5-27 of the reference: namespace apss26).  Only the
-// constants the MoE feed-forward path, its LayerNorm and the prompt prefix
-// deduplication read are kept here.
+// constants the MoE feed-forward path, its LayerNorm, the prompt prefix
+// deduplication and the tree attention read are kept here.
 #pragma once
 
 #include <cstddef>
@@ -22,4 +22,10 @@ constexpr float NORM_EPS = 1.0e-5f;
 // include/config.h:7, 16).
 constexpr std::size_t VOCAB_SIZE = 32064;
 constexpr std::size_t MAX_POSITION_EMBEDDINGS = 4096;
+// Attention of the decoder layer (reference include/config.h:10-12, 17-18).
+constexpr std::size_t NUM_ATTENTION_HEADS = 16;
+constexpr std::size_t NUM_KV_HEADS = 4;
+constexpr std::size_t HEAD_DIM = 128;
+constexpr std::size_t SLIDING_WINDOW = 2047;
+constexpr float ROPE_THETA = 10000.0f;
 }  // namespace apss26

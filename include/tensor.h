@@ -151,4 +151,22 @@ private:
 // include/tensor.h:138, src/tensor.cu:3420-3426); same checks as above.
 void gather_rows_gpu(const Tensor& x, const RowIndexBuffer& rows, Tensor& out);
 
+// RoPE in place on q [rows][q_heads * head_dim] and k [rows][kv_heads *
+// head_dim] at the device positions row_pos[rows] (reference
+// include/tensor.h:100-103, src/tensor.cu:3342-3359): the cos/sin tables of
+// max_seq positions are built on the host once per (head_dim, theta) and
+// kept on the device, grown when a larger max_seq arrives.  Positions must
+// be < max_seq (a row past the table is left unchanged).
+void apply_rope_tree_gpu(Tensor& q, Tensor& k, const std::uint32_t* row_pos, std::size_t rows, std::size_t max_seq,
+                         std::size_t q_heads, std::size_t kv_heads, std::size_t head_dim, float theta);
+
+// Attention of each row over its ancestor chain anc[row][0 .. row_pos[row]]
+// (device arrays; the last SLIDING_WINDOW keys), GQA-4, head_dim 128
+// (reference include/tensor.h:109-114, src/tensor.cu:3361-3377).  Throws
+// std::invalid_argument("attention_tree_gpu expects GQA-4") as the
+// reference does; out must hold rows x q_heads x head_dim values.
+void attention_tree_gpu(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out, const std::uint32_t* row_pos,
+                        const std::uint32_t* anc, std::size_t anc_stride, std::size_t rows, std::size_t max_seq,
+                        std::size_t q_heads, std::size_t kv_heads, std::size_t head_dim);
+
 }  // namespace tensor_ops

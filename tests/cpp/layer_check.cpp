@@ -234,6 +234,31 @@ int main(int argc, char** argv) {
                                             "gather_rows_gpu shape", "gather output size");
     }
 
+    // --- tree attention on a small trie: RoPE, then attention ----------------
+    {
+        const PrefixTrie trie = build_prefix_trie({{5, 6, 7, 8, 9}, {5, 6, 7, 1}, {2, 3}});
+        const std::size_t n = trie.nodes(), qh = apss26::NUM_ATTENTION_HEADS, kvh = apss26::NUM_KV_HEADS,
+                          hd = apss26::HEAD_DIM;
+        Tensor aq = random_tensor({n, qh * hd}, rng, 1.0f), ak = random_tensor({n, kvh * hd}, rng, 1.0f),
+               av = random_tensor({n, kvh * hd}, rng, 1.0f);
+        write_raw(dir, "attn_q", aq);
+        write_raw(dir, "attn_k", ak);
+        write_raw(dir, "attn_v", av);
+        const tensor_ops::RowIndexBuffer pos(trie.node_depth), anc(trie.node_anc);
+        tensor_ops::apply_rope_tree_gpu(aq, ak, pos.data(), n, apss26::MAX_POSITION_EMBEDDINGS, qh, kvh, hd,
+                                        apss26::ROPE_THETA);
+        Tensor ao({n, qh * hd});
+        tensor_ops::attention_tree_gpu(aq, ak, av, ao, pos.data(), anc.data(), trie.max_len, n,
+                                       apss26::MAX_POSITION_EMBEDDINGS, qh, kvh, hd);
+        write_raw(dir, "attn_qr", aq);
+        write_raw(dir, "attn_kr", ak);
+        write_raw(dir, "attn_out", ao);
+        expect_throw<std::invalid_argument>(
+            [&] { tensor_ops::attention_tree_gpu(aq, ak, av, ao, pos.data(), anc.data(), trie.max_len, n, 4096, 16, 2,
+                                                 hd); },
+            "attention_tree_gpu expects GQA-4", "GQA-4 check");
+    }
+
     // --- Tensor synchronisation rules ----------------------------------------
     {
         Tensor t({4, 8});

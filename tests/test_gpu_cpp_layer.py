@@ -44,6 +44,7 @@ def run(tmp_path_factory, gpu_device):
          "ln_w": load("ln_w", (H,)), "ln_b": load("ln_b", (H,)), "resid": load("resid", (T, H)),
          "ln_y": load("ln_y", (T, H)), "ln_x": load("ln_x", (T, H)), "add_y": load("add_y", (T, H))}
     d["ref"] = oracle.reference_path(d["x"], d["gate"], d["w1"], d["w3"], d["w2"])
+    d["dir"] = out
     return d
 
 
@@ -123,3 +124,22 @@ def test_python_loader_load_all(tmp_path, gpu_device):
     got = ModelLoader(str(tmp_path / "m.bin")).load_all(list(ts), device=gpu_device)
     for (name, want), g in zip(ts.items(), got):
         assert np.array_equal(g.cpu().numpy().view(np.uint32), want.view(np.uint32)), name
+
+
+def test_tree_attention_ops_bit_exact(run):
+    """tensor_ops::apply_rope_tree_gpu and attention_tree_gpu through the C++
+    API on a 3-prompt trie (16 query / 4 KV heads): rotated q, k and the
+    attention output equal the oracle bit for bit."""
+    from aps2026_amd import prefix
+    plan = prefix.prefix_dedup([[5, 6, 7, 8, 9], [5, 6, 7, 1], [2, 3]])
+    n = plan.nodes
+    d = run["dir"]
+    ld = lambda name, w: np.fromfile(d / f"{name}.f32", dtype=np.float32).reshape(n, w)
+    q, k, v = ld("attn_q", 2048), ld("attn_k", 512), ld("attn_v", 512)
+    c, s_ = oracle.rope_table(4096, 128)
+    qr = oracle.rope_tree(q, plan.node_depth, 16, 128, c, s_)
+    kr = oracle.rope_tree(k, plan.node_depth, 4, 128, c, s_)
+    assert np.array_equal(ld("attn_qr", 2048).view(np.uint32), qr.view(np.uint32))
+    assert np.array_equal(ld("attn_kr", 512).view(np.uint32), kr.view(np.uint32))
+    want = oracle.attention_tree(qr, kr, v, plan.node_depth, plan.node_anc, plan.max_len, 16, 4, 128)
+    assert np.array_equal(ld("attn_out", 2048).view(np.uint32), want.view(np.uint32))
