@@ -145,6 +145,33 @@ def test_c2_bf16_zipf_parity(gpu_device):
     w.release()
 
 
+def test_large_batch_65536_tokens(gpu_device):
+    """A batch 16x C2 (65,536 tokens, bf16, Zipf loads): 8,192-row expert
+    groups, work lists of thousands of tiles, a 1024-tile histogram.  Logits
+    and the whole routing plan bit-exact; expert FFN and block output on a
+    sample of tokens within the bf16 bar."""
+    T = 65536
+    note(f"large batch T={T}")
+    inp = synth.make_config("c2", T=T)
+    w = weights_for(inp, gpu_device)
+    x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+    out = moe.moe_forward_gpu(x, gate, w, out_dtype=torch.bfloat16)
+    plan = w.plan_views(T)
+    torch.cuda.synchronize()
+    ref = oracle_routing(inp)
+    np.testing.assert_array_equal(plan["logits"].cpu().numpy().view(np.uint32), ref["logits"].view(np.uint32))
+    check_plan(plan, ref, T)
+    rng = np.random.default_rng(1)
+    toks = np.unique(np.concatenate([np.arange(16), np.arange(T - 16, T), rng.choice(T, 96, replace=False)]))
+    y_ref = oracle.ffn_rows(np.repeat(inp.x[toks], 2, axis=0), ref["routes"][toks].reshape(-1), inp.w1, inp.w3,
+                            inp.w2)
+    out_ref = (0.5 * (y_ref[0::2].astype(np.float64) + y_ref[1::2])).astype(np.float32)
+    err = rowwise_err(bf16_to_np(out)[toks], out_ref)
+    note(f"large batch sample max normwise err {err.max():.3e}")
+    assert err.max() <= TOL_BF16
+    w.release()
+
+
 def test_c2_deterministic_and_entry_points_agree(gpu_device):
     note("C2 determinism + fused vs grouped vs staged entry points (T=1024)")
     inp = synth.make_config("c2", T=1024)
@@ -193,7 +220,7 @@ def test_router_kernel_shapes(gpu_device, E, H):
         w.release()
 
 
-@pytest.mark.parametrize("E,T", [(16, 20000), (24, 5000), (64, 9000), (2, 3000)])
+@pytest.mark.parametrize("E,T", [(16, 20000), (24, 5000), (64, 9000), (2, 3000), (16, 1 << 20)])
 def test_dispatch_many_tiles(gpu_device, E, T):
     """The staged dispatch on random routes over many 64-token tiles (more
     than one batch of histogram loads per wave, partial last workgroup),
