@@ -353,7 +353,7 @@ int aps_router_logits(const void* x, int32_t x_dtype, const float* gate, int64_t
         return fail(APS_ERR_DTYPE, "router x dtype %d not supported", x_dtype);
     if (rows > 0 && (!x || !gate || !logits)) return fail(APS_ERR_ARG, "router: NULL pointer");
     APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, hidden, num_experts, logits, nullptr,
-                               nullptr, static_cast<hipStream_t>(stream)),
+                               nullptr, nullptr, static_cast<hipStream_t>(stream)),
             "router_logits launch");
     return APS_OK;
 }
@@ -662,13 +662,17 @@ int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float
     if (!gate) return fail(APS_ERR_ARG, "forward: NULL gate");
     char* ws = static_cast<char*>(workspace);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // logits, routes and the tile histogram in one kernel; the grouped path
+    // logits, routes and the tile histogram in one kernel (and, for fp32 x
+    // with a bf16 weight set, the FFN's bf16 copy of x); the grouped path
     // then starts at the dispatch
     float* logits = reinterpret_cast<float*>(ws + L.logits);
     auto* routes = reinterpret_cast<uint8_t*>(ws + L.routes);
     auto* tiles = reinterpret_cast<uint32_t*>(ws + L.tile_counts);
-    APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, w->H, w->E, logits, routes, tiles, s),
+    const bool copy = x_dtype == APS_DTYPE_F32 && w->compute == APS_DTYPE_BF16;
+    auto* xb = copy ? reinterpret_cast<aps::bf16_t*>(ws + L.xq) : nullptr;
+    APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, w->H, w->E, logits, routes, tiles, xb, s),
             "router launch");
+    if (copy) return grouped_from_logits(*w, xb, false, nullptr, rows, out, out_dtype, ws, L, s);
     return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, nullptr, rows, out, out_dtype, ws, L, s);
 }
 

@@ -115,10 +115,11 @@ __device__ inline RowTile wave_find_tile(int tile, int bm, uint32_t lo, uint32_t
 // ---- launchers (defined in the .hip files) --------------------------------
 
 // Router GEMM; with routes != nullptr also the top-2 routes and the tile
-// histogram (tile_counts), in the same kernel.
+// histogram (tile_counts), in the same kernel; with x_copy != nullptr (fp32
+// x only) also the bf16 copy of x [rows][hidden].
 hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t rows, int hidden,
                          int experts, float* logits, uint8_t* routes, uint32_t* tile_counts,
-                         hipStream_t s);
+                         bf16_t* x_copy, hipStream_t s);
 hipError_t launch_route_top2(const float* logits, int64_t rows, int experts, uint8_t* routes,
                              uint32_t* tile_counts, hipStream_t s);
 hipError_t launch_tile_hist(const uint8_t* routes, int64_t rows, int experts,

@@ -181,15 +181,31 @@ struct RInt {
     static constexpr int value = V;
 };
 
+// Two fp32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32), the
+// same conversion as the library's standalone fp32 -> bf16 kernel.
+__device__ inline uint32_t r_pack2_bf16(float lo, float hi) {
+    typedef __bf16 rbf16x2_t __attribute__((ext_vector_type(2)));
+    rbf16x2_t v;
+    v[0] = static_cast<__bf16>(lo);
+    v[1] = static_cast<__bf16>(hi);
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // One workgroup = 16 tokens x 16 R expert lanes.  logits [rows][E] always;
-// routes [rows][2] and the tile histogram when routes != nullptr.  A ring
+// routes [rows][2] and the tile histogram when routes != nullptr.  XCOPY
+// (fp32 x only): the bf16 copy of x the expert FFN reads is written on the
+// way, each lane storing its 8 converted elements of every window (the R
+// rows of a token and the clamped rows past the end store identical values),
+// which spares the FFN path a separate conversion pass over x.  A ring
 // stage holds GW windows; H is a multiple of GW * 128, so every stage is full
 // and the step sequence has no run-time bounds (the compiler can then count
 // the LDS reads in flight instead of draining them).
-template <bool XBF16, int R, int GW>
+template <bool XBF16, int R, int GW, bool XCOPY = false>
 __global__ void __launch_bounds__(256 * R)
 k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, int E,
-         float* __restrict__ logits, uint8_t* __restrict__ routes, uint8_t* __restrict__ tile_bytes) {
+         float* __restrict__ logits, uint8_t* __restrict__ routes, uint8_t* __restrict__ tile_bytes,
+         bf16_t* __restrict__ xcopy) {
+    static_assert(!(XCOPY && XBF16), "the bf16 copy is made from fp32 x");
     constexpr int kGW = GW;                    // windows per ring stage
     constexpr int kWinBytes = 8 * 1024 * R;    // 32 (k/4) x 16 R experts x 16 B
     constexpr int kElt = XBF16 ? 2 : 4;
@@ -217,6 +233,7 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
     // dropped)
     const uint8_t* xsrc = static_cast<const uint8_t*>(xv) +
                           ((t < rows ? t : rows - 1) * static_cast<int64_t>(H) + 8 * (lane & 15)) * kElt;
+    bf16_t* xdst = XCOPY ? xcopy + (t < rows ? t : rows - 1) * static_cast<int64_t>(H) + 8 * (lane & 15) : nullptr;
     // gate copies: copy i of a stage (i = 0 .. 2 kGW - 1) is instruction
     // a = w + 4R i of the stage and fills bytes [a KB, a KB + 1 KB): window
     // i / 2 of the stage, piece (w + 4R (i % 2)) * 64 + lane of the window,
@@ -267,6 +284,14 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
         float c[kGW][8];
 #pragma unroll
         for (int wi = 0; wi < kGW; ++wi) r_elements(c[wi], xr[P][wi]);
+        if constexpr (XCOPY) {
+#pragma unroll
+            for (int wi = 0; wi < kGW; ++wi) {
+                const ru32x4_t pk = {r_pack2_bf16(c[wi][0], c[wi][1]), r_pack2_bf16(c[wi][2], c[wi][3]),
+                                     r_pack2_bf16(c[wi][4], c[wi][5]), r_pack2_bf16(c[wi][6], c[wi][7])};
+                *reinterpret_cast<ru32x4_t*>(xdst + (g * kGW + wi) * kRWin) = pk;
+            }
+        }
         if (g + 1 < NG) issue_x(xr[P ^ 1], g + 1);
         const uint32_t gaddr = P ? gaddr1 : gaddr0;
         rf32x4_t gs[3][4];
@@ -371,16 +396,23 @@ k_route_top2(const float* __restrict__ logits, int64_t rows, int E, uint8_t* __r
 
 hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t rows, int hidden,
                          int experts, float* logits, uint8_t* routes, uint32_t* tile_counts,
-                         hipStream_t s) {
+                         bf16_t* x_copy, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (hidden <= 0 || hidden % (2 * kRWin) != 0 || experts <= 0 || experts > kMaxExperts)
         return hipErrorInvalidValue;
     if (routes && (experts < 2 || !tile_counts)) return hipErrorInvalidValue;
+    if (x_copy && x_bf16) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>(ceil_div(rows, kRTokens)));
     auto* tb = reinterpret_cast<uint8_t*>(tile_counts);
-#define APS_ROUTER_LAUNCH(XB, R, GW)                                                                    \
-    hipLaunchKernelGGL((k_router<XB, R, GW>), grid, dim3(256 * R), 0, s, x, gate, rows, hidden, experts, \
-                       logits, routes, tb)
+#define APS_ROUTER_LAUNCH(XB, R, GW)                                                                      \
+    do {                                                                                                  \
+        if (!(XB) && x_copy)                                                                             \
+            hipLaunchKernelGGL((k_router<false, R, GW, true>), grid, dim3(256 * R), 0, s, x, gate, rows, \
+                               hidden, experts, logits, routes, tb, x_copy);                             \
+        else                                                                                             \
+            hipLaunchKernelGGL((k_router<XB, R, GW>), grid, dim3(256 * R), 0, s, x, gate, rows, hidden,  \
+                               experts, logits, routes, tb, nullptr);                                    \
+    } while (0)
     // windows per stage: 512 steps of 16 R experts (32 KB) when H allows
     const int R = experts <= 16 ? 1 : experts <= 32 ? 2 : 4;
     const bool wide = hidden % (4 * kRWin) == 0;
