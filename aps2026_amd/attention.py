@@ -94,11 +94,11 @@ def attention_tree_gpu(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: t
     if rows:
         if int(pos.max().item()) >= anc_stride or a.numel() < rows * anc_stride:
             raise ValueError("attention_tree_gpu ancestor table")
-        # every key a row can see must be a row of this batch
-        used = a.view(rows, anc_stride).to(torch.int64) & 0xFFFFFFFF
-        cols = torch.arange(anc_stride, device=q.device)
-        live = cols[None, :] <= pos.to(torch.int64)[:, None]
-        if bool((used[live] >= rows).any()):
+        # every key a row can see must be a row of this batch (the u32 table
+        # is viewed as int32: entries >= 2^31 read as negative)
+        tab = a[:rows * anc_stride].view(rows, anc_stride)
+        live = torch.arange(anc_stride, device=q.device)[None, :] <= pos[:, None]
+        if bool((((tab < 0) | (tab >= rows)) & live).any()):
             raise ValueError("attention_tree_gpu ancestor index")
     _call(capi.lib().aps_attention_tree(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(pos), _ptr(a), anc_stride, rows,
                                         q_heads, kv_heads, head_dim, window, _stream(q.device)))
