@@ -2,6 +2,7 @@
 ABI (include/aps_moe.h).
 
 Reference API mirrored (file:line in the reference tree):
+  Linear::forward (projections)     src/layer.cu:30-42, src/tensor.cu:3120-3143
   tensor_ops::apply_rope_tree_gpu   include/tensor.h:100-103, src/tensor.cu:3342-3359
   tensor_ops::attention_tree_gpu    include/tensor.h:109-114, src/tensor.cu:3361-3377
   rope_table                        src/tensor.cu:2703-2735 (host tables)
@@ -58,6 +59,27 @@ def _rows_u32(t: Union[torch.Tensor, np.ndarray], device) -> torch.Tensor:
     if isinstance(t, torch.Tensor):
         return t.to(device=device, dtype=torch.int32).contiguous()
     return torch.from_numpy(np.ascontiguousarray(np.asarray(t, dtype=np.uint32)).view(np.int32)).to(device)
+
+
+def linear_gpu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor = None,
+               out: torch.Tensor = None) -> torch.Tensor:
+    """y = x weight^T (+ bias), fp32, each output one FMA chain over k
+    ascending and the bias added once: the decoder's Linear layers (reference
+    src/layer.cu:30-42, src/tensor.cu:3120-3143, kernel :715-800)."""
+    k = x.shape[-1]
+    rows = x.numel() // k if k else 0
+    n = weight.shape[0]
+    if weight.shape[1] != k or (bias is not None and bias.numel() != n):
+        raise ValueError("matmul_transposed_bias_gpu shape")
+    for t in (x, weight) + ((bias,) if bias is not None else ()):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("linear_gpu expects contiguous fp32 tensors")
+    if out is None:
+        out = torch.empty((rows, n), dtype=torch.float32, device=x.device)
+    elif out.numel() != rows * n or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("matmul_transposed_bias_gpu shape")
+    _call(capi.lib().aps_linear(_ptr(x), _ptr(weight), _ptr(bias), rows, k, n, _ptr(out), _stream(x.device)))
+    return out
 
 
 def apply_rope_tree_gpu(q: torch.Tensor, k: torch.Tensor, row_pos, max_seq: int,

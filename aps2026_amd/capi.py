@@ -103,6 +103,7 @@ def lib():
     L.aps_layer_norm.argtypes = [_c_vp, _c_vp, _c_vp, i64, i32, ctypes.c_float, _c_vp, _c_vp]
     L.aps_add_layer_norm.argtypes = [_c_vp, _c_vp, _c_vp, _c_vp, i64, i32, ctypes.c_float, _c_vp, _c_vp]
     L.aps_gather_rows.argtypes = [_c_vp, i64, i64, _c_vp, i64, _c_vp, _c_vp]
+    L.aps_linear.argtypes = [_c_vp, _c_vp, _c_vp, i64, i32, i32, _c_vp, _c_vp]
     L.aps_rope_table.argtypes = [i64, i32, ctypes.c_float, _c_vp, _c_vp]
     L.aps_rope_tree.argtypes = [_c_vp, _c_vp, _c_vp, i64, i32, i32, i32, _c_vp, _c_vp, i64, _c_vp]
     L.aps_attention_tree.argtypes = [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, i64, i64, i32, i32, i32, i32, _c_vp]
@@ -113,7 +114,7 @@ def lib():
                  "aps_moe_combine", "aps_moe_forward_grouped", "aps_moe_forward", "aps_moe_ffn_up",
                  "aps_moe_ffn_down", "aps_mlp_forward", "aps_quantise_rows_e4m3", "aps_moe_ffn_up_fp8",
                  "aps_moe_ffn_down_fp8", "aps_layer_norm", "aps_add_layer_norm", "aps_gather_rows",
-                 "aps_prefix_dedup", "aps_rope_table", "aps_rope_tree", "aps_attention_tree"):
+                 "aps_prefix_dedup", "aps_linear", "aps_rope_table", "aps_rope_tree", "aps_attention_tree"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

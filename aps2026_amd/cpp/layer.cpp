@@ -70,3 +70,59 @@ void PhiMoE::forward(const Tensor& x, Tensor& y, bool use_gpu) const {
     if (rows) tensor_ops::matmul_transposed_gpu(x, gate_, router);
     tensor_ops::moe_forward_grouped_gpu(x, router, gpu_weights_handle_, y);
 }
+
+// ---- Linear and PhiAttention (reference src/layer.cu:21-42, 150-188) --------
+
+Linear::Linear(Tensor weight, Tensor bias) : weight_(std::move(weight)), bias_(std::move(bias)) {
+    if (weight_.ndim() != 2 || (bias_.size() && bias_.size() != weight_.size(0)))
+        throw std::invalid_argument("Linear weight shapes");
+}
+
+Linear::Linear(const ModelLoader& loader, const std::string& weight, const std::string& bias)
+    : Linear(loader.load(weight), bias.empty() ? Tensor() : loader.load(bias)) {}
+
+void Linear::forward(const Tensor& x, Tensor& y, bool use_gpu) const {
+    if (!use_gpu) throw std::invalid_argument("Linear::forward: the CPU path (use_gpu = false) is not provided");
+    const std::size_t rows = x.size() / x.size(x.ndim() - 1);
+    y = Tensor({rows, weight_.size(0)});
+    if (bias_.size())
+        tensor_ops::matmul_transposed_bias_gpu(x, weight_, bias_, y);
+    else
+        tensor_ops::matmul_transposed_gpu(x, weight_, y);
+}
+
+namespace {
+std::string attn_name(std::size_t layer, const char* proj, const char* what) {
+    return "model.layers." + std::to_string(layer) + ".self_attn." + proj + "." + what;
+}
+}  // namespace
+
+PhiAttention::PhiAttention(const ModelLoader& loader, std::size_t layer_idx)
+    : q_proj_(loader, attn_name(layer_idx, "q_proj", "weight"), attn_name(layer_idx, "q_proj", "bias")),
+      k_proj_(loader, attn_name(layer_idx, "k_proj", "weight"), attn_name(layer_idx, "k_proj", "bias")),
+      v_proj_(loader, attn_name(layer_idx, "v_proj", "weight"), attn_name(layer_idx, "v_proj", "bias")),
+      o_proj_(loader, attn_name(layer_idx, "o_proj", "weight"), attn_name(layer_idx, "o_proj", "bias")) {}
+
+PhiAttention::PhiAttention(Linear q_proj, Linear k_proj, Linear v_proj, Linear o_proj)
+    : q_proj_(std::move(q_proj)), k_proj_(std::move(k_proj)), v_proj_(std::move(v_proj)), o_proj_(std::move(o_proj)) {}
+
+void PhiAttention::forward(const Tensor& x, Tensor& y, const std::vector<std::size_t>& seq_lens, bool use_gpu,
+                           const PrefixExpansion& expansion) const {
+    (void)seq_lens;  // the trie path takes positions and key chains from the expansion
+    if (!use_gpu) throw std::invalid_argument("PhiAttention::forward: the CPU path (use_gpu = false) is not provided");
+    if (!expansion.active() || !expansion.node_pos)
+        throw std::invalid_argument("PhiAttention::forward: this build provides the prefix-trie path (an active expansion)");
+    const std::size_t s = x.size(0);
+    Tensor q, k, v;
+    q_proj_.forward(x, q, true);
+    k_proj_.forward(x, k, true);
+    v_proj_.forward(x, v, true);
+    tensor_ops::apply_rope_tree_gpu(q, k, expansion.node_pos->data(), s, expansion.max_seq,
+                                    apss26::NUM_ATTENTION_HEADS, apss26::NUM_KV_HEADS, apss26::HEAD_DIM,
+                                    apss26::ROPE_THETA);
+    Tensor out({s, apss26::NUM_ATTENTION_HEADS * apss26::HEAD_DIM});
+    tensor_ops::attention_tree_gpu(q, k, v, out, expansion.node_pos->data(), expansion.node_anc->data(),
+                                   expansion.anc_stride, s, expansion.max_seq, apss26::NUM_ATTENTION_HEADS,
+                                   apss26::NUM_KV_HEADS, apss26::HEAD_DIM);
+    o_proj_.forward(out, y, true);
+}

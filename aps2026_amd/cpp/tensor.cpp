@@ -218,14 +218,32 @@ void matmul_transposed_gpu(const Tensor& a, const Tensor& b, Tensor& c) {
     const std::size_t n = b.size(0);
     if (b.size(1) != k || c.size(0) != m || c.size(1) != n)
         throw std::invalid_argument("matmul_transposed_gpu shape");
-    if (n > 64 || k % 256 != 0)
-        throw std::invalid_argument("matmul_transposed_gpu: this build covers the router shape (n <= 64, k % 256 == 0)");
     const float* da = a.cuda_data();
     const float* db = b.cuda_data();
-    float* dc = c.cuda_data_write();
-    const int rc = aps_router_logits(da, APS_DTYPE_F32, db, static_cast<int64_t>(m), static_cast<int32_t>(k),
-                                     static_cast<int32_t>(n), dc, nullptr);
+    if (n <= 64 && k % 256 == 0) {  // the router shape: the router kernel
+        const int rc = aps_router_logits(da, APS_DTYPE_F32, db, static_cast<int64_t>(m), static_cast<int32_t>(k),
+                                         static_cast<int32_t>(n), c.cuda_data_write(), nullptr);
+        if (rc) throw_status(rc, "matmul_transposed_gpu");
+        return;
+    }
+    if (k % 16 != 0 || n % 4 != 0)
+        throw std::invalid_argument("matmul_transposed_gpu: this build needs k % 16 == 0 and n % 4 == 0");
+    const int rc = aps_linear(da, db, nullptr, static_cast<int64_t>(m), static_cast<int32_t>(k),
+                              static_cast<int32_t>(n), c.cuda_data_write(), nullptr);
     if (rc) throw_status(rc, "matmul_transposed_gpu");
+}
+
+void matmul_transposed_bias_gpu(const Tensor& a, const Tensor& b, const Tensor& bias, Tensor& c) {
+    const std::size_t k = a.size(a.ndim() - 1);
+    const std::size_t m = a.size() / k;
+    const std::size_t n = b.size(0);
+    if (b.size(1) != k || c.size(0) != m || c.size(1) != n || bias.size() != n)
+        throw std::invalid_argument("matmul_transposed_bias_gpu shape");
+    if (k % 16 != 0 || n % 4 != 0)
+        throw std::invalid_argument("matmul_transposed_bias_gpu: this build needs k % 16 == 0 and n % 4 == 0");
+    const int rc = aps_linear(a.cuda_data(), b.cuda_data(), bias.cuda_data(), static_cast<int64_t>(m),
+                              static_cast<int32_t>(k), static_cast<int32_t>(n), c.cuda_data_write(), nullptr);
+    if (rc) throw_status(rc, "matmul_transposed_bias_gpu");
 }
 
 void layer_norm_gpu(const Tensor& x, const Tensor& weight, const Tensor& bias, float eps, Tensor& y) {

@@ -559,6 +559,25 @@ int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int64_t bat
     return APS_OK;
 }
 
+int aps_linear(const float* x, const float* weight, const float* bias, int64_t rows, int32_t in_features,
+               int32_t out_features, float* y, void* stream) {
+    if (rows < 0 || in_features <= 0 || out_features <= 0 || in_features % 16 != 0 || out_features % 4 != 0 ||
+        (rows + 63) / 64 > 65535)
+        return fail(APS_ERR_SHAPE,
+                    "linear shape: rows %lld in %d (multiple of 16) out %d (multiple of 4)", (long long)rows,
+                    in_features, out_features);
+    if (rows == 0) return APS_OK;
+    if (!x || !weight || !y) return fail(APS_ERR_ARG, "linear: NULL pointer");
+    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
+          reinterpret_cast<uintptr_t>(y)) & 15u) != 0)
+        return fail(APS_ERR_ARG, "linear: arrays must be 16-byte aligned");
+    if (y == x) return fail(APS_ERR_ARG, "linear: y must not alias x");
+    APS_HIP(aps::launch_linear_f32(x, weight, bias, y, rows, in_features, out_features,
+                                   static_cast<hipStream_t>(stream)),
+            "linear launch");
+    return APS_OK;
+}
+
 int aps_rope_table(int64_t max_seq, int32_t head_dim, float theta, float* cos_out, float* sin_out) {
     if (max_seq < 0 || head_dim <= 0 || head_dim % 2 != 0)
         return fail(APS_ERR_SHAPE, "rope table shape: max_seq %lld head_dim %d", (long long)max_seq, head_dim);

@@ -147,6 +147,11 @@ hipError_t launch_attention_tree(const float* q, const float* k, const float* v,
                                  const uint32_t* anc, int64_t anc_stride, int64_t rows, int q_heads, int kv_heads,
                                  int head_dim, int window_max, hipStream_t s);
 
+// y = x w^T (+ bias): fp32 FMA chain over k ascending per output, bias added
+// once (in_f % 16 == 0, out_f % 4 == 0).
+hipError_t launch_linear_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows, int in_f,
+                             int out_f, hipStream_t s);
+
 hipError_t launch_layer_norm(float* x, const float* residual, const float* weight, const float* bias, float* y,
                              int64_t rows, int hidden, float eps, hipStream_t s);
 hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_counts,

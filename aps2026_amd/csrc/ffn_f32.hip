@@ -163,7 +163,75 @@ k_ffn_down_f32(const float* __restrict__ act, const uint32_t* __restrict__ offse
     }
 }
 
+// y[m][n] = (fp32 FMA chain over k ascending of x[m][k] w[n][k]) + bias[n]:
+// the decoder's Linear layers (the attention projections).  Reference:
+// Linear::forward (src/layer.cu:30-42) -> matmul_transposed_bias_gpu
+// (src/tensor.cu:3120-3143) -> k_matmul_transposed_8x8 (src/tensor.cu:
+// 715-800): one accumulator per output walked over k ascending, the bias
+// added once in the epilogue (nothing added without a bias).  64 x 64
+// outputs per block, 4 x 4 per thread, as the expert kernels above.
+__global__ void __launch_bounds__(256)
+k_linear_f32(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
+             float* __restrict__ y, int64_t M, int K, int N) {
+    __shared__ __align__(16) float As[kBK][kF32BM];
+    __shared__ __align__(16) float Bs[kBK][kF32BN];
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kF32BM;
+    const int n0 = blockIdx.x * kF32BN;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int sr = tid >> 2, sk = (tid & 3) * 4;
+    const bool a_ok = m0 + sr < M;
+    const float* a_src = x + (a_ok ? m0 + sr : 0) * static_cast<int64_t>(K) + sk;
+    const bool b_ok = n0 + sr < N;
+    const float* b_src = w + static_cast<int64_t>(b_ok ? n0 + sr : 0) * K + sk;
+    float acc[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[r][c] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += kBK) {
+        const float4 av = a_ok ? *reinterpret_cast<const float4*>(a_src + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 bv = b_ok ? *reinterpret_cast<const float4*>(b_src + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        __syncthreads();
+        As[sk + 0][sr] = av.x; As[sk + 1][sr] = av.y; As[sk + 2][sr] = av.z; As[sk + 3][sr] = av.w;
+        Bs[sk + 0][sr] = bv.x; Bs[sk + 1][sr] = bv.y; Bs[sk + 2][sr] = bv.z; Bs[sk + 3][sr] = bv.w;
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kBK; ++kk) {
+            const float4 a = *reinterpret_cast<const float4*>(&As[kk][ty * 4]);
+            const float4 b = *reinterpret_cast<const float4*>(&Bs[kk][tx * 4]);
+            const float ar[4] = {a.x, a.y, a.z, a.w};
+            const float br[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[r][c] = __builtin_fmaf(ar[r], br[c], acc[r][c]);
+        }
+    }
+    const int col = n0 + tx * 4;  // N % 4 == 0: a column group is all in or all out
+    float4 bb = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (bias && col < N) bb = *reinterpret_cast<const float4*>(bias + col);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t row = m0 + ty * 4 + r;
+        if (row >= M || col >= N) continue;
+        float4 o = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+        if (bias) o = make_float4(__fadd_rn(o.x, bb.x), __fadd_rn(o.y, bb.y), __fadd_rn(o.z, bb.z), __fadd_rn(o.w, bb.w));
+        *reinterpret_cast<float4*>(y + row * N + col) = o;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_linear_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows, int in_f,
+                             int out_f, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (in_f % kBK != 0 || out_f % 4 != 0 || out_f <= 0) return hipErrorInvalidValue;
+    const int64_t ty = ceil_div(rows, kF32BM);
+    if (ty > 65535) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(ceil_div(out_f, kF32BN)), static_cast<unsigned>(ty));
+    hipLaunchKernelGGL(k_linear_f32, grid, dim3(256), 0, s, x, w, bias, y, rows, in_f, out_f);
+    return hipGetLastError();
+}
 
 hipError_t launch_ffn_up_f32(const float* x, const uint32_t* offsets,
                              const uint32_t* assignment_rows, const float* w1,

@@ -297,6 +297,16 @@ APS_API int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int
 
 /* ---- attention over the prefix trie (scope row f4) --------------------- */
 
+/* Replaces Linear::forward's GPU path (reference src/layer.cu:30-42 ->
+ * matmul_transposed_bias_gpu / matmul_transposed_gpu, src/tensor.cu:
+ * 3034-3143, kernel k_matmul_transposed_8x8 :715-800): y [rows][out] =
+ * x [rows][in] . weight [out][in]^T, each output one fp32 FMA chain over k
+ * ascending, then + bias[out] when bias is not NULL (the decoder's q/k/v/o
+ * projections).  in % 16 == 0, out % 4 == 0, arrays 16-byte aligned, y not
+ * aliasing x. */
+APS_API int aps_linear(const float* x, const float* weight, const float* bias, int64_t rows, int32_t in_features,
+                       int32_t out_features, float* y, void* stream);
+
 /* The RoPE tables of the reference's rope_table (src/tensor.cu:2703-2735),
  * host code: cos/sin [max_seq][head_dim / 2] with inv = powf(theta,
  * (-2 j) / head_dim), cos = cosf(p * inv), sin = sinf(p * inv). */

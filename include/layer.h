@@ -17,6 +17,23 @@
 #include "model_loader.h"
 #include "tensor.h"
 
+// A dense layer y = x W^T (+ b) (reference include/layer.h:11-21,
+// src/layer.cu:21-42).  The GPU path is one fp32 FMA chain per output over k
+// ascending with the bias added once, the reference GPU kernel's arithmetic.
+class Linear {
+public:
+    Linear() = default;
+    Linear(Tensor weight, Tensor bias = Tensor());
+    Linear(const ModelLoader& loader, const std::string& weight, const std::string& bias = "");
+    void forward(const Tensor& x, Tensor& y, bool use_gpu = false) const;
+    const Tensor& weight() const { return weight_; }
+    const Tensor& bias() const { return bias_; }
+
+private:
+    Tensor weight_;
+    Tensor bias_;
+};
+
 class PhiMLP {
 public:
     // w1, w3: [F][H]; w2: [H][F] (nn.Linear layout).
@@ -52,4 +69,30 @@ private:
     Tensor gate_;
     std::vector<PhiMLP> experts_;
     std::size_t gpu_weights_handle_ = 0;
+};
+
+// The prefix trie's device arrays for attention on trie-node rows
+// (reference include/layer.h:57-63).
+struct PrefixExpansion {
+    const tensor_ops::RowIndexBuffer* node_pos = nullptr;  // node row -> depth
+    const tensor_ops::RowIndexBuffer* node_anc = nullptr;  // node row -> chain
+    std::size_t anc_stride = 0;
+    std::size_t max_seq = 0;
+    bool active() const { return node_anc != nullptr; }
+};
+
+// Self-attention of the decoder layer (reference include/layer.h:65-75,
+// src/layer.cu:150-188): q/k/v/o projections with bias, RoPE and GQA
+// attention.  This build provides the prefix-trie path (expansion.active():
+// RoPE at node depths, attention over ancestor chains, as the reference's
+// prefill); without an expansion forward throws std::invalid_argument.
+class PhiAttention {
+public:
+    PhiAttention(const ModelLoader& loader, std::size_t layer_idx);
+    PhiAttention(Linear q_proj, Linear k_proj, Linear v_proj, Linear o_proj);
+    void forward(const Tensor& x, Tensor& y, const std::vector<std::size_t>& seq_lens, bool use_gpu = false,
+                 const PrefixExpansion& expansion = {}) const;
+
+private:
+    Linear q_proj_, k_proj_, v_proj_, o_proj_;
 };

@@ -75,14 +75,21 @@ private:
 
 namespace tensor_ops {
 
-// c[m][n] = a[m][k] . b[n][k]^T on the GPU.  This build provides the narrow
-// shape the MoE router uses (n <= 64, k a multiple of 256), computed as one
-// fp32 FMA chain per output, k ascending (the reference's
-// k_matmul_transposed_narrow, src/tensor.cu:2943-3006).  Mismatched shapes
-// throw std::invalid_argument("matmul_transposed_gpu shape") as the
-// reference does; other valid shapes throw std::invalid_argument naming the
+// c[m][n] = a[m][k] . b[n][k]^T on the GPU, one fp32 FMA chain per output,
+// k ascending (the reference's k_matmul_transposed_narrow for the router
+// shape, src/tensor.cu:2943-3006, and k_matmul_transposed_8x8 for the
+// others, :715-800).  The router shape (n <= 64, k % 256 == 0) runs the
+// router kernel; other shapes need k % 16 == 0 and n % 4 == 0.  Mismatched
+// shapes throw std::invalid_argument("matmul_transposed_gpu shape") as the
+// reference does; unsupported ones throw std::invalid_argument naming the
 // limit.
 void matmul_transposed_gpu(const Tensor& a, const Tensor& b, Tensor& c);
+
+// c = a . b^T + bias (reference include/tensor.h, src/tensor.cu:3120-3143):
+// one fp32 FMA chain per output over k ascending, then the bias.  Throws
+// std::invalid_argument("matmul_transposed_bias_gpu shape") as the reference
+// does; this build needs k % 16 == 0 and n % 4 == 0.
+void matmul_transposed_bias_gpu(const Tensor& a, const Tensor& b, const Tensor& bias, Tensor& c);
 
 // Registers the 16 experts' w1 / w2 / w3 (nn.Linear layout: w1, w3 [F][H],
 // w2 [H][F]) and returns a 1-based handle.  Throws

@@ -58,6 +58,7 @@ def lib():
         L.oracle_layer_norm.argtypes = [_f32p, ctypes.c_void_p, _i64, _i32, _f32p, _f32p, ctypes.c_float,
                                         ctypes.c_void_p, _f32p, ctypes.c_void_p, ctypes.c_void_p]
         L.oracle_default_quantum.restype = ctypes.c_float
+        L.oracle_linear.argtypes = [_f32p, _f32p, ctypes.c_void_p, _i64, _i32, _i32, _f32p]
         L.oracle_rope_table.argtypes = [_i64, _i32, ctypes.c_float, _f32p, _f32p]
         L.oracle_rope_tree.argtypes = [_f32p, _u32p, _i64, _i32, _i32, _f32p, _f32p]
         L.oracle_attention_tree.argtypes = [_f32p, _f32p, _f32p, _f32p, _u32p, _u32p, _i64, _i64, _i32, _i32,
@@ -342,6 +343,20 @@ def model_bin_index(data: bytes):
 
 SLIDING_WINDOW = 2047   # reference include/config.h:17
 ROPE_THETA = 10000.0    # reference include/config.h:18
+
+
+def linear(x: np.ndarray, w: np.ndarray, bias: Optional[np.ndarray] = None) -> np.ndarray:
+    """y = x w^T (+ bias): one fp32 FMA chain over k ascending per output,
+    the bias added once (reference k_matmul_transposed_8x8 and its epilogue,
+    src/tensor.cu:715-800)."""
+    x = _c(x, np.float32); w = _c(w, np.float32)
+    T, K = x.shape
+    N = w.shape[0]
+    y = np.empty((T, N), np.float32)
+    b = _c(bias, np.float32) if bias is not None else None
+    _check(lib().oracle_linear(x, w, b.ctypes.data_as(ctypes.c_void_p) if b is not None else None, T, K, N, y),
+           "linear")
+    return y
 
 
 def rope_table(max_seq: int, head_dim: int, theta: float = ROPE_THETA):

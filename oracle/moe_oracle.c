@@ -579,3 +579,41 @@ ORACLE_API void oracle_attention_tree(const float* q, const float* k, const floa
         free(e);
     }
 }
+
+/* Linear layer, GPU-path semantics: src/layer.cu:30-42 (Linear::forward) ->
+ * src/tensor.cu:3120-3143 (matmul_transposed_bias_gpu) -> k_matmul_transposed_8x8
+ * (src/tensor.cu:715-800): y[t][n] = (fp32 FMA chain over k ascending of
+ * x[t][k] * w[n][k], +0 init) + bias[n] (one rounded add; none without a
+ * bias).  The same chain as oracle_router_logits for any output count. */
+ORACLE_API int oracle_linear(const float* x, const float* w, const float* bias, int64_t T, int32_t K, int32_t N,
+                             float* y) {
+    if (T < 0 || K <= 0 || N <= 0) return -1;
+    float* wt = (float*)malloc((size_t)K * (size_t)N * sizeof(float));
+    if (!wt) return -2;
+    for (int32_t n = 0; n < N; ++n)
+        for (int32_t k = 0; k < K; ++k) wt[(size_t)k * N + n] = w[(size_t)n * K + k];
+    int rc = 0;
+#pragma omp parallel
+    {
+        float* acc = (float*)malloc((size_t)N * sizeof(float));
+        if (!acc) {
+#pragma omp atomic write
+            rc = -2;
+        } else {
+#pragma omp for schedule(static)
+            for (int64_t t = 0; t < T; ++t) {
+                for (int32_t n = 0; n < N; ++n) acc[n] = 0.0f;
+                const float* xr = x + (size_t)t * K;
+                for (int32_t k = 0; k < K; ++k) {
+                    const float xv = xr[k];
+                    const float* g = wt + (size_t)k * N;
+                    for (int32_t n = 0; n < N; ++n) acc[n] = fmaf(xv, g[n], acc[n]);
+                }
+                for (int32_t n = 0; n < N; ++n) y[(size_t)t * N + n] = bias ? acc[n] + bias[n] : acc[n];
+            }
+            free(acc);
+        }
+    }
+    free(wt);
+    return rc;
+}

@@ -109,6 +109,27 @@ int loader_check(const std::string& dir, const std::string& model) {
     mlp.forward(x, ymlp, true);
     write_raw(dir, "loader_y", y);
     write_raw(dir, "loader_mlp_y", ymlp);
+    // PhiAttention's trie path on the 64 nodes of a two-prompt batch (the
+    // file's x rows are the node rows)
+    {
+        std::vector<int> p1(40), p2(44);
+        for (int i = 0; i < 40; ++i) p1[i] = i + 1;
+        for (int i = 0; i < 44; ++i) p2[i] = i < 20 ? i + 1 : i + 30;
+        const PrefixTrie trie = build_prefix_trie({p1, p2});
+        expect(trie.nodes() == x.size(0), "attention batch has one node per x row");
+        const tensor_ops::RowIndexBuffer pos(trie.node_depth), anc(trie.node_anc);
+        PrefixExpansion ex;
+        ex.node_pos = &pos;
+        ex.node_anc = &anc;
+        ex.anc_stride = trie.max_len;
+        ex.max_seq = trie.max_len;
+        const PhiAttention attn(loader, 0);
+        Tensor ya;
+        attn.forward(x, ya, trie.seq_lens, true, ex);
+        write_raw(dir, "loader_attn", ya);
+        expect_throw<std::invalid_argument>([&] { attn.forward(x, ya, trie.seq_lens, true); }, nullptr,
+                                            "attention without an expansion");
+    }
     expect_throw<std::runtime_error>([&] { (void)loader.load("nope"); }, "missing tensor: nope", "missing tensor");
     const std::string nofile = dir + "/absent.bin";
     expect_throw<std::runtime_error>([&] { ModelLoader l(nofile); }, ("cannot open model: " + nofile).c_str(),

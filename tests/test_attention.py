@@ -121,3 +121,22 @@ def test_attention_tree_equals_token_rows():
             tanc[off + si, :si + 1] = np.arange(off, off + si + 1)
     tok_out = oracle.attention_tree(q[tn], k[tn], v[tn], tpos, tanc, plan.max_len, 4, 1, 128)
     assert np.array_equal(tok_out.view(np.uint32), node_out[tn].view(np.uint32))
+
+
+def test_linear_pins():
+    """oracle.linear: equals the router-logits chain for narrow outputs (the
+    same FMA chain), its bias is one exact fp32 add, and it is within the
+    fp64 error bound of the product."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((5, 512)).astype(np.float32)
+    w = rng.standard_normal((40, 512)).astype(np.float32)
+    b = rng.standard_normal(40).astype(np.float32)
+    y0 = oracle.linear(x, w)
+    assert np.array_equal(y0.view(np.uint32), oracle.router_logits(x, w).view(np.uint32))
+    assert np.array_equal(oracle.linear(x, w, b), (y0 + b).astype(np.float32))
+    ref = x.astype(np.float64) @ w.T.astype(np.float64)
+    bound = 512 * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(w).T.astype(np.float64))
+    assert (np.abs(y0 - ref) <= bound).all()
+    wide = rng.standard_normal((300, 512)).astype(np.float32)
+    yw = oracle.linear(x, wide)
+    assert np.array_equal(yw[:, :40].view(np.uint32), oracle.linear(x, wide[:40]).view(np.uint32))

@@ -107,3 +107,19 @@ def test_attention_errors(gpu_device):
     with pytest.raises(ValueError, match="ancestor index"):
         attention.attention_tree_gpu(q, kv, kv, q.clone(), [0, 1], np.array([[0, 0], [0, 7]]), 2, q_heads=4,
                                      kv_heads=1)
+
+
+@pytest.mark.parametrize("rows,k,n,bias", [(10240 // 40, 4096, 2048, True), (300, 4096, 512, True),
+                                           (77, 2048, 4096, True), (64, 256, 12, False), (1, 16, 4, True)])
+def test_linear_bit_exact(gpu_device, rows, k, n, bias):
+    """aps_linear (the q/k/v/o projections) against the oracle's linear
+    (one FMA chain per output, k ascending, then the bias), bit for bit."""
+    note(f"linear rows={rows} k={k} n={n} bias={bias}")
+    rng = np.random.default_rng(rows + k + n)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    w = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32) if bias else None
+    got = attention.linear_gpu(dev(x, gpu_device), dev(w, gpu_device), dev(b, gpu_device) if bias else None)
+    torch.cuda.synchronize()
+    want = oracle.linear(x, w, b)
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
