@@ -6,9 +6,11 @@
 add_layer_norm (attention output += residual stream, LayerNorm with the
 reference kernel's serial sums) feeding the same MoE block, fp32 activations
 with bf16 experts (synthetic attention output; the attention itself is not
-built).  `--config c4` does the same on C4's 16 prompts x 1024 ids after
-the prompt prefix trie (host code) folds them into 10,240 rows, with the
-embedding gather of those rows in each step; its value counts prompt tokens.
+built).  `--config c4` runs C4's 16 prompts x 1024 ids, folded by the prompt prefix
+trie (host code) into 10,240 rows, through the embedding gather and the
+whole first decoder layer (input LayerNorm, fp32 q/k/v projections, RoPE,
+tree attention, o projection, add_layer_norm, MoE block) per step; its value
+counts prompt tokens.
 `--config load` times reading one MoE layer from a model.bin into HBM.
 
 One step = one full MoE block (router GEMM, quantised top-2, dispatch,
@@ -211,13 +213,19 @@ def main():
             gd = torch.Generator(device=dev).manual_seed(4)
             emb = torch.randn((prefix.VOCAB_SIZE, H), generator=gd, device=dev)
             node_rows = prefix.RowIndexBuffer(plan.node_token, dev)
-            # attention inputs (the q/k/v projections are not built: synthetic
-            # q, k, v of the reference's 16 query / 4 KV heads of 128)
+            # the attention half of the first decoder layer: input LayerNorm,
+            # q/k/v projections (16 query / 4 KV heads of 128, with bias),
+            # RoPE, tree attention, o projection; random-init weights
             from aps2026_amd import attention
-            qa = (0.5 * torch.randn((T, 16 * 128), generator=gd, device=dev)).contiguous()
-            ka = (0.5 * torch.randn((T, 4 * 128), generator=gd, device=dev)).contiguous()
-            va = torch.randn((T, 4 * 128), generator=gd, device=dev)
+            normed = torch.empty((T, H), dtype=torch.float32, device=dev)
+            qa = torch.empty((T, 16 * 128), dtype=torch.float32, device=dev)
+            ka = torch.empty((T, 4 * 128), dtype=torch.float32, device=dev)
+            va = torch.empty((T, 4 * 128), dtype=torch.float32, device=dev)
             oa = torch.empty((T, 16 * 128), dtype=torch.float32, device=dev)
+            proj = {nm: ((0.02 * torch.randn((o, i), generator=gd, device=dev)).contiguous(),
+                         (0.02 * torch.randn(o, generator=gd, device=dev)).contiguous())
+                    for nm, (o, i) in (("q", (2048, H)), ("k", (512, H)), ("v", (512, H)), ("o", (H, 2048)))}
+            proj_flops = 2.0 * T * H * (2048 + 512 + 512) + 2.0 * T * 2048 * H
             pos_d = attention._rows_u32(plan.node_depth, dev)
             anc_d = attention._rows_u32(plan.node_anc, dev)
             cos_d, sin_d = attention._device_table(dev, plan.max_len, 128, attention.ROPE_THETA)
@@ -276,6 +284,21 @@ def main():
     if c4:
         args_gather = (ctypes.c_void_p(emb.data_ptr()), emb.shape[0], H, ctypes.c_void_p(node_rows.data.data_ptr()),
                        T, ctypes.c_void_p(resid.data_ptr()), sptr)
+        def lin(src, nm, dst, k_in, n_out):
+            return (ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(proj[nm][0].data_ptr()),
+                    ctypes.c_void_p(proj[nm][1].data_ptr()), T, k_in, n_out, ctypes.c_void_p(dst.data_ptr()), sptr)
+        args_lnin = (ctypes.c_void_p(resid.data_ptr()), ctypes.c_void_p(ln_w.data_ptr()),
+                     ctypes.c_void_p(ln_b.data_ptr()), T, H, ctypes.c_float(moe.NORM_EPS),
+                     ctypes.c_void_p(normed.data_ptr()), sptr)
+        args_qkv = (lin(normed, "q", qa, H, 2048), lin(normed, "k", ka, H, 512), lin(normed, "v", va, H, 512))
+        args_o = lin(oa, "o", attn, 2048, H)
+
+        def qkv():
+            for a in args_qkv:
+                rc = L.aps_linear(*a)
+                if rc:
+                    return rc
+            return 0
         args_rope = (ctypes.c_void_p(qa.data_ptr()), ctypes.c_void_p(ka.data_ptr()), ctypes.c_void_p(pos_d.data_ptr()),
                      T, 16, 4, 128, ctypes.c_void_p(cos_d.data_ptr()), ctypes.c_void_p(sin_d.data_ptr()),
                      cos_d.shape[0], sptr)
@@ -285,9 +308,10 @@ def main():
 
     def step(i):
         if c4:
-            for fn, a in ((L.aps_gather_rows, args_gather), (L.aps_rope_tree, args_rope),
-                          (L.aps_attention_tree, args_attn)):
-                rc = fn(*a)
+            for fn in (lambda: L.aps_gather_rows(*args_gather), lambda: L.aps_layer_norm(*args_lnin), qkv,
+                       lambda: L.aps_rope_tree(*args_rope), lambda: L.aps_attention_tree(*args_attn),
+                       lambda: L.aps_linear(*args_o)):
+                rc = fn()
                 if rc:
                     raise RuntimeError(capi.last_error())
         if c3:
@@ -341,7 +365,8 @@ def main():
     else:
         stages = ["router_logits", "route_top2", "dispatch", "ffn_up", "ffn_down", "combine"]
     if c3:
-        stages = (["gather_rows", "rope", "attention_tree"] if c4 else []) + ["add_layer_norm"] + stages
+        stages = (["gather_rows", "input_layer_norm", "qkv_proj", "rope", "attention_tree", "o_proj"] if c4 else []) + \
+            ["add_layer_norm"] + stages
         L.aps_add_layer_norm(*args_ln)
         xb = x.to(torch.bfloat16)  # the FFN's bf16 copy of the norm output (the fused path makes its own)
     times = {s: [] for s in stages}
@@ -350,8 +375,9 @@ def main():
         w = layers[i % LAYERS]
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
         ev[0].record(stream)
-        calls = ([lambda: L.aps_gather_rows(*args_gather), lambda: L.aps_rope_tree(*args_rope),
-                  lambda: L.aps_attention_tree(*args_attn)] if c4 else [])
+        calls = ([lambda: L.aps_gather_rows(*args_gather), lambda: L.aps_layer_norm(*args_lnin), qkv,
+                  lambda: L.aps_rope_tree(*args_rope), lambda: L.aps_attention_tree(*args_attn),
+                  lambda: L.aps_linear(*args_o)] if c4 else [])
         calls += [lambda: L.aps_add_layer_norm(*args_ln)] if c3 else []
         calls += [
             lambda: L.aps_router_logits(p(x), xd, p(gate), T, H, E, p(logits), sptr),
@@ -418,6 +444,12 @@ def main():
         # gather: node rows read from the embedding table and written, plus the indices
         stage_report["gather_rows"] = {"us": mean_t["gather_rows"] * 1e6,
                                        "GB_s": (2.0 * T * H * 4 + T * 4) / mean_t["gather_rows"] / 1e9}
+        stage_report["input_layer_norm"] = {"us": mean_t["input_layer_norm"] * 1e6,
+                                            "GB_s": 2.0 * T * H * 4 / mean_t["input_layer_norm"] / 1e9}
+        qkv_flops = 2.0 * T * H * (2048 + 512 + 512)
+        stage_report["qkv_proj"] = {"us": mean_t["qkv_proj"] * 1e6, "TFLOP_s": qkv_flops / mean_t["qkv_proj"] / 1e12}
+        stage_report["o_proj"] = {"us": mean_t["o_proj"] * 1e6,
+                                  "TFLOP_s": (proj_flops - qkv_flops) / mean_t["o_proj"] / 1e12}
         stage_report["rope"] = {"us": mean_t["rope"] * 1e6,
                                 "GB_s": 2.0 * T * 20 * 128 * 4 / mean_t["rope"] / 1e9}
         stage_report["attention_tree"] = {"us": mean_t["attention_tree"] * 1e6,
@@ -457,10 +489,10 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8" if fp8 else ("bf16" if bf16 else "f32"), "data": "synthetic (seeded PCG64 normals, random-init weights)",
         "config": {"workload": (f"c4: 16 prompts x 1024 ids (groups of 4 share a 512-id prefix) deduplicated to "
-                                f"{T} prefix-trie rows; per step the embedding gather of those rows, RoPE and GQA "
-                                f"tree attention (16/4 heads of 128, synthetic q/k/v: the projections are not "
-                                f"built), then the decoder post-attention half (add_layer_norm fp32 + MoE FFN "
-                                f"block, hidden {H}, "
+                                f"{T} prefix-trie rows; per step the embedding gather of those rows and the "
+                                f"first decoder layer on them: input LayerNorm, q/k/v projections (fp32, 16/4 "
+                                f"heads of 128), RoPE, GQA tree attention, o projection, add_layer_norm and the "
+                                f"MoE FFN block (hidden {H}, "
                                 f"{E} experts top-2, ffn {F}, bf16 experts) on them; value counts the "
                                 f"{prompt_tokens} prompt tokens; the trie itself is host code, timed in stages"
                                 if c4 else
