@@ -194,8 +194,16 @@ hipError_t launch_attention_tree(const float* q, const float* k, const float* v,
     if (rows <= 0) return hipSuccess;
     if (head_dim != kHeadDim || q_heads != kGroup * kv_heads || anc_stride <= 0 || window_max <= 0)
         return hipErrorInvalidValue;
-    const int wmax = static_cast<int>(anc_stride < window_max ? anc_stride : window_max);
+    const int64_t keys = anc_stride < window_max ? anc_stride : window_max;
+    if (keys > kAttnMaxWindow) return hipErrorInvalidValue;
+    const int wmax = static_cast<int>(keys);
     const size_t lds = static_cast<size_t>(wmax) * (kGroup * sizeof(float) + sizeof(uint32_t));
+    // dynamic LDS past 64 KB needs the function's limit raised first
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention_tree),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+    }
     // 1 / sqrtf(head_dim), both correctly rounded, as the reference kernel computes it
     const float root = sqrtf(static_cast<float>(head_dim));
     const float scale = 1.0f / root;

@@ -619,6 +619,9 @@ int aps_attention_tree(const float* q, const float* k, const float* v, float* ou
     if (rows < 0 || head_dim != 128 || anc_stride <= 0 || window <= 0)
         return fail(APS_ERR_SHAPE, "attention tree shape: rows %lld head_dim %d (128 only) anc_stride %lld window %d",
                     (long long)rows, head_dim, (long long)anc_stride, window);
+    if ((anc_stride < window ? anc_stride : window) > aps::kAttnMaxWindow)
+        return fail(APS_ERR_SHAPE, "attention tree: a window of %lld keys exceeds the %d that fit in LDS",
+                    (long long)(anc_stride < window ? anc_stride : window), aps::kAttnMaxWindow);
     if (rows == 0) return APS_OK;
     if (!q || !k || !v || !out || !row_pos || !anc) return fail(APS_ERR_ARG, "attention tree: NULL pointer");
     if ((reinterpret_cast<uintptr_t>(k) & 15u) != 0) return fail(APS_ERR_ARG, "attention tree: k must be 16-byte aligned");

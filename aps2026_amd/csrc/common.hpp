@@ -143,6 +143,10 @@ hipError_t launch_rope_tree(float* x, const uint32_t* row_pos, int64_t rows, int
                             const float* cosv, const float* sinv, int64_t max_seq, hipStream_t s);
 
 // GQA-4 tree attention, head_dim 128 (the reference kernel's arithmetic).
+// A workgroup keeps 20 bytes of LDS per key of its window (four scores and
+// the key's row index) next to 2 KB of its own: windows up to kAttnMaxWindow
+// keys fit gfx950's 160 KB of LDS per workgroup.
+constexpr int kAttnMaxWindow = 7936;
 hipError_t launch_attention_tree(const float* q, const float* k, const float* v, float* out, const uint32_t* row_pos,
                                  const uint32_t* anc, int64_t anc_stride, int64_t rows, int q_heads, int kv_heads,
                                  int head_dim, int window_max, hipStream_t s);

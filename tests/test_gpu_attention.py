@@ -75,6 +75,29 @@ def test_attention_long_sequence_sliding_window(gpu_device):
     np.testing.assert_array_equal(out.cpu().numpy()[rows].view(np.uint32), want.view(np.uint32))
 
 
+def test_attention_window_past_64k_of_lds(gpu_device):
+    """A 3,500-key window (70 KB of the workgroup's dynamic LDS, past the
+    64 KB default) on a 3,500-token prompt: the last rows equal the oracle;
+    a window past the LDS budget (7,936 keys) is a shape error."""
+    note("attention tree 3500-key window")
+    batch = [list(np.random.default_rng(8).integers(0, 32064, 3500))]
+    plan, q, k, v = trie_inputs(batch, q_heads=4, kv_heads=1, seed=8)
+    rows = np.arange(plan.nodes - 16, plan.nodes)
+    out = torch.empty((plan.nodes, 4 * 128), dtype=torch.float32, device=gpu_device)
+    attention.attention_tree_gpu(dev(q, gpu_device), dev(k, gpu_device), dev(v, gpu_device), out,
+                                 plan.node_depth, plan.node_anc, plan.max_len, q_heads=4, kv_heads=1, window=4096)
+    torch.cuda.synchronize()
+    want = oracle.attention_tree(q[rows], k, v, plan.node_depth[rows], plan.node_anc[rows], plan.max_len, 4, 1, 128,
+                                 4096)
+    np.testing.assert_array_equal(out.cpu().numpy()[rows].view(np.uint32), want.view(np.uint32))
+    note("attention tree window past the LDS budget")
+    q1 = torch.zeros((1, 4 * 128), dtype=torch.float32, device=gpu_device)
+    kv1 = torch.zeros((1, 128), dtype=torch.float32, device=gpu_device)
+    with pytest.raises(ValueError, match="exceeds"):
+        attention.attention_tree_gpu(q1, kv1, kv1, q1.clone(), [0], np.zeros((1, 8000), np.uint32), 8000,
+                                     q_heads=4, kv_heads=1, window=8000)
+
+
 def test_attention_nodes_equal_token_rows(gpu_device):
     note("attention tree nodes vs token rows")
     batch = shared_batch(4, groups=2, per=4, pre=60, suf=20)
