@@ -200,7 +200,7 @@ int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const 
         x = xb;
     }
     if (logits) APS_HIP(aps::launch_route_top2(logits, rows, w.E, routes, tiles, s), "route_top2 launch");
-    APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, w.E, counts, offsets, arows, rpos, s),
+    APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, w.E, counts, offsets, arows, rpos, nullptr, s),
             "dispatch launch");
     if (w.compute == APS_DTYPE_E4M3) {
         auto* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
@@ -340,8 +340,9 @@ int aps_moe_workspace_layout(uint64_t handle, int64_t rows, aps_moe_ws_layout* o
 }
 
 size_t aps_moe_dispatch_workspace_size(int64_t rows, int32_t num_experts) {
-    if (rows <= 0 || num_experts <= 0) return 0;
-    return static_cast<size_t>(aps::ceil_div(rows, aps::kTileTokens)) * num_experts * 4;
+    if (rows < 0 || num_experts <= 0) return 0;
+    // tile histogram, then the clamped-id counter
+    return static_cast<size_t>(aps::ceil_div(rows, aps::kTileTokens)) * num_experts * 4 + 4;
 }
 
 int aps_router_logits(const void* x, int32_t x_dtype, const float* gate, int64_t rows,
@@ -382,9 +383,10 @@ int aps_moe_dispatch(const uint8_t* routes, int64_t rows, int32_t num_experts, u
         return fail(APS_ERR_WORKSPACE, "dispatch: scratch %zu bytes, need %zu", scratch_bytes, need);
     hipStream_t s = static_cast<hipStream_t>(stream);
     auto* tiles = static_cast<uint32_t*>(scratch);
-    APS_HIP(aps::launch_tile_hist(routes, rows, num_experts, tiles, s), "tile_hist launch");
+    auto* status = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + need - 4);
+    APS_HIP(aps::launch_tile_hist(routes, rows, num_experts, tiles, status, s), "tile_hist launch");
     APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, num_experts, counts, offsets,
-                                         assignment_rows, route_positions, s),
+                                         assignment_rows, route_positions, status, s),
             "dispatch launch");
     return APS_OK;
 }

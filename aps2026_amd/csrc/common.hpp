@@ -67,6 +67,20 @@ __device__ inline uint32_t tile_quarter_counts(int first, int second, int e) {
 }
 __host__ __device__ inline uint32_t tile_word_total(uint32_t w) { return (w * 0x01010101u) >> 24; }
 
+// Caller-supplied routes (aps_moe_dispatch) are made memory-safe before they
+// are counted or ranked: an expert id >= E is clamped to E - 1 (and reported
+// by the caller-visible counter), a token whose two slots name the same
+// expert keeps both -- it takes two consecutive positions of that expert,
+// slot 0 first, as a stable sort of the (token, slot) pairs gives.  Routes
+// the router writes are always two distinct ids < E, which this leaves
+// unchanged.  Returns the number of clamped ids (0..2).
+__device__ inline int clamp_routes(int& r0, int& r1, int E) {
+    int bad = 0;
+    if (r0 >= E) { r0 = E - 1; ++bad; }
+    if (r1 >= E) { r1 = E - 1; ++bad; }
+    return bad;
+}
+
 // Upper bound on sum_e ceil(count_e / bm) over E experts with sum count_e = n.
 __host__ __device__ inline int64_t max_row_tiles(int64_t n, int64_t bm, int64_t E) {
     return ceil_div(n, bm) + E;
@@ -122,8 +136,10 @@ hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t 
                          bf16_t* x_copy, hipStream_t s);
 hipError_t launch_route_top2(const float* logits, int64_t rows, int experts, uint8_t* routes,
                              uint32_t* tile_counts, hipStream_t s);
+// status (may be null): one u32 that counts the route ids >= experts the
+// dispatch clamped (zeroed by launch_tile_hist, added to by the scatter).
 hipError_t launch_tile_hist(const uint8_t* routes, int64_t rows, int experts,
-                            uint32_t* tile_counts, hipStream_t s);
+                            uint32_t* tile_counts, uint32_t* status, hipStream_t s);
 // Decoder-layer LayerNorm (residual == nullptr: plain; else x += residual
 // in place first).  hidden % 256 == 0.
 // Row gather out[i] = x[rows[i]] (fp32); rows past x_rows give zero rows.
@@ -161,7 +177,7 @@ hipError_t launch_layer_norm(float* x, const float* residual, const float* weigh
 hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_counts,
                                    int64_t rows, int experts, uint32_t* counts,
                                    uint32_t* offsets, uint32_t* assignment_rows,
-                                   uint32_t* route_positions, hipStream_t s);
+                                   uint32_t* route_positions, uint32_t* status, hipStream_t s);
 
 // bf16 MFMA path.  w13 / w2 are packed tile images (see launch_pack_*):
 // w13 [E][F/64][H/64][128][64], w2 [E][H/128][F/64][128][64]; act/y bf16.

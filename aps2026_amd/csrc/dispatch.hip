@@ -28,17 +28,21 @@ __global__ void k_zero_u32(uint32_t* __restrict__ p, int n) {
     if (i < n) p[i] = 0u;
 }
 
+// status (may be null): zeroed here, before k_dispatch_scatter counts the
+// clamped route ids into it.
 __global__ void __launch_bounds__(256)
 k_tile_hist(const uint8_t* __restrict__ routes, int64_t rows, int E,
-            uint32_t* __restrict__ tile_counts) {
+            uint32_t* __restrict__ tile_counts, uint32_t* __restrict__ status) {
     const int lane = threadIdx.x & 63;
     const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     const int64_t tile = t >> 6;
     const int64_t ntiles = (rows + kWave - 1) / kWave;
+    if (status && t == 0) *status = 0u;
     int first = 255, second = 255;
     if (t < rows) {
         first = routes[2 * t];
         second = routes[2 * t + 1];
+        clamp_routes(first, second, E);
     }
     uint32_t mine = 0;
     for (int e = 0; e < E; ++e) {
@@ -52,7 +56,7 @@ __global__ void __launch_bounds__(256)
 k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restrict__ tile_counts,
                    int64_t rows, int E, uint32_t* __restrict__ counts,
                    uint32_t* __restrict__ offsets, uint32_t* __restrict__ assignment_rows,
-                   uint32_t* __restrict__ route_positions) {
+                   uint32_t* __restrict__ route_positions, uint32_t* __restrict__ status) {
     const int lane = threadIdx.x & 63;
     const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     const int64_t ntiles = (rows + kWave - 1) / kWave;
@@ -138,18 +142,24 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
         if (lane == E - 1) offsets[E] = incl;
     }
 
-    // 3. stable rank of each lane's token inside this tile, per expert
-    const int first = t < rows ? r0 : 255;
-    const int second = t < rows ? r1 : 255;
+    // 3. stable rank of each lane's (token, slot) pairs inside this tile, per
+    //    expert: the pairs of lower lanes come first, slot 0 before slot 1
+    int first = 255, second = 255;
+    if (t < rows) {
+        first = r0;
+        second = r1;
+        const int bad = clamp_routes(first, second, E);
+        if (status && bad) atomicAdd(status, static_cast<uint32_t>(bad));
+    }
     const uint64_t below = (1ull << lane) - 1ull;
     uint32_t p0 = 0, p1 = 0;
     for (int e = 0; e < E; ++e) {
-        const uint64_t m = __ballot(first == e || second == e);
-        if (m == 0) continue;  // wave-uniform
+        const uint64_t m0 = __ballot(first == e), m1 = __ballot(second == e);
+        if ((m0 | m1) == 0) continue;  // wave-uniform
         const uint32_t b = __shfl(base, e);
-        const uint32_t r = static_cast<uint32_t>(__popcll(m & below));
+        const uint32_t r = static_cast<uint32_t>(__popcll(m0 & below) + __popcll(m1 & below));
         if (first == e) p0 = b + r;
-        if (second == e) p1 = b + r;
+        if (second == e) p1 = b + r + (first == e ? 1u : 0u);
     }
     if (t < rows) {
         assignment_rows[p0] = static_cast<uint32_t>(t);
@@ -180,17 +190,20 @@ hipError_t launch_dense_plan(uint32_t* offsets, uint32_t* assignment_rows, int64
 }
 
 hipError_t launch_tile_hist(const uint8_t* routes, int64_t rows, int experts,
-                            uint32_t* tile_counts, hipStream_t s) {
-    if (rows <= 0) return hipSuccess;
+                            uint32_t* tile_counts, uint32_t* status, hipStream_t s) {
+    if (rows <= 0) {
+        if (status) hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, s, status, 1);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_tile_hist, dim3(static_cast<unsigned>(ceil_div(rows, 256))), dim3(256),
-                       0, s, routes, rows, experts, tile_counts);
+                       0, s, routes, rows, experts, tile_counts, status);
     return hipGetLastError();
 }
 
 hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_counts,
                                    int64_t rows, int experts, uint32_t* counts,
                                    uint32_t* offsets, uint32_t* assignment_rows,
-                                   uint32_t* route_positions, hipStream_t s) {
+                                   uint32_t* route_positions, uint32_t* status, hipStream_t s) {
     if (experts <= 0 || experts > kMaxExperts) return hipErrorInvalidValue;
     if (rows <= 0) {
         // empty batch: counts and offsets are all zero
@@ -201,7 +214,7 @@ hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_c
     const int64_t ntiles = ceil_div(rows, kWave);
     hipLaunchKernelGGL(k_dispatch_scatter, dim3(static_cast<unsigned>(ceil_div(ntiles, 4))),
                        dim3(256), 0, s, routes, tile_counts, rows, experts, counts, offsets,
-                       assignment_rows, route_positions);
+                       assignment_rows, route_positions, status);
     return hipGetLastError();
 }
 

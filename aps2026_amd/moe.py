@@ -275,9 +275,12 @@ def route_top2(logits: torch.Tensor) -> torch.Tensor:
     return routes
 
 
-def dispatch(routes: torch.Tensor, num_experts: int):
+def dispatch(routes: torch.Tensor, num_experts: int, check_ids: bool = True):
     """Stable counting-sort dispatch; returns (counts, offsets,
-    assignment_rows, route_positions) as int32 tensors (u32 values)."""
+    assignment_rows, route_positions) as int32 tensors (u32 values).
+    Route ids >= num_experts are clamped by the kernels (every index stays in
+    range) and counted; with check_ids (the default) the call waits for the
+    count and raises ValueError when it is not zero."""
     rows = routes.shape[0]
     dev = routes.device
     counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
@@ -288,6 +291,10 @@ def dispatch(routes: torch.Tensor, num_experts: int):
     scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     _call(capi.lib().aps_moe_dispatch(_ptr(routes), rows, num_experts, _ptr(counts), _ptr(offsets),
                                       _ptr(arows), _ptr(rpos), _ptr(scratch), nbytes, _stream(dev)))
+    if check_ids:
+        bad = int(scratch[nbytes - 4:nbytes].view(torch.int32).item())
+        if bad:
+            raise ValueError(f"dispatch: {bad} route ids >= num_experts ({num_experts})")
     return counts, offsets, arows, rpos
 
 

@@ -128,7 +128,9 @@ APS_API int aps_moe_weights_release(uint64_t handle);
  * per-call intermediate Tensors (src/tensor.cu:2835, 2867). */
 APS_API int aps_moe_workspace_layout(uint64_t handle, int64_t rows, aps_moe_ws_layout* out);
 
-/* Scratch for aps_moe_dispatch: u32 [ceil(rows/64)][num_experts]. */
+/* Scratch for aps_moe_dispatch: u32 [ceil(rows/64)][num_experts] (the tile
+ * histogram), then one u32 that the call sets to the number of route ids
+ * >= num_experts it clamped (the last 4 bytes of this size). */
 APS_API size_t aps_moe_dispatch_workspace_size(int64_t rows, int32_t num_experts);
 
 /* ---- stages ------------------------------------------------------------ */
@@ -150,7 +152,13 @@ APS_API int aps_moe_route_top2(const float* logits, int64_t rows, int32_t num_ex
 /* Stable counting-sort dispatch (reference k_moe_offsets_work +
  * k_moe_fill_stable, src/tensor.cu:1333-1418).  Outputs counts[E],
  * offsets[E+1], assignment_rows[2*rows], route_positions[2*rows].
- * `scratch` must hold aps_moe_dispatch_workspace_size(rows, E) bytes. */
+ * `scratch` must hold aps_moe_dispatch_workspace_size(rows, E) bytes.
+ * Routes are (token, slot) pairs sorted stably by expert, token-major, slot
+ * 0 before slot 1.  The reference's routes are always two distinct ids < E;
+ * for caller routes that are not, every output index still stays in range:
+ * a token whose two slots name one expert takes two consecutive positions
+ * of it, and an id >= E is treated as E - 1 and counted into the scratch's
+ * last u32 (0 after a call with valid routes). */
 APS_API int aps_moe_dispatch(const uint8_t* routes, int64_t rows, int32_t num_experts,
                      uint32_t* counts, uint32_t* offsets,
                      uint32_t* assignment_rows, uint32_t* route_positions,

@@ -77,8 +77,10 @@ def test_stage_argument_checks():
     assert L.aps_moe_combine(None, capi.DTYPE_BF16, None, 8, 12, None, capi.DTYPE_BF16, None) == capi.APS_ERR_SHAPE
     assert L.aps_moe_combine(None, capi.DTYPE_E4M3, None, 8, 16, None, capi.DTYPE_BF16, None) == capi.APS_ERR_DTYPE
     assert L.aps_moe_dispatch(None, 8, 16, None, None, None, None, None, 0, None) == capi.APS_ERR_ARG
-    assert L.aps_moe_dispatch_workspace_size(0, 16) == 0
-    assert L.aps_moe_dispatch_workspace_size(65, 16) == 2 * 16 * 4
+    # tile histogram [ceil(rows/64)][E] u32, then the clamped-id counter
+    assert L.aps_moe_dispatch_workspace_size(0, 16) == 4
+    assert L.aps_moe_dispatch_workspace_size(65, 16) == 2 * 16 * 4 + 4
+    assert L.aps_moe_dispatch_workspace_size(-1, 16) == 0
 
 
 def test_python_mirror_raises_value_error_on_shapes():

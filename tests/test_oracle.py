@@ -149,15 +149,22 @@ def test_route_never_picks_same_expert_twice():
 
 # ---- dispatch ---------------------------------------------------------------
 
-@pytest.mark.parametrize("T,E,skew", [(0, 16, False), (1, 16, False), (63, 16, False), (64, 4, True),
-                                      (65, 16, True), (1000, 16, True), (777, 64, False)])
-def test_dispatch_brute_force(T, E, skew):
+@pytest.mark.parametrize("T,E,skew,dup", [(0, 16, False, False), (1, 16, False, False), (63, 16, False, False),
+                                          (64, 4, True, False), (65, 16, True, False), (1000, 16, True, False),
+                                          (777, 64, False, False), (300, 16, False, True), (5, 2, False, True)])
+def test_dispatch_brute_force(T, E, skew, dup):
+    # dup: some tokens name one expert in both slots (caller routes outside
+    # the router's contract); the stable sort of (expert, token, slot) gives
+    # them two consecutive positions, slot 0 first -- the rule the GPU
+    # dispatch keeps for such routes
     rng = np.random.default_rng(T + E)
     if T:
         p = np.arange(1, E + 1, dtype=np.float64) ** (-2.0 if skew else 0.0)
         p /= p.sum()
         first = rng.choice(E, size=T, p=p)
         second = (first + 1 + rng.integers(0, E - 1, size=T)) % E
+        if dup:
+            second[::3] = first[::3]
         routes = np.stack([first, second], 1).astype(np.int32)
     else:
         routes = np.zeros((0, 2), np.int32)
