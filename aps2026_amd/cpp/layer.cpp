@@ -1,8 +1,9 @@
-// PhiMLP / PhiMoE over the C ABI (declared in include/layer.h).
+// The layer classes over the C ABI (declared in include/layer.h).
 //
 // Reference: PhiMLP::PhiMLP and forward (src/layer.cu:44-67), PhiMoE::PhiMoE
-// (src/layer.cu:94-111, the tensor names) and PhiMoE::forward (src/layer.cu:113-121, the GPU
-// branch: router GEMM, then moe_forward_grouped_gpu).
+// (src/layer.cu:94-111, the tensor names) and PhiMoE::forward
+// (src/layer.cu:113-121, the GPU branch), Linear (:13-42), PhiAttention
+// (:150-264) and PhiDecoderLayer (:266-326).
 #include "../../include/layer.h"
 
 #include <stdexcept>
@@ -12,6 +13,7 @@
 namespace aps_cpp_detail {
 void mlp_forward_gpu(std::size_t handle, const Tensor& x, std::size_t rows, Tensor& out);
 std::size_t register_dense(const Tensor& w1, const Tensor& w2, const Tensor& w3);
+void moe_forward_fused(std::size_t handle, const Tensor& x, const Tensor& gate, Tensor& out);
 }  // namespace aps_cpp_detail
 
 PhiMLP::PhiMLP(Tensor w1, Tensor w2, Tensor w3) : w1_(std::move(w1)), w2_(std::move(w2)), w3_(std::move(w3)) {
@@ -65,10 +67,7 @@ PhiMoE::PhiMoE(const ModelLoader& loader, std::size_t layer_idx, aps_dtype compu
 
 void PhiMoE::forward(const Tensor& x, Tensor& y, bool use_gpu) const {
     if (!use_gpu) throw std::invalid_argument("PhiMoE::forward: the CPU path (use_gpu = false) is not provided");
-    const std::size_t rows = x.size(0);
-    Tensor router({rows, apss26::NUM_EXPERTS});
-    if (rows) tensor_ops::matmul_transposed_gpu(x, gate_, router);
-    tensor_ops::moe_forward_grouped_gpu(x, router, gpu_weights_handle_, y);
+    aps_cpp_detail::moe_forward_fused(gpu_weights_handle_, x, gate_, y);
 }
 
 // ---- Linear and PhiAttention (reference src/layer.cu:21-42, 150-188) --------
@@ -79,7 +78,7 @@ Linear::Linear(Tensor weight, Tensor bias) : weight_(std::move(weight)), bias_(s
 }
 
 Linear::Linear(const ModelLoader& loader, const std::string& weight, const std::string& bias)
-    : Linear(loader.load(weight), bias.empty() ? Tensor() : loader.load(bias)) {}
+    : Linear(loader.load(weight), !bias.empty() && loader.has(bias) ? loader.load(bias) : Tensor()) {}
 
 void Linear::forward(const Tensor& x, Tensor& y, bool use_gpu) const {
     if (!use_gpu) throw std::invalid_argument("Linear::forward: the CPU path (use_gpu = false) is not provided");
@@ -108,21 +107,89 @@ PhiAttention::PhiAttention(Linear q_proj, Linear k_proj, Linear v_proj, Linear o
 
 void PhiAttention::forward(const Tensor& x, Tensor& y, const std::vector<std::size_t>& seq_lens, bool use_gpu,
                            const PrefixExpansion& expansion) const {
-    (void)seq_lens;  // the trie path takes positions and key chains from the expansion
     if (!use_gpu) throw std::invalid_argument("PhiAttention::forward: the CPU path (use_gpu = false) is not provided");
-    if (!expansion.active() || !expansion.node_pos)
-        throw std::invalid_argument("PhiAttention::forward: this build provides the prefix-trie path (an active expansion)");
     const std::size_t s = x.size(0);
+    if (expansion.active()) {
+        // the kernels clamp out-of-range device indices for memory safety
+        // only; the expansion's extremes are known on the host, so check them
+        if (!expansion.node_pos || expansion.node_pos->size() != s || expansion.node_anc->size() < s * expansion.anc_stride ||
+            expansion.anc_stride == 0 || expansion.node_pos->max_row() >= expansion.max_seq ||
+            expansion.node_pos->max_row() >= expansion.anc_stride || expansion.node_anc->max_row() >= s)
+            throw std::invalid_argument("PhiAttention prefix expansion");
+    }
     Tensor q, k, v;
     q_proj_.forward(x, q, true);
     k_proj_.forward(x, k, true);
     v_proj_.forward(x, v, true);
-    tensor_ops::apply_rope_tree_gpu(q, k, expansion.node_pos->data(), s, expansion.max_seq,
-                                    apss26::NUM_ATTENTION_HEADS, apss26::NUM_KV_HEADS, apss26::HEAD_DIM,
-                                    apss26::ROPE_THETA);
     Tensor out({s, apss26::NUM_ATTENTION_HEADS * apss26::HEAD_DIM});
-    tensor_ops::attention_tree_gpu(q, k, v, out, expansion.node_pos->data(), expansion.node_anc->data(),
-                                   expansion.anc_stride, s, expansion.max_seq, apss26::NUM_ATTENTION_HEADS,
-                                   apss26::NUM_KV_HEADS, apss26::HEAD_DIM);
+    if (expansion.active()) {
+        // rows are trie nodes: RoPE at the node depth, keys along the chain
+        tensor_ops::apply_rope_tree_gpu(q, k, expansion.node_pos->data(), s, expansion.max_seq,
+                                        apss26::NUM_ATTENTION_HEADS, apss26::NUM_KV_HEADS, apss26::HEAD_DIM,
+                                        apss26::ROPE_THETA);
+        tensor_ops::attention_tree_gpu(q, k, v, out, expansion.node_pos->data(), expansion.node_anc->data(),
+                                       expansion.anc_stride, s, expansion.max_seq, apss26::NUM_ATTENTION_HEADS,
+                                       apss26::NUM_KV_HEADS, apss26::HEAD_DIM);
+    } else {
+        // rows are the packed sequences of seq_lens
+        tensor_ops::apply_rope_gpu(q, k, seq_lens, apss26::NUM_ATTENTION_HEADS, apss26::NUM_KV_HEADS,
+                                   apss26::HEAD_DIM, apss26::ROPE_THETA);
+        tensor_ops::attention_gpu(q, k, v, out, seq_lens, apss26::NUM_ATTENTION_HEADS, apss26::NUM_KV_HEADS,
+                                  apss26::HEAD_DIM);
+    }
     o_proj_.forward(out, y, true);
+}
+
+// ---- PhiDecoderLayer (reference src/layer.cu:266-326) -----------------------
+
+namespace {
+std::string layer_name(std::size_t layer, const char* what) {
+    return "model.layers." + std::to_string(layer) + "." + what;
+}
+}  // namespace
+
+PhiDecoderLayer::PhiDecoderLayer(const ModelLoader& loader, std::size_t layer_idx, aps_dtype moe_compute)
+    : PhiDecoderLayer(loader.load(layer_name(layer_idx, "input_layernorm.weight")),
+                      loader.load(layer_name(layer_idx, "input_layernorm.bias")),
+                      loader.load(layer_name(layer_idx, "post_attention_layernorm.weight")),
+                      loader.load(layer_name(layer_idx, "post_attention_layernorm.bias")),
+                      PhiAttention(loader, layer_idx), PhiMoE(loader, layer_idx, moe_compute)) {}
+
+PhiDecoderLayer::PhiDecoderLayer(Tensor input_norm_weight, Tensor input_norm_bias, Tensor post_norm_weight,
+                                 Tensor post_norm_bias, PhiAttention attention, PhiMoE moe)
+    : input_norm_weight_(std::move(input_norm_weight)),
+      input_norm_bias_(std::move(input_norm_bias)),
+      post_norm_weight_(std::move(post_norm_weight)),
+      post_norm_bias_(std::move(post_norm_bias)),
+      attention_(std::move(attention)),
+      moe_(std::move(moe)) {}
+
+void PhiDecoderLayer::forward_carry(Tensor& x, Tensor& carry, bool has_carry,
+                                    const std::vector<std::size_t>& seq_lens,
+                                    const PrefixExpansion& expansion) const {
+    // layer input: x, or x + carry folded into the input norm (x += carry in place)
+    Tensor normed(x.shape());
+    if (has_carry)
+        tensor_ops::add_layer_norm_gpu(x, carry, input_norm_weight_, input_norm_bias_, apss26::NORM_EPS, normed);
+    else
+        tensor_ops::layer_norm_gpu(x, input_norm_weight_, input_norm_bias_, apss26::NORM_EPS, normed);
+    Tensor attn;
+    attention_.forward(normed, attn, seq_lens, true, expansion);
+    // attn += layer input; the post-attention norm of that feeds the MoE
+    Tensor post(attn.shape());
+    tensor_ops::add_layer_norm_gpu(attn, x, post_norm_weight_, post_norm_bias_, apss26::NORM_EPS, post);
+    Tensor ff;
+    moe_.forward(post, ff, true);
+    x = std::move(ff);
+    carry = std::move(attn);
+}
+
+void PhiDecoderLayer::forward(const Tensor& x, Tensor& y, const std::vector<std::size_t>& seq_lens, bool use_gpu,
+                              const PrefixExpansion& expansion) const {
+    if (!use_gpu)
+        throw std::invalid_argument("PhiDecoderLayer::forward: the CPU path (use_gpu = false) is not provided");
+    Tensor h = x, carry;
+    forward_carry(h, carry, false, seq_lens, expansion);
+    tensor_ops::add_inplace_gpu(h, carry);  // MoE output + residual
+    y = std::move(h);
 }

@@ -1,14 +1,16 @@
-// Tensor and tensor_ops over the C ABI (declared in include/tensor.h).
+// tensor_ops over the C ABI (declared in include/tensor.h; the Tensor class
+// itself is in tensor_storage.cpp).
 //
-// Reference behaviour mirrored: Tensor storage and lazy host/device
-// synchronisation (src/tensor.cu:20-273), register_moe_weights_gpu
-// (src/tensor.cu:2757-2788), moe_forward_grouped_gpu (src/tensor.cu:2790-2928)
-// and the error conventions of check_cuda (src/tensor.cu:370-374).
+// Reference behaviour mirrored: register_moe_weights_gpu
+// (src/tensor.cu:2757-2788), moe_forward_grouped_gpu (src/tensor.cu:2790-2928),
+// the other tensor_ops launchers named at each function, and the error
+// conventions of check_cuda (src/tensor.cu:370-374).
 #include "../../include/tensor.h"
 
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <deque>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -53,160 +55,6 @@ Workspace& workspace() {
 }
 
 }  // namespace
-
-// ---- Tensor ----------------------------------------------------------------
-
-Tensor::Tensor(std::vector<std::size_t> shape) : shape_(std::move(shape)) {
-    numel_ = 1;
-    for (std::size_t d : shape_) numel_ *= d;
-}
-
-Tensor::~Tensor() { drop_dev(); }
-
-Tensor::Tensor(const Tensor& other) : shape_(other.shape_), numel_(other.numel_) {
-    other.ensure_host();
-    host_ = other.host_;
-}
-
-Tensor& Tensor::operator=(const Tensor& other) {
-    if (this == &other) return *this;
-    other.ensure_host();
-    drop_dev();
-    shape_ = other.shape_;
-    numel_ = other.numel_;
-    host_ = other.host_;
-    host_valid_ = true;
-    dev_valid_ = false;
-    return *this;
-}
-
-Tensor::Tensor(Tensor&& other) noexcept
-    : shape_(std::move(other.shape_)),
-      numel_(other.numel_),
-      host_(std::move(other.host_)),
-      dev_(other.dev_),
-      host_valid_(other.host_valid_),
-      dev_valid_(other.dev_valid_) {
-    other.dev_ = nullptr;
-    other.numel_ = 0;
-    other.host_valid_ = true;
-    other.dev_valid_ = false;
-}
-
-Tensor& Tensor::operator=(Tensor&& other) noexcept {
-    if (this == &other) return *this;
-    drop_dev();
-    shape_ = std::move(other.shape_);
-    numel_ = other.numel_;
-    host_ = std::move(other.host_);
-    dev_ = other.dev_;
-    host_valid_ = other.host_valid_;
-    dev_valid_ = other.dev_valid_;
-    other.dev_ = nullptr;
-    other.numel_ = 0;
-    other.host_valid_ = true;
-    other.dev_valid_ = false;
-    return *this;
-}
-
-std::size_t Tensor::size(std::size_t dim) const {
-    if (dim >= shape_.size()) throw std::out_of_range("Tensor dimension");
-    return shape_[dim];
-}
-
-void Tensor::drop_dev() {
-    if (dev_) (void)hipFreeAsync(dev_, nullptr);
-    dev_ = nullptr;
-    dev_valid_ = false;
-}
-
-void Tensor::ensure_dev_alloc() const {
-    if (!dev_ && numel_) hip_check(hipMallocAsync(reinterpret_cast<void**>(&dev_), numel_ * sizeof(float), nullptr),
-                                   "hipMallocAsync tensor");
-}
-
-void Tensor::ensure_host() const {
-    if (host_.size() != numel_) host_.assign(numel_, 0.0f);
-    if (host_valid_) return;
-    if (!dev_ || !dev_valid_) throw std::runtime_error("tensor has no valid storage");
-    hip_check(hipMemcpy(host_.data(), dev_, numel_ * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy tensor D2H");
-    host_valid_ = true;
-}
-
-void Tensor::prepare_cuda() const {
-    if (numel_ == 0) return;
-    ensure_dev_alloc();
-    if (!dev_valid_) {
-        ensure_host();
-        hip_check(hipMemcpy(dev_, host_.data(), numel_ * sizeof(float), hipMemcpyHostToDevice),
-                  "hipMemcpy tensor H2D");
-        dev_valid_ = true;
-    }
-}
-
-const float* Tensor::cuda_data() const {
-    prepare_cuda();
-    return dev_;
-}
-
-float* Tensor::cuda_data_write() {
-    ensure_dev_alloc();
-    dev_valid_ = true;
-    host_valid_ = false;
-    return dev_;
-}
-
-void Tensor::sync_cuda_to_host() const { ensure_host(); }
-
-float* Tensor::data() {
-    ensure_host();
-    dev_valid_ = false;
-    return host_.data();
-}
-
-const float* Tensor::data() const {
-    ensure_host();
-    return host_.data();
-}
-
-float& Tensor::operator[](std::size_t i) { return data()[i]; }
-const float& Tensor::operator[](std::size_t i) const { return data()[i]; }
-
-std::size_t Tensor::index(std::initializer_list<std::size_t> idx) const {
-    if (idx.size() != shape_.size()) throw std::out_of_range("Tensor index");
-    std::size_t flat = 0;
-    std::size_t d = 0;
-    for (std::size_t v : idx) {
-        if (v >= shape_[d]) throw std::out_of_range("Tensor index");
-        flat = flat * shape_[d] + v;
-        ++d;
-    }
-    return flat;
-}
-
-float& Tensor::at(std::size_t i) { return data()[index({i})]; }
-float& Tensor::at(std::size_t i, std::size_t j) { return data()[index({i, j})]; }
-float& Tensor::at(std::size_t i, std::size_t j, std::size_t k) { return data()[index({i, j, k})]; }
-float& Tensor::at(std::size_t i, std::size_t j, std::size_t k, std::size_t l) { return data()[index({i, j, k, l})]; }
-const float& Tensor::at(std::size_t i) const { return data()[index({i})]; }
-const float& Tensor::at(std::size_t i, std::size_t j) const { return data()[index({i, j})]; }
-const float& Tensor::at(std::size_t i, std::size_t j, std::size_t k) const { return data()[index({i, j, k})]; }
-const float& Tensor::at(std::size_t i, std::size_t j, std::size_t k, std::size_t l) const {
-    return data()[index({i, j, k, l})];
-}
-
-void Tensor::reshape(std::vector<std::size_t> shape) {
-    std::size_t n = 1;
-    for (std::size_t d : shape) n *= d;
-    if (n != numel_) throw std::invalid_argument("reshape changes tensor size");
-    shape_ = std::move(shape);
-}
-
-void Tensor::fill(float value) {
-    host_.assign(numel_, value);
-    host_valid_ = true;
-    dev_valid_ = false;
-}
 
 // ---- tensor_ops ------------------------------------------------------------
 
@@ -332,6 +180,28 @@ void moe_forward_grouped_gpu(const Tensor& x, const Tensor& router, std::size_t 
 // ---- dense FFN (used by PhiMLP) ---------------------------------------------
 
 namespace aps_cpp_detail {
+
+// PhiMoE::forward's GPU branch as one aps_moe_forward call: router logits,
+// routing, dispatch, expert FFN and combine over fp32 x [rows][H] into a new
+// out [rows][H].  Throws as moe_forward_grouped_gpu does.
+void moe_forward_fused(std::size_t handle, const Tensor& x, const Tensor& gate, Tensor& out) {
+    const std::size_t rows = x.size(0), h = x.size(x.ndim() - 1);
+    aps_moe_ws_layout L{};
+    if (x.ndim() != 2 || gate.ndim() != 2 || gate.size(0) != apss26::NUM_EXPERTS || gate.size(1) != h ||
+        handle == 0 || aps_moe_workspace_layout(handle, static_cast<int64_t>(rows), &L) != APS_OK)
+        throw std::invalid_argument("grouped MoE shape or handle");
+    out = Tensor({rows, h});
+    if (rows == 0) return;
+    const float* dx = x.cuda_data();
+    const float* dg = gate.cuda_data();
+    float* dout = out.cuda_data_write();
+    Workspace& ws = workspace();
+    std::lock_guard<std::mutex> lk(ws.mu);
+    void* buf = ws.get(L.total_bytes);
+    const int rc = aps_moe_forward(handle, dx, APS_DTYPE_F32, dg, static_cast<int64_t>(rows), dout, APS_DTYPE_F32, buf,
+                                   L.total_bytes, nullptr);
+    if (rc) throw_status(rc, "PhiMoE::forward");
+}
 
 void mlp_forward_gpu(std::size_t handle, const Tensor& x, std::size_t rows, Tensor& out) {
     const std::size_t need = aps_mlp_workspace_size(handle, static_cast<int64_t>(rows));
@@ -549,6 +419,163 @@ void attention_tree_gpu(const Tensor& q, const Tensor& k, const Tensor& v, Tenso
                                       static_cast<int32_t>(head_dim), static_cast<int32_t>(apss26::SLIDING_WINDOW),
                                       nullptr);
     if (rc) throw_status(rc, "attention_tree_gpu");
+}
+
+}  // namespace tensor_ops
+
+// ---- elementwise ops, paired projections (reference src/tensor.cu:3146-3260) -
+
+namespace tensor_ops {
+
+void zero_gpu(Tensor& x) {
+    const int rc = aps_zero(x.cuda_data_write(), static_cast<int64_t>(x.size()), nullptr);
+    if (rc) throw_status(rc, "zero_gpu");
+}
+
+void add_inplace_gpu(Tensor& a, const Tensor& b) {
+    if (a.size() != b.size()) throw std::invalid_argument("add shape");
+    if (!a.size()) return;
+    a.cuda_data();  // upload a stale device copy before writing in place
+    const int rc = aps_add_inplace(a.cuda_data_write(), b.cuda_data(), static_cast<int64_t>(a.size()), nullptr);
+    if (rc) throw_status(rc, "add_inplace_gpu");
+}
+
+void add_bias_inplace_gpu(Tensor& a, const Tensor& bias) {
+    if (bias.ndim() != 1 || a.ndim() == 0 || a.size(a.ndim() - 1) != bias.size(0) || bias.size(0) == 0)
+        throw std::invalid_argument("bias shape");
+    if (!a.size()) return;
+    a.cuda_data();
+    const int rc = aps_add_bias_inplace(a.cuda_data_write(), bias.cuda_data(), static_cast<int64_t>(a.size()),
+                                        static_cast<int32_t>(bias.size(0)), nullptr);
+    if (rc) throw_status(rc, "add_bias_inplace_gpu");
+}
+
+void silu_mul_gpu(const Tensor& gate, const Tensor& up, Tensor& out) {
+    if (gate.size() != up.size() || out.size() != gate.size()) throw std::invalid_argument("silu_mul shape");
+    if (!gate.size()) return;
+    const float* g = gate.cuda_data();
+    const float* u = up.cuda_data();
+    const int rc = aps_silu_mul(g, u, out.cuda_data_write(), static_cast<int64_t>(gate.size()), nullptr);
+    if (rc) throw_status(rc, "silu_mul_gpu");
+}
+
+void matmul_pair_silu_gpu(const Tensor& a, const Tensor& gate_weight, const Tensor& up_weight, Tensor& out) {
+    const std::size_t k = a.size(a.ndim() - 1);
+    const std::size_t m = a.size() / k;
+    const std::size_t n = gate_weight.size(0);
+    if (gate_weight.size(1) != k || up_weight.size(0) != n || up_weight.size(1) != k || out.size(0) != m ||
+        out.size(1) != n)
+        throw std::invalid_argument("matmul_pair_silu_gpu shape");
+    // the two products as single fp32 chains, then the SiLU-mul: the
+    // reference kernel's arithmetic per output, in three launches
+    Tensor g({m, n}), u({m, n});
+    matmul_transposed_gpu(a, gate_weight, g);
+    matmul_transposed_gpu(a, up_weight, u);
+    silu_mul_gpu(g, u, out);
+}
+
+void matmul_pair_bias_gpu(const Tensor& a, const Tensor& first_weight, const Tensor& first_bias, Tensor& first_out,
+                          const Tensor& second_weight, const Tensor& second_bias, Tensor& second_out) {
+    const std::size_t k = a.size(a.ndim() - 1);
+    const std::size_t m = a.size() / k;
+    const std::size_t n = first_weight.size(0);
+    if (first_weight.size(1) != k || second_weight.size(0) != n || second_weight.size(1) != k ||
+        first_bias.size() != n || second_bias.size() != n || first_out.size(0) != m || first_out.size(1) != n ||
+        second_out.size(0) != m || second_out.size(1) != n)
+        throw std::invalid_argument("matmul_pair_bias_gpu shape");
+    matmul_transposed_bias_gpu(a, first_weight, first_bias, first_out);
+    matmul_transposed_bias_gpu(a, second_weight, second_bias, second_out);
+}
+
+}  // namespace tensor_ops
+
+// ---- packed-sequence RoPE and attention (reference src/tensor.cu:3296-3340) ---
+
+namespace {
+
+// Per-row segment start and position of a packed batch, on the device,
+// cached per seq_lens (the reference's packed_meta keeps the last one; this
+// keeps a few, since a prefill alternates between the same two or three).
+struct PackedSegments {
+    std::vector<std::size_t> lens;
+    std::size_t rows = 0, max_seq = 0;
+    int dev = 0;
+    std::uint32_t* offset = nullptr;  // [rows]
+    std::uint32_t* pos = nullptr;     // [rows]
+};
+std::mutex g_seg_mu;
+std::deque<PackedSegments> g_segs;  // push_back keeps references to the others valid
+
+const PackedSegments& packed_segments(const std::vector<std::size_t>& seq_lens) {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_seg_mu);
+    for (const PackedSegments& s : g_segs)
+        if (s.dev == dev && s.lens == seq_lens) return s;
+    PackedSegments s;
+    s.lens = seq_lens;
+    s.dev = dev;
+    std::vector<std::uint32_t> off, pos;
+    for (std::size_t len : seq_lens) {
+        if (s.rows + len > 0xFFFFFFFFull) throw std::invalid_argument("packed sequence lengths");
+        for (std::size_t p = 0; p < len; ++p) {
+            off.push_back(static_cast<std::uint32_t>(s.rows));
+            pos.push_back(static_cast<std::uint32_t>(p));
+        }
+        s.rows += len;
+        s.max_seq = std::max(s.max_seq, len);
+    }
+    if (s.rows) {
+        hip_check(hipMalloc(&s.offset, s.rows * sizeof(std::uint32_t)), "hipMalloc segment offsets");
+        hip_check(hipMalloc(&s.pos, s.rows * sizeof(std::uint32_t)), "hipMalloc segment positions");
+        hip_check(hipMemcpy(s.offset, off.data(), s.rows * sizeof(std::uint32_t), hipMemcpyHostToDevice),
+                  "copy segment offsets");
+        hip_check(hipMemcpy(s.pos, pos.data(), s.rows * sizeof(std::uint32_t), hipMemcpyHostToDevice),
+                  "copy segment positions");
+    }
+    if (g_segs.size() == 8) {  // keep the cache small; the legacy stream orders the frees after queued use
+        hip_check(hipDeviceSynchronize(), "segment cache");
+        (void)hipFree(g_segs.front().offset);
+        (void)hipFree(g_segs.front().pos);
+        g_segs.pop_front();
+    }
+    g_segs.push_back(std::move(s));
+    return g_segs.back();
+}
+
+}  // namespace
+
+namespace tensor_ops {
+
+void apply_rope_gpu(Tensor& q, Tensor& k, const std::vector<std::size_t>& seq_lens, std::size_t q_heads,
+                    std::size_t kv_heads, std::size_t head_dim, float theta) {
+    const std::size_t rows = head_dim && q_heads ? q.size() / (q_heads * head_dim) : 0;
+    if (q.size() != rows * q_heads * head_dim || k.size() != rows * kv_heads * head_dim || head_dim % 2 != 0)
+        throw std::invalid_argument("apply_rope_gpu shape");
+    const PackedSegments& seg = packed_segments(seq_lens);
+    if (seg.rows != rows) throw std::invalid_argument("packed sequence lengths");
+    if (rows == 0) return;
+    // positions restart per sequence, so the longest sequence bounds the table
+    apply_rope_tree_gpu(q, k, seg.pos, rows, seg.max_seq, q_heads, kv_heads, head_dim, theta);
+}
+
+void attention_gpu(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out,
+                   const std::vector<std::size_t>& seq_lens, std::size_t q_heads, std::size_t kv_heads,
+                   std::size_t head_dim) {
+    if (q_heads != 4 * kv_heads) throw std::invalid_argument("attention_gpu expects GQA-4");
+    const std::size_t rows = head_dim && q_heads ? q.size() / (q_heads * head_dim) : 0;
+    if (q.size() != rows * q_heads * head_dim || k.size() != rows * kv_heads * head_dim || v.size() != k.size() ||
+        out.size() != q.size())
+        throw std::invalid_argument("attention_gpu shape");
+    const PackedSegments& seg = packed_segments(seq_lens);
+    if (seg.rows != rows) throw std::invalid_argument("packed sequence lengths");
+    if (rows == 0) return;
+    const int rc = aps_attention_packed(q.cuda_data(), k.cuda_data(), v.cuda_data(), out.cuda_data_write(),
+                                        seg.offset, seg.pos, static_cast<int64_t>(seg.max_seq),
+                                        static_cast<int64_t>(rows), static_cast<int32_t>(q_heads),
+                                        static_cast<int32_t>(kv_heads), static_cast<int32_t>(head_dim),
+                                        static_cast<int32_t>(apss26::SLIDING_WINDOW), nullptr);
+    if (rc) throw_status(rc, "attention_gpu");
 }
 
 }  // namespace tensor_ops

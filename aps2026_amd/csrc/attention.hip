@@ -47,7 +47,7 @@ k_rope_tree(float* __restrict__ x, const uint32_t* __restrict__ row_pos, int64_t
     const int64_t rh = pair / half;  // row * heads + head
     const int64_t row = rh / heads;
     const uint32_t pos = row_pos[row];
-    if (pos >= max_seq) return;  // outside the table: left as is (the host checks positions)
+    if (pos >= max_seq) return;  // outside the table: left as is (the C++ layer checks positions)
     float* base = x + rh * (2 * half);
     const int64_t t = static_cast<int64_t>(pos) * half + j;
     const float c = cosv[t], s = sinv[t];
@@ -57,6 +57,13 @@ k_rope_tree(float* __restrict__ x, const uint32_t* __restrict__ row_pos, int64_t
 }
 
 // Dynamic LDS: scores [wmax][4] fp32, then chain [wmax] u32.
+// PACKED: the rows are packed token sequences (reference k_attention_grouped_gqa4,
+// src/tensor.cu:2267-2405, which the tree kernel restates with an index
+// indirection): `anc` holds each row's segment start seg_offset[row], the
+// keys of a row are the contiguous rows seg_offset + begin .. seg_offset +
+// pos, and anc_stride is the longest segment.  Otherwise the keys are the
+// ancestor chain anc[row][begin .. pos] of a trie node.
+template <bool PACKED>
 __global__ void __launch_bounds__(kAttnThreads)
 k_attention_tree(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
                  float* __restrict__ out, const uint32_t* __restrict__ row_pos, const uint32_t* __restrict__ anc,
@@ -70,14 +77,18 @@ k_attention_tree(const float* __restrict__ q, const float* __restrict__ k, const
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t row = blockIdx.x / kv_heads;
     const int kh = static_cast<int>(blockIdx.x % kv_heads);
-    // positions past the ancestor table are clamped (the host checks them)
+    // Positions past the ancestor table and key rows past the end are
+    // clamped, for memory safety only: the C++ layer checks them (through
+    // RowIndexBuffer::max_row and the packed segment table), and direct
+    // C-ABI callers must keep them in range.
     int64_t pos = row_pos[row];
     pos = pos < anc_stride ? pos : anc_stride - 1;
     const int64_t begin = pos + 1 > wmax ? pos + 1 - wmax : 0;
     const int window = static_cast<int>(pos - begin + 1);
+    const int64_t seg = PACKED ? static_cast<int64_t>(anc[row]) : 0;
     for (int i = tid; i < window; i += kAttnThreads) {
-        const uint32_t a = anc[row * anc_stride + begin + i];
-        chain[i] = a < rows ? a : static_cast<uint32_t>(rows - 1);  // memory safety only
+        const int64_t a = PACKED ? seg + begin + i : static_cast<int64_t>(anc[row * anc_stride + begin + i]);
+        chain[i] = static_cast<uint32_t>(a < rows ? a : rows - 1);
     }
     for (int i = tid; i < kGroup * kHeadDim; i += kAttnThreads) {
         const int g = i / kHeadDim, d = i % kHeadDim;
@@ -190,7 +201,7 @@ hipError_t launch_rope_tree(float* x, const uint32_t* row_pos, int64_t rows, int
 
 hipError_t launch_attention_tree(const float* q, const float* k, const float* v, float* out, const uint32_t* row_pos,
                                  const uint32_t* anc, int64_t anc_stride, int64_t rows, int q_heads, int kv_heads,
-                                 int head_dim, int window_max, hipStream_t s) {
+                                 int head_dim, int window_max, bool packed, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (head_dim != kHeadDim || q_heads != kGroup * kv_heads || anc_stride <= 0 || window_max <= 0)
         return hipErrorInvalidValue;
@@ -199,16 +210,17 @@ hipError_t launch_attention_tree(const float* q, const float* k, const float* v,
     const int wmax = static_cast<int>(keys);
     const size_t lds = static_cast<size_t>(wmax) * (kGroup * sizeof(float) + sizeof(uint32_t));
     // dynamic LDS past 64 KB needs the function's limit raised first
+    auto kern = packed ? &k_attention_tree<true> : &k_attention_tree<false>;
     if (lds > 65536) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention_tree),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (e != hipSuccess) return e;
     }
     // 1 / sqrtf(head_dim), both correctly rounded, as the reference kernel computes it
     const float root = sqrtf(static_cast<float>(head_dim));
     const float scale = 1.0f / root;
-    hipLaunchKernelGGL(k_attention_tree, dim3(static_cast<unsigned>(rows * kv_heads)), dim3(kAttnThreads), lds, s, q,
-                       k, v, out, row_pos, anc, anc_stride, rows, q_heads, kv_heads, wmax, scale);
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(rows * kv_heads)), dim3(kAttnThreads), lds, s, q, k, v, out,
+                       row_pos, anc, anc_stride, rows, q_heads, kv_heads, wmax, scale);
     return hipGetLastError();
 }
 

@@ -628,8 +628,56 @@ int aps_attention_tree(const float* q, const float* k, const float* v, float* ou
     if (!q || !k || !v || !out || !row_pos || !anc) return fail(APS_ERR_ARG, "attention tree: NULL pointer");
     if ((reinterpret_cast<uintptr_t>(k) & 15u) != 0) return fail(APS_ERR_ARG, "attention tree: k must be 16-byte aligned");
     APS_HIP(aps::launch_attention_tree(q, k, v, out, row_pos, anc, anc_stride, rows, q_heads, kv_heads, head_dim,
-                                       window, static_cast<hipStream_t>(stream)),
+                                       window, false, static_cast<hipStream_t>(stream)),
             "attention tree launch");
+    return APS_OK;
+}
+
+int aps_attention_packed(const float* q, const float* k, const float* v, float* out, const uint32_t* seg_offset,
+                         const uint32_t* seg_pos, int64_t max_seq, int64_t rows, int32_t q_heads, int32_t kv_heads,
+                         int32_t head_dim, int32_t window, void* stream) {
+    if (kv_heads <= 0 || q_heads != 4 * kv_heads) return fail(APS_ERR_SHAPE, "attention_gpu expects GQA-4");
+    if (rows < 0 || head_dim != 128 || max_seq <= 0 || window <= 0)
+        return fail(APS_ERR_SHAPE, "attention shape: rows %lld head_dim %d (128 only) max_seq %lld window %d",
+                    (long long)rows, head_dim, (long long)max_seq, window);
+    if ((max_seq < window ? max_seq : window) > aps::kAttnMaxWindow)
+        return fail(APS_ERR_SHAPE, "attention: a window of %lld keys exceeds the %d that fit in LDS",
+                    (long long)(max_seq < window ? max_seq : window), aps::kAttnMaxWindow);
+    if (rows == 0) return APS_OK;
+    if (!q || !k || !v || !out || !seg_offset || !seg_pos) return fail(APS_ERR_ARG, "attention: NULL pointer");
+    if ((reinterpret_cast<uintptr_t>(k) & 15u) != 0) return fail(APS_ERR_ARG, "attention: k must be 16-byte aligned");
+    APS_HIP(aps::launch_attention_tree(q, k, v, out, seg_pos, seg_offset, max_seq, rows, q_heads, kv_heads, head_dim,
+                                       window, true, static_cast<hipStream_t>(stream)),
+            "attention launch");
+    return APS_OK;
+}
+
+int aps_add_inplace(float* a, const float* b, int64_t n, void* stream) {
+    if (n < 0) return fail(APS_ERR_SHAPE, "add shape: %lld elements", (long long)n);
+    if (n > 0 && (!a || !b)) return fail(APS_ERR_ARG, "add: NULL pointer");
+    APS_HIP(aps::launch_add_inplace(a, b, n, static_cast<hipStream_t>(stream)), "add launch");
+    return APS_OK;
+}
+
+int aps_add_bias_inplace(float* a, const float* bias, int64_t n, int32_t h, void* stream) {
+    if (n < 0 || h <= 0 || n % h != 0)
+        return fail(APS_ERR_SHAPE, "bias shape: %lld elements, bias of %d", (long long)n, h);
+    if (n > 0 && (!a || !bias)) return fail(APS_ERR_ARG, "add bias: NULL pointer");
+    APS_HIP(aps::launch_add_bias(a, bias, n, h, static_cast<hipStream_t>(stream)), "add bias launch");
+    return APS_OK;
+}
+
+int aps_silu_mul(const float* gate, const float* up, float* out, int64_t n, void* stream) {
+    if (n < 0) return fail(APS_ERR_SHAPE, "silu_mul shape: %lld elements", (long long)n);
+    if (n > 0 && (!gate || !up || !out)) return fail(APS_ERR_ARG, "silu_mul: NULL pointer");
+    APS_HIP(aps::launch_silu_mul(gate, up, out, n, static_cast<hipStream_t>(stream)), "silu_mul launch");
+    return APS_OK;
+}
+
+int aps_zero(float* x, int64_t n, void* stream) {
+    if (n < 0) return fail(APS_ERR_SHAPE, "zero shape: %lld elements", (long long)n);
+    if (n > 0 && !x) return fail(APS_ERR_ARG, "zero: NULL pointer");
+    APS_HIP(aps::launch_zero(x, n, static_cast<hipStream_t>(stream)), "zero launch");
     return APS_OK;
 }
 

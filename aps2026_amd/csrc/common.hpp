@@ -165,7 +165,13 @@ hipError_t launch_rope_tree(float* x, const uint32_t* row_pos, int64_t rows, int
 constexpr int kAttnMaxWindow = 7936;
 hipError_t launch_attention_tree(const float* q, const float* k, const float* v, float* out, const uint32_t* row_pos,
                                  const uint32_t* anc, int64_t anc_stride, int64_t rows, int q_heads, int kv_heads,
-                                 int head_dim, int window_max, hipStream_t s);
+                                 int head_dim, int window_max, bool packed, hipStream_t s);
+
+// Elementwise fp32 ops (reference k_add, k_add_bias, k_silu_mul, zero_gpu).
+hipError_t launch_add_inplace(float* a, const float* b, int64_t n, hipStream_t s);
+hipError_t launch_add_bias(float* a, const float* bias, int64_t n, int h, hipStream_t s);
+hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t s);
+hipError_t launch_zero(float* x, int64_t n, hipStream_t s);
 
 // y = x w^T (+ bias): fp32 FMA chain over k ascending per output, bias added
 // once (in_f % 16 == 0, out_f % 4 == 0).

@@ -345,6 +345,42 @@ APS_API int aps_attention_tree(const float* q, const float* k, const float* v, f
                                const uint32_t* anc, int64_t anc_stride, int64_t rows, int32_t q_heads,
                                int32_t kv_heads, int32_t head_dim, int32_t window, void* stream);
 
+/* Replaces tensor_ops::attention_gpu's GQA-4 path (reference include/tensor.h:
+ * 95-98, src/tensor.cu:3318-3340, kernel k_attention_grouped_gqa4
+ * :2267-2405): the same attention and arithmetic as aps_attention_tree, over
+ * packed token sequences instead of trie nodes -- row r of a segment that
+ * starts at row seg_offset[r] sits at position seg_pos[r] in it, and its
+ * keys are rows seg_offset[r] + begin .. seg_offset[r] + seg_pos[r] (begin =
+ * max(0, pos + 1 - window)).  max_seq bounds every segment length (the
+ * reference's PackedMeta::max_seq).  q_heads = 4 kv_heads ("attention_gpu
+ * expects GQA-4": the reference's fallback kernel for other ratios,
+ * k_attention, is not provided); head_dim 128; k 16-byte aligned.  RoPE of
+ * packed rows is aps_rope_tree with row_pos = seg_pos. */
+APS_API int aps_attention_packed(const float* q, const float* k, const float* v, float* out,
+                                 const uint32_t* seg_offset, const uint32_t* seg_pos, int64_t max_seq, int64_t rows,
+                                 int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t window, void* stream);
+
+/* ---- elementwise fp32 ops of the decoder layer ---------------------------- */
+
+/* a[i] += b[i] for i < n (reference add_inplace_gpu, include/tensor.h:83,
+ * src/tensor.cu:3236-3242, kernel k_add :1990-1993). */
+APS_API int aps_add_inplace(float* a, const float* b, int64_t n, void* stream);
+
+/* a[i] += bias[i % h] for i < n, n a multiple of h (reference
+ * add_bias_inplace_gpu, include/tensor.h:84, src/tensor.cu:3244-3252, kernel
+ * k_add_bias :1995-1999). */
+APS_API int aps_add_bias_inplace(float* a, const float* bias, int64_t n, int32_t h, void* stream);
+
+/* out[i] = (g / (1 + (float)exp((double)-g))) * up[i], g = gate[i] (reference
+ * silu_mul_gpu, include/tensor.h:85, src/tensor.cu:3254-3260, kernel
+ * k_silu_mul :2001-2010); out may alias gate or up. */
+APS_API int aps_silu_mul(const float* gate, const float* up, float* out, int64_t n, void* stream);
+
+/* x[i] = 0 for i < n by a kernel, so the call may be recorded into a HIP
+ * graph (reference zero_gpu, include/tensor.h:82, src/tensor.cu:277-281,
+ * a cudaMemsetAsync there). */
+APS_API int aps_zero(float* x, int64_t n, void* stream);
+
 /* ---- diagnostics ------------------------------------------------------- */
 
 APS_API const char* aps_moe_last_error(void);

@@ -1,12 +1,11 @@
-// Model constants of the MoE block, under the reference's names
-// (include/config.h:5-27 of the reference: namespace apss26).  Only the
-// constants the MoE feed-forward path, its LayerNorm, the prompt prefix
-// deduplication and the tree attention read are kept here.
+// Model constants under the reference's names (include/config.h:5-27 of the
+// reference: namespace apss26), the same values.
 #pragma once
 
 #include <cstddef>
 
 namespace apss26 {
+constexpr std::size_t NUM_LAYERS = 32;
 constexpr std::size_t HIDDEN_SIZE = 4096;
 constexpr std::size_t NUM_EXPERTS = 16;
 constexpr std::size_t TOP_K = 2;
@@ -28,4 +27,10 @@ constexpr std::size_t NUM_KV_HEADS = 4;
 constexpr std::size_t HEAD_DIM = 128;
 constexpr std::size_t SLIDING_WINDOW = 2047;
 constexpr float ROPE_THETA = 10000.0f;
+// Greedy decoding (reference include/config.h:20, 24-25): the end-of-text
+// token and the default number of generated tokens.  ROUTER_JITTER_EPS is
+// declared by the reference and read nowhere, here neither.
+constexpr float ROUTER_JITTER_EPS = 0.01f;
+constexpr std::size_t MAX_DECODE_TOKENS = 8;
+constexpr int EOS_TOKEN_ID = 32000;
 }  // namespace apss26

@@ -1,4 +1,5 @@
-// PhiMLP and PhiMoE layers over the C ABI (reference include/layer.h:23-43).
+// Linear, PhiMLP, PhiMoE, PhiAttention and PhiDecoderLayer over the C ABI
+// (reference include/layer.h:11-95).
 //
 // The forward signatures are the reference's, and so are the ModelLoader
 // constructors (src/layer.cu:44-47, 94-111: the same tensor names); the
@@ -18,8 +19,10 @@
 #include "tensor.h"
 
 // A dense layer y = x W^T (+ b) (reference include/layer.h:11-21,
-// src/layer.cu:21-42).  The GPU path is one fp32 FMA chain per output over k
+// src/layer.cu:13-42).  The GPU path is one fp32 FMA chain per output over k
 // ascending with the bias added once, the reference GPU kernel's arithmetic.
+// The loader constructor loads the bias only when the file holds it, as the
+// reference does (a bias-less lm_head is valid).
 class Linear {
 public:
     Linear() = default;
@@ -62,7 +65,11 @@ public:
     // model.layers.<layer_idx>.block_sparse_moe.gate.weight and
     // ....experts.<e>.{w1,w2,w3}.weight for e < NUM_EXPERTS
     PhiMoE(const ModelLoader& loader, std::size_t layer_idx, aps_dtype compute = APS_DTYPE_F32);
-    // y [rows][H] = sum over the two routed experts of 0.5 * expert(x).
+    // y [rows][H] = sum over the two routed experts of 0.5 * expert(x): the
+    // reference's router GEMM and grouped block (src/layer.cu:113-121) as one
+    // fused call (aps_moe_forward: the router kernel also routes, and for
+    // bf16 compute writes the FFN's bf16 copy of x), with the same logits,
+    // routes and, for fp32 compute, the same output bits.
     void forward(const Tensor& x, Tensor& y, bool use_gpu = false) const;
 
 private:
@@ -82,10 +89,14 @@ struct PrefixExpansion {
 };
 
 // Self-attention of the decoder layer (reference include/layer.h:65-75,
-// src/layer.cu:150-188): q/k/v/o projections with bias, RoPE and GQA
-// attention.  This build provides the prefix-trie path (expansion.active():
-// RoPE at node depths, attention over ancestor chains, as the reference's
-// prefill); without an expansion forward throws std::invalid_argument.
+// src/layer.cu:150-264): q/k/v/o projections with bias, RoPE and GQA-4
+// attention.  With an active expansion the rows are prefix-trie nodes (RoPE
+// at node depths, attention over ancestor chains: the reference's prefill);
+// without one they are the sequences of seq_lens packed one after another
+// (positions restart per sequence, keys never cross a sequence).  The
+// expansion's positions must be < max_seq and < anc_stride and its
+// ancestors < the row count (std::invalid_argument("PhiAttention prefix
+// expansion") otherwise).
 class PhiAttention {
 public:
     PhiAttention(const ModelLoader& loader, std::size_t layer_idx);
@@ -95,4 +106,33 @@ public:
 
 private:
     Linear q_proj_, k_proj_, v_proj_, o_proj_;
+};
+
+// One decoder layer (reference include/layer.h:77-95, src/layer.cu:266-326):
+// LayerNorm -> attention -> residual add + LayerNorm -> MoE.  Norms are
+// LayerNorm with bias, eps NORM_EPS.
+class PhiDecoderLayer {
+public:
+    // model.layers.<i>.{input_layernorm,post_attention_layernorm}.{weight,bias},
+    // the layer's attention and MoE block; moe_compute as in PhiMoE.
+    PhiDecoderLayer(const ModelLoader& loader, std::size_t layer_idx, aps_dtype moe_compute = APS_DTYPE_F32);
+    PhiDecoderLayer(Tensor input_norm_weight, Tensor input_norm_bias, Tensor post_norm_weight, Tensor post_norm_bias,
+                    PhiAttention attention, PhiMoE moe);
+    // Residual-carrying form of the packed GPU prefill: on entry the layer
+    // input is x (has_carry false) or x + carry (has_carry true, the add
+    // folded into the input LayerNorm); on exit x holds the MoE output and
+    // carry the attention residual (attention output + layer input), whose
+    // add rides into the next LayerNorm.
+    void forward_carry(Tensor& x, Tensor& carry, bool has_carry, const std::vector<std::size_t>& seq_lens,
+                       const PrefixExpansion& expansion) const;
+    // y = MoE(LN(attn + x)) + (attn + x), attn = attention(LN(x)).  GPU only
+    // (use_gpu = false throws std::invalid_argument).
+    void forward(const Tensor& x, Tensor& y, const std::vector<std::size_t>& seq_lens, bool use_gpu = false,
+                 const PrefixExpansion& expansion = {}) const;
+
+private:
+    Tensor input_norm_weight_, input_norm_bias_;
+    Tensor post_norm_weight_, post_norm_bias_;
+    PhiAttention attention_;
+    PhiMoE moe_;
 };

@@ -17,7 +17,6 @@
 
 #include <cstddef>
 #include <cstdint>
-#include <initializer_list>
 #include <vector>
 
 #include "aps_moe.h"
@@ -60,17 +59,23 @@ public:
     void sync_cuda_to_host() const;
 
 private:
+    // Which copies hold the current values: a bit mask of kOnHost / kOnDevice.
+    // A host copy that was never materialised (host_ empty while kOnHost is
+    // set) stands for all zeros, so a fresh tensor costs no host memory until
+    // the host reads it, and a device-written one never allocates it at all.
+    enum : unsigned { kOnHost = 1u, kOnDevice = 2u };
     std::vector<std::size_t> shape_;
     std::size_t numel_ = 0;
     mutable std::vector<float> host_;
     mutable float* dev_ = nullptr;
-    mutable bool host_valid_ = true;
-    mutable bool dev_valid_ = false;
+    mutable unsigned fresh_ = kOnHost;
 
-    std::size_t index(std::initializer_list<std::size_t> idx) const;
-    void ensure_host() const;
-    void ensure_dev_alloc() const;
-    void drop_dev();
+    std::size_t flat_index(const std::size_t* idx, std::size_t n) const;
+    float* host_current() const;      // host copy brought up to date
+    float* host_for_write();          // ... and made the only current copy
+    float* device_buffer() const;     // allocated on first use, stream-ordered
+    void release_device() noexcept;
+    void swap(Tensor& other) noexcept;
 };
 
 namespace tensor_ops {
@@ -90,6 +95,45 @@ void matmul_transposed_gpu(const Tensor& a, const Tensor& b, Tensor& c);
 // std::invalid_argument("matmul_transposed_bias_gpu shape") as the reference
 // does; this build needs k % 16 == 0 and n % 4 == 0.
 void matmul_transposed_bias_gpu(const Tensor& a, const Tensor& b, const Tensor& bias, Tensor& c);
+
+// out = silu(a . gate_weight^T) * (a . up_weight^T) (reference
+// include/tensor.h:75-76, src/tensor.cu:3146-3170): each product one fp32
+// FMA chain per output over k ascending, then the reference's SiLU-mul
+// (exp in double).  Throws std::invalid_argument("matmul_pair_silu_gpu
+// shape") as the reference does.
+void matmul_pair_silu_gpu(const Tensor& a, const Tensor& gate_weight, const Tensor& up_weight, Tensor& out);
+
+// first_out = a . first_weight^T + first_bias and the same for second
+// (reference include/tensor.h:77-81, src/tensor.cu:3172-3234: the k/v
+// projections sharing their input).  Throws
+// std::invalid_argument("matmul_pair_bias_gpu shape").
+void matmul_pair_bias_gpu(const Tensor& a, const Tensor& first_weight, const Tensor& first_bias, Tensor& first_out,
+                          const Tensor& second_weight, const Tensor& second_bias, Tensor& second_out);
+
+// Elementwise ops of the reference (include/tensor.h:82-85,
+// src/tensor.cu:3236-3260, 277-281): x = 0; a += b ("add shape");
+// a += bias per last-dimension column ("bias shape"); out = silu(gate) * up
+// ("silu_mul shape").
+void zero_gpu(Tensor& x);
+void add_inplace_gpu(Tensor& a, const Tensor& b);
+void add_bias_inplace_gpu(Tensor& a, const Tensor& bias);
+void silu_mul_gpu(const Tensor& gate, const Tensor& up, Tensor& out);
+
+// RoPE and GQA-4 attention over packed sequences (reference
+// include/tensor.h:91-98, src/tensor.cu:3296-3340): the rows of q/k/v are
+// the sequences of seq_lens one after another; a row's position restarts at
+// 0 with its sequence and its keys are the earlier rows of its own sequence
+// (the last SLIDING_WINDOW of them).  The per-row segment table is
+// uploaded once per distinct seq_lens and cached, as the reference's
+// packed_meta.  attention_gpu throws std::invalid_argument("attention_gpu
+// expects GQA-4") unless q_heads == 4 kv_heads (the reference's fallback
+// kernel for other ratios is not provided); a seq_lens total different from
+// the row count throws std::invalid_argument("packed sequence lengths").
+void apply_rope_gpu(Tensor& q, Tensor& k, const std::vector<std::size_t>& seq_lens, std::size_t q_heads,
+                    std::size_t kv_heads, std::size_t head_dim, float theta);
+void attention_gpu(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out,
+                   const std::vector<std::size_t>& seq_lens, std::size_t q_heads, std::size_t kv_heads,
+                   std::size_t head_dim);
 
 // Registers the 16 experts' w1 / w2 / w3 (nn.Linear layout: w1, w3 [F][H],
 // w2 [H][F]) and returns a 1-based handle.  Throws
@@ -163,7 +207,9 @@ void gather_rows_gpu(const Tensor& x, const RowIndexBuffer& rows, Tensor& out);
 // include/tensor.h:100-103, src/tensor.cu:3342-3359): the cos/sin tables of
 // max_seq positions are built on the host once per (head_dim, theta) and
 // kept on the device, grown when a larger max_seq arrives.  Positions must
-// be < max_seq (a row past the table is left unchanged).
+// be < max_seq: the positions are device data this function does not read,
+// so a row past the table is left unchanged rather than reported
+// (PhiAttention checks its expansion's positions before the call).
 void apply_rope_tree_gpu(Tensor& q, Tensor& k, const std::uint32_t* row_pos, std::size_t rows, std::size_t max_seq,
                          std::size_t q_heads, std::size_t kv_heads, std::size_t head_dim, float theta);
 
@@ -172,6 +218,9 @@ void apply_rope_tree_gpu(Tensor& q, Tensor& k, const std::uint32_t* row_pos, std
 // (reference include/tensor.h:109-114, src/tensor.cu:3361-3377).  Throws
 // std::invalid_argument("attention_tree_gpu expects GQA-4") as the
 // reference does; out must hold rows x q_heads x head_dim values.
+// Positions must be < anc_stride and ancestors < rows: the kernel clamps
+// device values outside those ranges for memory safety only (PhiAttention
+// checks its expansion first).
 void attention_tree_gpu(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out, const std::uint32_t* row_pos,
                         const std::uint32_t* anc, std::size_t anc_stride, std::size_t rows, std::size_t max_seq,
                         std::size_t q_heads, std::size_t kv_heads, std::size_t head_dim);

@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "../../include/layer.h"
+#include "../../include/model.h"
 #include "../../include/prefix.h"
 
 namespace {
@@ -127,8 +128,14 @@ int loader_check(const std::string& dir, const std::string& model) {
         Tensor ya;
         attn.forward(x, ya, trie.seq_lens, true, ex);
         write_raw(dir, "loader_attn", ya);
-        expect_throw<std::invalid_argument>([&] { attn.forward(x, ya, trie.seq_lens, true); }, nullptr,
-                                            "attention without an expansion");
+        // the packed path needs seq_lens covering the rows
+        expect_throw<std::invalid_argument>([&] { attn.forward(x, ya, {1, 2}, true); }, "packed sequence lengths",
+                                            "attention packed lengths");
+        // an expansion whose positions run past max_seq is refused on the host
+        PrefixExpansion short_ex = ex;
+        short_ex.max_seq = 3;
+        expect_throw<std::invalid_argument>([&] { attn.forward(x, ya, trie.seq_lens, true, short_ex); },
+                                            "PhiAttention prefix expansion", "expansion positions checked");
     }
     expect_throw<std::runtime_error>([&] { (void)loader.load("nope"); }, "missing tensor: nope", "missing tensor");
     const std::string nofile = dir + "/absent.bin";
@@ -157,14 +164,141 @@ int loader_check(const std::string& dir, const std::string& model) {
     return g_failures ? 1 : 0;
 }
 
+// The prompts of the model mode (tests/test_gpu_cpp_layer.py uses the same):
+// shared prefixes, a prompt that is a prefix of another, a lone token.
+const std::vector<std::vector<int>> kPrompts = {
+    {5, 6, 7, 8, 9, 10}, {5, 6, 7, 1, 2}, {3, 4}, {5, 6, 7, 8, 11}, {5, 6, 7}, {9}};
+
+// model mode: a two-layer PhiTinyMoEModel from the file's layers 0 and 1
+// (the loader constructor reads NUM_LAYERS layers; this one is built from
+// PhiDecoderLayer(loader, i) parts): generate() on kPrompts, forward() on
+// the first prompt, generate_decode() for three tokens of the third, a
+// two-layer decoder-layer forward() chain on the packed prompts, the
+// elementwise tensor_ops, and the reference's error messages.
+int model_check(const std::string& dir, const std::string& model) {
+    const ModelLoader loader(model);
+    std::vector<PhiDecoderLayer> layers;
+    for (std::size_t i = 0; i < 2; ++i) layers.emplace_back(loader, i);
+    const Linear head(loader, "lm_head.weight", "lm_head.bias");
+    const Linear head_nobias(loader, "lm_head.weight", "lm_head.no_such_bias");
+    expect(head.bias().size() == head.weight().size(0), "lm_head bias loaded");
+    expect(head_nobias.bias().size() == 0, "an absent bias is skipped, as the reference does");
+    const PhiTinyMoEModel m(loader.load("model.embed_tokens.weight"), loader.load("model.norm.weight"),
+                            loader.load("model.norm.bias"), head, std::move(layers));
+    expect(m.num_layers() == 2, "two layers");
+    Tensor gen;
+    m.generate(kPrompts, gen);
+    expect(gen.ndim() == 2 && gen.size(0) == kPrompts.size() && gen.size(1) == head.weight().size(0),
+           "generate logits shape");
+    write_raw(dir, "gen_logits", gen);
+    Tensor fwd;
+    m.forward(kPrompts[0], fwd, true);
+    expect(fwd.ndim() == 2 && fwd.size(0) == 1, "forward logits shape");
+    write_raw(dir, "fwd_logits", fwd);
+    Tensor dec;
+    std::vector<std::vector<int>> ids;
+    m.generate_decode({kPrompts[2]}, 3, dec, ids);
+    expect(dec.size(0) == 1 && dec.size(1) == 3 && ids.size() == 1 && ids[0].size() == 3, "decode shapes");
+    write_raw(dir, "dec_logits", dec);
+    Tensor idt({3});
+    for (std::size_t i = 0; i < 3; ++i) idt.at(i) = static_cast<float>(ids[0][i]);
+    write_raw(dir, "dec_ids", idt);
+    expect_throw<std::runtime_error>([&] { Tensor l; m.generate({}, l); }, "generate received an empty input batch",
+                                     "generate: empty batch");
+    expect_throw<std::invalid_argument>([&] { Tensor l; m.forward({}, l, true); }, "empty input", "forward: empty");
+    expect_throw<std::invalid_argument>([&] { Tensor l; m.forward({1, 32064}, l, true); }, "token out of vocabulary",
+                                        "forward: token range");
+    expect_throw<std::invalid_argument>([&] { Tensor l; m.forward({1}, l, false); }, nullptr, "forward: CPU path");
+    expect_throw<std::runtime_error>([&] { Tensor l; std::vector<std::vector<int>> g; m.generate_decode({}, 2, l, g); },
+                                     "generate_decode received an empty input batch", "decode: empty batch");
+    expect_throw<std::invalid_argument>(
+        [&] { Tensor l; std::vector<std::vector<int>> g; m.generate_decode({{1}}, 0, l, g); },
+        "max_new_tokens must be positive", "decode: zero tokens");
+
+    // the decoder layer's forward() on the packed prompts (no trie)
+    {
+        std::vector<std::size_t> lens, rows;
+        for (const auto& p : kPrompts) {
+            lens.push_back(p.size());
+            for (int t : p) rows.push_back(static_cast<std::size_t>(t));
+        }
+        const Tensor emb = loader.load("model.embed_tokens.weight");
+        Tensor h({rows.size(), emb.size(1)});
+        tensor_ops::gather_rows_gpu(emb, rows, h);
+        const PhiDecoderLayer l0(loader, 0), l1(loader, 1);
+        Tensor a, b;
+        l0.forward(h, a, lens, true);
+        l1.forward(a, b, lens, true);
+        write_raw(dir, "packed_layers", b);
+        std::vector<std::size_t> bad = lens;
+        bad.back() += 1;
+        expect_throw<std::invalid_argument>([&] { Tensor c; l0.forward(h, c, bad, true); }, "packed sequence lengths",
+                                            "packed lengths must cover the rows");
+    }
+
+    // elementwise ops and the paired projections
+    {
+        Rng rng(77);
+        const std::size_t n = 6, c = 40;
+        Tensor a = random_tensor({n, c}, rng, 1.0f), b = random_tensor({n, c}, rng, 1.0f);
+        Tensor bias = random_tensor({c}, rng, 1.0f);
+        write_raw(dir, "ew_a", a);
+        write_raw(dir, "ew_b", b);
+        write_raw(dir, "ew_bias", bias);
+        Tensor s = a;
+        tensor_ops::add_inplace_gpu(s, b);
+        write_raw(dir, "ew_add", s);
+        Tensor t = a;
+        tensor_ops::add_bias_inplace_gpu(t, bias);
+        write_raw(dir, "ew_add_bias", t);
+        Tensor u({n, c});
+        tensor_ops::silu_mul_gpu(a, b, u);
+        write_raw(dir, "ew_silu_mul", u);
+        Tensor z = a;
+        tensor_ops::zero_gpu(z);
+        bool zero = true;
+        for (std::size_t i = 0; i < z.size(); ++i) zero = zero && z[i] == 0.0f;
+        expect(zero, "zero_gpu");
+        Tensor wrong({n, c + 1});
+        expect_throw<std::invalid_argument>([&] { tensor_ops::add_inplace_gpu(s, wrong); }, "add shape", "add shape");
+        expect_throw<std::invalid_argument>([&] { tensor_ops::add_bias_inplace_gpu(s, b); }, "bias shape", "bias shape");
+        expect_throw<std::invalid_argument>([&] { tensor_ops::silu_mul_gpu(a, wrong, u); }, "silu_mul shape",
+                                            "silu_mul shape");
+        // matmul_pair_silu_gpu / matmul_pair_bias_gpu on the layer-0 expert 0 and k/v weights
+        const std::string e0 = "model.layers.0.block_sparse_moe.experts.0.";
+        const Tensor w1 = loader.load(e0 + "w1.weight"), w3 = loader.load(e0 + "w3.weight");
+        const Tensor xin = random_tensor({n, w1.size(1)}, rng, 1.0f);
+        write_raw(dir, "pair_x", xin);
+        Tensor ps({n, w1.size(0)});
+        tensor_ops::matmul_pair_silu_gpu(xin, w1, w3, ps);
+        write_raw(dir, "pair_silu", ps);
+        const Tensor kw = loader.load("model.layers.0.self_attn.k_proj.weight");
+        const Tensor kb = loader.load("model.layers.0.self_attn.k_proj.bias");
+        const Tensor vw = loader.load("model.layers.0.self_attn.v_proj.weight");
+        const Tensor vb = loader.load("model.layers.0.self_attn.v_proj.bias");
+        Tensor ko({n, kw.size(0)}), vo({n, vw.size(0)});
+        tensor_ops::matmul_pair_bias_gpu(xin, kw, kb, ko, vw, vb, vo);
+        write_raw(dir, "pair_k", ko);
+        write_raw(dir, "pair_v", vo);
+        Tensor bad({n, w1.size(0) + 4});
+        expect_throw<std::invalid_argument>([&] { tensor_ops::matmul_pair_silu_gpu(xin, w1, w3, bad); },
+                                            "matmul_pair_silu_gpu shape", "pair silu shape");
+        expect_throw<std::invalid_argument>([&] { tensor_ops::matmul_pair_bias_gpu(xin, kw, kb, bad, vw, vb, vo); },
+                                            "matmul_pair_bias_gpu shape", "pair bias shape");
+    }
+    std::printf("layer_check (model): %d failure(s)\n", g_failures);
+    return g_failures ? 1 : 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
-    if (argc != 2 && argc != 3) {
-        std::fprintf(stderr, "usage: %s <out_dir> [<model.bin>]\n", argv[0]);
+    if (argc < 2 || argc > 4) {
+        std::fprintf(stderr, "usage: %s <out_dir> [<model.bin> [model]]\n", argv[0]);
         return 2;
     }
     const std::string dir = argv[1];
+    if (argc == 4) return model_check(dir, argv[2]);
     if (argc == 3) return loader_check(dir, argv[2]);
     const std::size_t T = 96, H = 512, F = 128, E = apss26::NUM_EXPERTS;
     Rng rng(20260);
@@ -299,7 +433,30 @@ int main(int argc, char** argv) {
         u.at(0, 0) = 7.0f;
         expect(t.at(0, 0) == 5.0f, "copies are independent");
         expect_throw<std::out_of_range>([&] { (void)t.at(4, 0); }, "Tensor index", "at() bounds");
+        expect_throw<std::invalid_argument>([&] { (void)t.at(1); }, "Tensor rank mismatch", "at() rank");
+        expect_throw<std::out_of_range>([&] { (void)t.size(2); }, "Tensor dimension", "size(dim) bounds");
         expect_throw<std::invalid_argument>([&] { t.reshape({5, 7}); }, "reshape changes tensor size", "reshape");
+        // a device-resident tensor copies on the device and stays independent
+        Tensor dv({4, 8});
+        float* dw = dv.cuda_data_write();
+        std::vector<float> ramp(32);
+        for (int i = 0; i < 32; ++i) ramp[i] = static_cast<float>(i);
+        expect(hipMemcpy(dw, ramp.data(), sizeof(float) * 32, hipMemcpyHostToDevice) == hipSuccess, "ramp upload");
+        Tensor dc = dv;
+        Tensor moved = std::move(dc);
+        dv.at(1, 1) = -1.0f;
+        expect(moved.at(1, 1) == 9.0f && moved.at(3, 7) == 31.0f, "device copy then move keeps the values");
+        expect(dv.at(1, 1) == -1.0f && dv.at(3, 7) == 31.0f, "source keeps its own values");
+        // a fresh tensor reads as zeros on both sides
+        Tensor fresh({3, 5});
+        const float* fz = fresh.cuda_data();
+        float probe = 1.0f;
+        expect(hipMemcpy(&probe, fz + 14, sizeof(float), hipMemcpyDeviceToHost) == hipSuccess && probe == 0.0f,
+               "fresh tensor uploads zeros");
+        expect(fresh.at(2, 4) == 0.0f, "fresh tensor reads zeros on the host");
+        Tensor assigned({1});
+        assigned = dv;
+        expect(assigned.shape() == dv.shape() && assigned.at(3, 7) == 31.0f, "copy assignment");
     }
 
     // --- the reference's exceptions -------------------------------------------

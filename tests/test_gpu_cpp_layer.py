@@ -166,3 +166,119 @@ def test_tree_attention_ops_bit_exact(run):
     assert np.array_equal(ld("attn_kr", 512).view(np.uint32), kr.view(np.uint32))
     want = oracle.attention_tree(qr, kr, v, plan.node_depth, plan.node_anc, plan.max_len, 16, 4, 128)
     assert np.array_equal(ld("attn_out", 2048).view(np.uint32), want.view(np.uint32))
+
+
+# The model mode of the check program: a two-layer model (hidden 512, 16
+# experts of 128, vocabulary 96, the reference's 16 query / 4 KV heads of
+# 128) written as a model.bin, built from PhiDecoderLayer(loader, i) parts.
+PROMPTS = [[5, 6, 7, 8, 9, 10], [5, 6, 7, 1, 2], [3, 4], [5, 6, 7, 8, 11], [5, 6, 7], [9]]
+MH, MF, MV = 512, 128, 96
+
+
+def small_model_weights(seed=31):
+    rng = np.random.default_rng(seed)
+    nrm = lambda shape, s: (s * rng.standard_normal(shape)).astype(np.float32)
+    W = {"model.embed_tokens.weight": nrm((MV, MH), 1.0), "model.norm.weight": nrm(MH, 1.0) + 1.0,
+         "model.norm.bias": nrm(MH, 0.1), "lm_head.weight": nrm((MV, MH), 0.05), "lm_head.bias": nrm(MV, 0.1)}
+    for i in range(2):
+        p = f"model.layers.{i}."
+        for nm in ("input_layernorm", "post_attention_layernorm"):
+            W[p + nm + ".weight"] = nrm(MH, 0.2) + 1.0
+            W[p + nm + ".bias"] = nrm(MH, 0.1)
+        for nm, (o, k) in (("q_proj", (2048, MH)), ("k_proj", (512, MH)), ("v_proj", (512, MH)),
+                           ("o_proj", (MH, 2048))):
+            W[p + f"self_attn.{nm}.weight"] = nrm((o, k), 0.05)
+            W[p + f"self_attn.{nm}.bias"] = nrm(o, 0.05)
+        m = p + "block_sparse_moe."
+        W[m + "gate.weight"] = nrm((E, MH), 0.05)
+        for e in range(E):
+            W[m + f"experts.{e}.w1.weight"] = nrm((MF, MH), 0.05)
+            W[m + f"experts.{e}.w3.weight"] = nrm((MF, MH), 0.05)
+            W[m + f"experts.{e}.w2.weight"] = nrm((MH, MF), 0.05)
+    return W
+
+
+@pytest.fixture(scope="module")
+def model_run(tmp_path_factory, gpu_device):
+    from aps2026_amd.model_loader import write_model_bin
+    out = tmp_path_factory.mktemp("model_check")
+    W = small_model_weights()
+    write_model_bin(str(out / "model.bin"), W)
+    print(f"running {BIN} (model mode)", flush=True)
+    res = subprocess.run([BIN, str(out), str(out / "model.bin"), "model"], capture_output=True, text=True,
+                         timeout=120)
+    assert res.returncode == 0, f"layer_check failed:\n{res.stdout}\n{res.stderr}"
+    return W, out
+
+
+def _ld(d, name, shape):
+    return np.fromfile(d / f"{name}.f32", dtype=np.float32).reshape(shape)
+
+
+def test_model_generate_two_layers_bit_exact(model_run):
+    """PhiTinyMoEModel::generate (trie, node-row gather, two forward_carry
+    layers with the carried residual, final add+LayerNorm, last-row gather,
+    LM head with bias) equals the oracle chain bit for bit."""
+    from tests import model_chain
+    W, d = model_run
+    want = model_chain.generate(W, PROMPTS, 2)
+    got = _ld(d, "gen_logits", (len(PROMPTS), MV))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_model_forward_and_decoder_forward_packed_bit_exact(model_run):
+    """The packed (non-trie) path: PhiTinyMoEModel::forward on one prompt
+    and PhiDecoderLayer::forward on the packed batch (positions restart per
+    prompt, keys stay inside it, output = MoE + residual) equal the oracle."""
+    from tests import model_chain
+    W, d = model_run
+    want = model_chain.forward(W, PROMPTS[0], 2)
+    assert np.array_equal(_ld(d, "fwd_logits", (1, MV)).view(np.uint32), want.view(np.uint32))
+    # two decoder layers on the packed prompts
+    lens = [len(p) for p in PROMPTS]
+    pos, chains = model_chain.packed_chains(lens)
+    row_pos, anc, stride = model_chain.chain_table(pos, chains)
+    h = oracle.gather_rows(W["model.embed_tokens.weight"], [t for p in PROMPTS for t in p])
+    for i in range(2):
+        ff, res = model_chain.layer_carry(h, None, model_chain.layer_weights(W, i), row_pos, anc, stride)
+        h = (ff + res).astype(np.float32)
+    got = _ld(d, "packed_layers", h.shape)
+    assert np.array_equal(got.view(np.uint32), h.view(np.uint32))
+
+
+def test_model_generate_decode_greedy(model_run):
+    """generate_decode: three greedy steps from the third prompt; every
+    step's logits equal the oracle forward of the growing prefix and the
+    chosen ids are its first maxima."""
+    from tests import model_chain
+    W, d = model_run
+    ids = _ld(d, "dec_ids", (3,)).astype(np.int64).tolist()
+    logits = _ld(d, "dec_logits", (1, 3, MV))
+    prefix = list(PROMPTS[2])
+    for step in range(3):
+        want = model_chain.forward(W, prefix, 2)[0]
+        assert np.array_equal(logits[0, step].view(np.uint32), want.view(np.uint32)), step
+        assert ids[step] == int(np.argmax(want))
+        prefix.append(ids[step])
+
+
+def test_elementwise_and_paired_ops_bit_exact(model_run):
+    """add_inplace_gpu, add_bias_inplace_gpu, silu_mul_gpu (exp in double),
+    matmul_pair_silu_gpu and matmul_pair_bias_gpu through the C++ API equal
+    the reference's per-element arithmetic."""
+    W, d = model_run
+    a, b, bias = _ld(d, "ew_a", (6, 40)), _ld(d, "ew_b", (6, 40)), _ld(d, "ew_bias", (40,))
+    assert np.array_equal(_ld(d, "ew_add", (6, 40)).view(np.uint32), (a + b).view(np.uint32))
+    assert np.array_equal(_ld(d, "ew_add_bias", (6, 40)).view(np.uint32), (a + bias).view(np.uint32))
+    e = np.exp(-a.astype(np.float64)).astype(np.float32)
+    silu = ((a / (np.float32(1) + e)).astype(np.float32) * b).astype(np.float32)
+    assert np.array_equal(_ld(d, "ew_silu_mul", (6, 40)).view(np.uint32), silu.view(np.uint32))
+    x = _ld(d, "pair_x", (6, MH))
+    e0 = "model.layers.0.block_sparse_moe.experts.0."
+    want = oracle.ffn_rows(x, np.zeros(6, np.int32), W[e0 + "w1.weight"][None], W[e0 + "w3.weight"][None],
+                           np.zeros((1, MH, MF), np.float32), want_act=True)[1]
+    assert np.array_equal(_ld(d, "pair_silu", (6, MF)).view(np.uint32), want.view(np.uint32))
+    for nm in ("k", "v"):
+        p = f"model.layers.0.self_attn.{nm}_proj."
+        ref = oracle.linear(x, W[p + "weight"], W[p + "bias"])
+        assert np.array_equal(_ld(d, f"pair_{nm}", (6, 512)).view(np.uint32), ref.view(np.uint32))
