@@ -113,6 +113,9 @@ def lib():
     L.aps_add_bias_inplace.argtypes = [_c_vp, _c_vp, i64, i32, _c_vp]
     L.aps_silu_mul.argtypes = [_c_vp, _c_vp, _c_vp, i64, _c_vp]
     L.aps_zero.argtypes = [_c_vp, i64, _c_vp]
+    L.aps_moe_forward_noalloc.argtypes = [u64, _c_vp, i32, _c_vp, i64, _c_vp, i32, _c_vp]
+    L.aps_moe_noalloc_scratch_bytes.argtypes = []
+    L.aps_moe_noalloc_scratch_bytes.restype = sz
     L.aps_prefix_dedup.argtypes = [_c_vp, _c_vp, i64, i64, i64, _c_vp, _c_vp, _c_vp, _c_vp, i64,
                                    ctypes.POINTER(i64)]
     for name in ("aps_moe_weights_register", "aps_moe_weights_release", "aps_moe_workspace_layout",
@@ -121,7 +124,8 @@ def lib():
                  "aps_moe_ffn_down", "aps_mlp_forward", "aps_quantise_rows_e4m3", "aps_moe_ffn_up_fp8",
                  "aps_moe_ffn_down_fp8", "aps_layer_norm", "aps_add_layer_norm", "aps_gather_rows",
                  "aps_prefix_dedup", "aps_linear", "aps_rope_table", "aps_rope_tree", "aps_attention_tree",
-                 "aps_attention_packed", "aps_add_inplace", "aps_add_bias_inplace", "aps_silu_mul", "aps_zero"):
+                 "aps_attention_packed", "aps_add_inplace", "aps_add_bias_inplace", "aps_silu_mul", "aps_zero",
+                 "aps_moe_forward_noalloc"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

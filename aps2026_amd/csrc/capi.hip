@@ -748,6 +748,58 @@ int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float
     return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, nullptr, rows, out, out_dtype, ws, L, s);
 }
 
+// ---- allocation-free forward --------------------------------------------
+//
+// aps_moe_forward with its workspace in a static device array instead of a
+// caller buffer, for callers that cannot allocate (code under HIP graph
+// capture, serving loops).  Each device holds its own copy of `scratch` for
+// the life of the process; its address is looked up once per device (with
+// that device current) and kept, since the host-side name is not a device
+// address.  The forward path writes every workspace byte it reads, so the
+// previous call's contents never matter; calls that overlap on one device
+// share the array and race.
+namespace {
+
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;  // 64 MiB per device
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+int static_scratch(void** out) {
+    int dev = 0;
+    APS_HIP(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(APS_ERR_ARG, "forward_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        APS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress scratch");
+        if (!p) return fail(APS_ERR_HIP, "hipGetSymbolAddress scratch: null address");
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return APS_OK;
+}
+
+}  // namespace
+
+size_t aps_moe_noalloc_scratch_bytes(void) { return kStaticScratchBytes; }
+
+int aps_moe_forward_noalloc(uint64_t handle, const void* x, int32_t x_dtype, const float* gate, int64_t rows,
+                            void* out, int32_t out_dtype, void* stream) {
+    aps_moe_ws_layout L;
+    if (int rc = aps_moe_workspace_layout(handle, rows, &L)) return rc;
+    if (L.total_bytes > kStaticScratchBytes)
+        return fail(APS_ERR_WORKSPACE,
+                    "forward_noalloc: %lld rows need %zu bytes of scratch, the static scratch holds %zu "
+                    "(use aps_moe_forward with a workspace)",
+                    (long long)rows, L.total_bytes, kStaticScratchBytes);
+    void* ws = nullptr;
+    if (int rc = static_scratch(&ws)) return rc;
+    return aps_moe_forward(handle, x, x_dtype, gate, rows, out, out_dtype, ws, kStaticScratchBytes, stream);
+}
+
 // Dense FFN of a single-expert weight set: offsets {0, rows} and the
 // identity assignment in the workspace, then the two grouped GEMMs with
 // y_perm = out (position p is row p).

@@ -238,6 +238,19 @@ APS_API int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, con
                     int64_t rows, void* out, int32_t out_dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* aps_moe_forward without a workspace argument: the intermediate arrays
+ * live in a static device array of aps_moe_noalloc_scratch_bytes() bytes
+ * (64 MiB, one copy per device, held until the process ends), so the call
+ * allocates nothing -- for callers that cannot allocate: code under HIP
+ * graph capture, serving loops, harnesses that forbid it.  No counterpart
+ * in the reference.  Rows whose aps_moe_workspace_layout total exceeds the
+ * scratch are refused with APS_ERR_WORKSPACE (about 3,500 tokens at hidden
+ * 4096, ffn 448, bf16).  Calls that overlap on one device share the scratch
+ * and race: serialise them (one stream, or events). */
+APS_API int aps_moe_forward_noalloc(uint64_t handle, const void* x, int32_t x_dtype, const float* gate,
+                                    int64_t rows, void* out, int32_t out_dtype, void* stream);
+APS_API size_t aps_moe_noalloc_scratch_bytes(void);
+
 /* ---- dense FFN --------------------------------------------------------- */
 
 /* Workspace bytes of aps_mlp_forward for `rows` rows (0 for a bad handle). */
