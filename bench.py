@@ -2,15 +2,13 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 
-`--config c3` times the decoder layer's post-attention half instead:
-add_layer_norm (attention output += residual stream, LayerNorm with the
-reference kernel's serial sums) feeding the same MoE block, fp32 activations
-with bf16 experts (synthetic attention output; the attention itself is not
-built).  `--config c4` runs C4's 16 prompts x 1024 ids, folded by the prompt prefix
-trie (host code) into 10,240 rows, through the embedding gather and the
-whole first decoder layer (input LayerNorm, fp32 q/k/v projections, RoPE,
-tree attention, o projection, add_layer_norm, MoE block) per step; its value
-counts prompt tokens.
+`--config c3` times one whole decoder layer (input LayerNorm, fp32 q/k/v
+projections, RoPE, tree attention, o projection, residual add+LayerNorm, bf16
+MoE block) on the 4096 prefix-trie rows of 8 prompts x 512 ids, chaining
+forward_carry through 4 random-init layers.  `--config c4` times the whole
+32-layer model's prefill (generate) on C4's 16 prompts x 1024 ids: host
+prefix trie, 10,240 node rows through 32 layers, final norm, last rows, LM
+head; its value counts prompt tokens.  Both report one layer's stages.
 `--config load` times reading one MoE layer from a model.bin into HBM.
 
 One step = one full MoE block (router GEMM, quantised top-2, dispatch,
@@ -69,7 +67,8 @@ FETCH_SCALE, WRITE_SCALE = 262144.0 / 131088.5, 1.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 200; 20 for --config c3, 3 for c4)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--settle", type=float, default=0.5,
                     help="seconds of untimed steps before the warm-up steps: the GPU raises its clocks over the "
@@ -82,7 +81,10 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true",
                     help="run one 256 MiB device-to-device copy before the steps (scale reference for the "
                          "FETCH_SIZE / WRITE_SIZE counter passes)")
-    return ap.parse_args()
+    args = ap.parse_args()
+    if args.steps is None:
+        args.steps = {"c3": 20, "c4": 3}.get(args.config, 200)
+    return args
 
 
 def load_bench(args):
@@ -161,6 +163,167 @@ def load_bench(args):
     }), flush=True)
 
 
+def decoder_bench(args):
+    """--config c3: one whole decoder layer (input LayerNorm, fp32 q/k/v
+    projections with bias, RoPE, GQA-4 tree attention, o projection, residual
+    add + LayerNorm, bf16 MoE block) on the 4096 prefix-trie rows of 8
+    prompts x 512 random ids; steps chain forward_carry through LAYERS
+    random-init layers in turn (each step's input is the previous step's
+    output and carried residual), as consecutive layers of a prefill.
+    --config c4: the whole 32-layer model's prefill (PhiTinyMoEModel::generate)
+    on C4's 16 prompts x 1024 ids: per step the host prefix trie and its
+    upload, the embedding gather of the 10,240 node rows, 32 layers, the
+    final add+LayerNorm, the last-row gather and the LM head (vocab 32064)."""
+    import torch
+    from aps2026_amd import capi, decoder, synth
+    from aps2026_amd.moe import NORM_EPS
+
+    dev = torch.device("cuda:0")
+    H, F, E, V = 4096, 448, 16, 32064
+    c4 = args.config == "c4"
+    g = torch.Generator(device=dev).manual_seed(11)
+    stream = torch.cuda.current_stream(dev)
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    L = capi.lib()
+    if c4:
+        prompts = synth.c4_prompts()
+        nl = 32
+        lws = [decoder.random_layer(H, F, E, dev, g) for _ in range(nl)]
+        emb = torch.randn((V, H), generator=g, device=dev)
+        head_w = (0.02 * torch.randn((V, H), generator=g, device=dev)).contiguous()
+        head_b = (0.02 * torch.randn(V, generator=g, device=dev)).contiguous()
+        model = decoder.Model(emb, torch.ones(H, device=dev), torch.zeros(H, device=dev), head_w, head_b, lws)
+        plan = decoder.RowPlan.from_prompts(prompts, dev)
+        T, tokens = plan.rows, plan.prompt_tokens
+
+        def step(i):
+            p = decoder.RowPlan.from_prompts(prompts, dev)  # the host trie and its upload, as generate() does
+            model.prefill(p)
+        layer0, bufs = model.layers[0], model.buffers(T)
+    else:
+        rng = np.random.default_rng(7)
+        prompts = [rng.integers(0, V, 512).tolist() for _ in range(8)]
+        plan = decoder.RowPlan.from_prompts(prompts, dev)
+        T = tokens = plan.rows
+        lws = [decoder.random_layer(H, F, E, dev, g) for _ in range(LAYERS)]
+        layers = [decoder.DecoderLayer(w) for w in lws]
+        bufs = decoder.Buffers.allocate(T, H, lws[0].moe, dev)
+        bufs.x.copy_(torch.randn((T, H), generator=g, device=dev))
+        bufs.carry.zero_()
+        layer0 = layers[0]
+
+        def step(i):
+            layers[i % LAYERS].forward_carry(bufs, plan, True, sptr)
+    torch.cuda.synchronize()
+
+    t_settle = time.perf_counter()
+    n_settle = 0
+    while time.perf_counter() - t_settle < args.settle:
+        step(n_settle)
+        n_settle += 1
+        torch.cuda.synchronize()
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+
+    # ---- one layer's stages with HIP events on the launch stream ----------
+    def p(t):
+        return ctypes.c_void_p(t.data_ptr())
+    w = layer0.w
+    eps = ctypes.c_float(NORM_EPS)
+    cos_d, sin_d = decoder._device_table(dev, plan.max_len, 128, decoder.ROPE_THETA)
+    lin = lambda src, nm, dst, k, n: L.aps_linear(p(src), p(w.proj[nm][0]), p(w.proj[nm][1]), T, k, n, p(dst), sptr)
+    calls = [
+        ("input_layer_norm", lambda: L.aps_add_layer_norm(p(bufs.x), p(bufs.carry), p(w.in_w), p(w.in_b), T, H, eps,
+                                                           p(bufs.normed), sptr)),
+        ("qkv_proj", lambda: lin(bufs.normed, "q_proj", bufs.q, H, 2048) or lin(bufs.normed, "k_proj", bufs.k, H, 512)
+         or lin(bufs.normed, "v_proj", bufs.v, H, 512)),
+        ("rope", lambda: L.aps_rope_tree(p(bufs.q), p(bufs.k), p(plan.pos), T, 16, 4, 128, p(cos_d), p(sin_d),
+                                         cos_d.shape[0], sptr)),
+        ("attention_tree", lambda: L.aps_attention_tree(p(bufs.q), p(bufs.k), p(bufs.v), p(bufs.att), p(plan.pos),
+                                                        p(plan.anc), plan.max_len, T, 16, 4, 128,
+                                                        decoder.SLIDING_WINDOW, sptr)),
+        ("o_proj", lambda: lin(bufs.att, "o_proj", bufs.carry, 2048, H)),
+        ("add_layer_norm", lambda: L.aps_add_layer_norm(p(bufs.carry), p(bufs.x), p(w.post_w), p(w.post_b), T, H,
+                                                         eps, p(bufs.post), sptr)),
+        ("moe_block", lambda: L.aps_moe_forward(w.moe.handle, p(bufs.post), capi.DTYPE_F32, p(w.gate), T, p(bufs.x),
+                                                capi.DTYPE_F32, p(bufs.ws), bufs.ws.numel(), sptr)),
+    ]
+    times = {nm: [] for nm, _ in calls}
+    for i in range(12):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(calls) + 1)]
+        ev[0].record(stream)
+        for k, (nm, c) in enumerate(calls):
+            rc = c()
+            if rc:
+                raise RuntimeError(f"{nm}: {capi.last_error()}")
+            ev[k + 1].record(stream)
+        torch.cuda.synchronize()
+        if i >= 2:
+            for k, (nm, _) in enumerate(calls):
+                times[nm].append(ev[k].elapsed_time(ev[k + 1]) * 1e-3)
+    mt = {nm: statistics.mean(v) for nm, v in times.items()}
+    qkv_flops = 2.0 * T * H * (2048 + 512 + 512)
+    o_flops = 2.0 * T * 2048 * H
+    windows = plan.pos.cpu().numpy().astype(np.int64) + 1
+    attn_flops = float(np.minimum(windows, decoder.SLIDING_WINDOW).sum()) * 16 * 128 * 4
+    stages = {
+        "input_layer_norm": {"us": mt["input_layer_norm"] * 1e6,
+                             "GB_s": 4.0 * T * H * 4 / mt["input_layer_norm"] / 1e9},
+        "qkv_proj": {"us": mt["qkv_proj"] * 1e6, "TFLOP_s": qkv_flops / mt["qkv_proj"] / 1e12},
+        "rope": {"us": mt["rope"] * 1e6},
+        "attention_tree": {"us": mt["attention_tree"] * 1e6, "TFLOP_s": attn_flops / mt["attention_tree"] / 1e12},
+        "o_proj": {"us": mt["o_proj"] * 1e6, "TFLOP_s": o_flops / mt["o_proj"] / 1e12},
+        "add_layer_norm": {"us": mt["add_layer_norm"] * 1e6, "GB_s": 4.0 * T * H * 4 / mt["add_layer_norm"] / 1e9},
+        "moe_block": {"us": mt["moe_block"] * 1e6},
+        "layer_total_us": sum(mt.values()) * 1e6,
+    }
+    if c4:
+        t_plan = []
+        for _ in range(5):
+            t1 = time.perf_counter()
+            decoder.RowPlan.from_prompts(prompts, dev)
+            torch.cuda.synchronize()
+            t_plan.append(time.perf_counter() - t1)
+        stages["prefix_trie_and_upload_ms"] = statistics.median(t_plan) * 1e3
+    # the projections dominate: one fp32 FMA chain per output (the reference's
+    # order), on the VALU; MI355X's published fp32 rate is 157.3 TFLOP/s
+    proj_s = mt["qkv_proj"] + mt["o_proj"]
+    roofline = {"bound": "valu", "kernel": "k_linear_f32 (q/k/v/o projections)",
+                "achieved": (qkv_flops + o_flops) / proj_s / 1e12, "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
+                "frac": (qkv_flops + o_flops) / proj_s / PEAK_F32, "traffic": None,
+                "flops_per_launch": (qkv_flops + o_flops) / 4, "launch_us": proj_s / 4 * 1e6}
+    workload = (f"c4: whole 32-layer random-init model prefill (generate): 16 prompts x 1024 ids, groups of 4 "
+                f"sharing a 512-id prefix, host prefix trie + upload, embedding gather of {T} node rows, 32 "
+                f"decoder layers (LayerNorm+bias, fp32 q/k/v/o projections with bias, 16/4 heads of 128, RoPE, "
+                f"GQA tree attention, bf16 MoE: hidden {H}, {E} experts top-2, ffn {F}), final add+LayerNorm, "
+                f"last-row gather, LM head (vocab {V}); value counts the {tokens} prompt tokens"
+                if c4 else
+                f"c3: one whole decoder layer on the {T} prefix-trie rows of 8 prompts x 512 random ids "
+                f"(LayerNorm+bias, fp32 q/k/v/o projections with bias, 16/4 heads of 128, RoPE, GQA tree "
+                f"attention, residual add+LayerNorm, bf16 MoE: hidden {H}, {E} experts top-2, ffn {F}); steps "
+                f"chain forward_carry through {LAYERS} random-init layers")
+    line = {
+        "metric": "whole-model prefill tokens/s" if c4 else "decoder-layer prefill tokens/s",
+        "value": tokens * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "settle_steps": n_settle, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32 attention, bf16 experts",
+        "data": "synthetic (seeded torch normals, random-init weights)",
+        "config": {"workload": workload, "tokens": tokens, "rows": T, "hidden": H, "experts": E, "ffn": F,
+                   "layers": 32 if c4 else LAYERS},
+        "roofline": roofline, "cpu_baseline": None, "stages": stages,
+    }
+    print(json.dumps(line), flush=True)
+    for lw in lws:
+        lw.release()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -170,27 +333,16 @@ def main():
     if args.config == "load":
         load_bench(args)
         return
+    if args.config in ("c3", "c4"):
+        decoder_bench(args)
+        return
 
     import torch
     from aps2026_amd import capi, moe, synth
 
     dev = torch.device("cuda:0")
-    c3 = args.config in ("c3", "c4")   # the decoder's post-attention half (c4: on deduplicated rows)
-    c4 = args.config == "c4"
-    inp = synth.make_config("c2" if c3 else args.config)
+    inp = synth.make_config(args.config)
     T, H, E, F = inp.T, inp.H, inp.E, inp.F
-    if c4:
-        # C4's prompt batch through the prefix trie (host code, the reference's
-        # CPU-side step): the layer's rows are the trie nodes
-        from aps2026_amd import prefix
-        prompts = synth.c4_prompts()
-        dedup_s = []
-        for _ in range(5):
-            t0 = time.perf_counter()
-            plan = prefix.prefix_dedup(prompts)
-            dedup_s.append(time.perf_counter() - t0)
-        prompt_tokens = int(plan.token_node.shape[0])
-        T = plan.nodes
     A = 2 * T
     fp8 = inp.dtype == "fp8"
     bf16 = inp.dtype in ("bf16", "fp8")        # x and outputs are bf16 on both MFMA paths
@@ -199,39 +351,7 @@ def main():
     def dev_bits(bits):
         return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(dev).view(torch.bfloat16)
 
-    if c3:
-        # residual stream and attention output, fp32 (the reference's activations)
-        g = torch.Generator(device="cpu").manual_seed(3)
-        resid = (0.5 * torch.randn(T, H, generator=g)).to(dev)
-        attn = (0.5 * torch.randn(T, H, generator=g)).to(dev)
-        ln_w = (1.0 + 0.05 * torch.randn(H, generator=g)).to(dev)
-        ln_b = (0.05 * torch.randn(H, generator=g)).to(dev)
-        x = torch.empty(T, H, dtype=torch.float32, device=dev)  # post-attention LayerNorm output
-        if c4:
-            # embedding table on the device; the node rows are gathered from it
-            # every step (the residual stream the first layer adds to)
-            gd = torch.Generator(device=dev).manual_seed(4)
-            emb = torch.randn((prefix.VOCAB_SIZE, H), generator=gd, device=dev)
-            node_rows = prefix.RowIndexBuffer(plan.node_token, dev)
-            # the attention half of the first decoder layer: input LayerNorm,
-            # q/k/v projections (16 query / 4 KV heads of 128, with bias),
-            # RoPE, tree attention, o projection; random-init weights
-            from aps2026_amd import attention
-            normed = torch.empty((T, H), dtype=torch.float32, device=dev)
-            qa = torch.empty((T, 16 * 128), dtype=torch.float32, device=dev)
-            ka = torch.empty((T, 4 * 128), dtype=torch.float32, device=dev)
-            va = torch.empty((T, 4 * 128), dtype=torch.float32, device=dev)
-            oa = torch.empty((T, 16 * 128), dtype=torch.float32, device=dev)
-            proj = {nm: ((0.02 * torch.randn((o, i), generator=gd, device=dev)).contiguous(),
-                         (0.02 * torch.randn(o, generator=gd, device=dev)).contiguous())
-                    for nm, (o, i) in (("q", (2048, H)), ("k", (512, H)), ("v", (512, H)), ("o", (H, 2048)))}
-            proj_flops = 2.0 * T * H * (2048 + 512 + 512) + 2.0 * T * 2048 * H
-            pos_d = attention._rows_u32(plan.node_depth, dev)
-            anc_d = attention._rows_u32(plan.node_anc, dev)
-            cos_d, sin_d = attention._device_table(dev, plan.max_len, 128, attention.ROPE_THETA)
-            windows = np.minimum(plan.node_depth.astype(np.int64) + 1, attention.SLIDING_WINDOW)
-            attn_flops = float(windows.sum()) * 16 * 128 * 4   # scores and values, 2 FLOP per FMA
-    elif bf16:
+    if bf16:
         x = dev_bits(inp.packed["x_bf16"])
     else:
         x = torch.from_numpy(inp.x).to(dev)
@@ -270,54 +390,10 @@ def main():
     stream = torch.cuda.current_stream(dev)
     sptr = ctypes.c_void_p(stream.cuda_stream)
     xd = capi.DTYPE_BF16 if bf16 else capi.DTYPE_F32
-    if c3:
-        out = torch.empty((T, H), dtype=torch.float32, device=dev)
-        xd = capi.DTYPE_F32
     args_fwd = [(w.handle, ctypes.c_void_p(x.data_ptr()), xd, ctypes.c_void_p(gate.data_ptr()), T,
                  ctypes.c_void_p(out.data_ptr()), xd, ctypes.c_void_p(ws.data_ptr()), ws.numel(), sptr)
                 for w in layers]
-    if c3:
-        args_ln = (ctypes.c_void_p(attn.data_ptr()), ctypes.c_void_p(resid.data_ptr()),
-                   ctypes.c_void_p(ln_w.data_ptr()), ctypes.c_void_p(ln_b.data_ptr()), T, H,
-                   ctypes.c_float(moe.NORM_EPS), ctypes.c_void_p(x.data_ptr()), sptr)
-
-    if c4:
-        args_gather = (ctypes.c_void_p(emb.data_ptr()), emb.shape[0], H, ctypes.c_void_p(node_rows.data.data_ptr()),
-                       T, ctypes.c_void_p(resid.data_ptr()), sptr)
-        def lin(src, nm, dst, k_in, n_out):
-            return (ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(proj[nm][0].data_ptr()),
-                    ctypes.c_void_p(proj[nm][1].data_ptr()), T, k_in, n_out, ctypes.c_void_p(dst.data_ptr()), sptr)
-        args_lnin = (ctypes.c_void_p(resid.data_ptr()), ctypes.c_void_p(ln_w.data_ptr()),
-                     ctypes.c_void_p(ln_b.data_ptr()), T, H, ctypes.c_float(moe.NORM_EPS),
-                     ctypes.c_void_p(normed.data_ptr()), sptr)
-        args_qkv = (lin(normed, "q", qa, H, 2048), lin(normed, "k", ka, H, 512), lin(normed, "v", va, H, 512))
-        args_o = lin(oa, "o", attn, 2048, H)
-
-        def qkv():
-            for a in args_qkv:
-                rc = L.aps_linear(*a)
-                if rc:
-                    return rc
-            return 0
-        args_rope = (ctypes.c_void_p(qa.data_ptr()), ctypes.c_void_p(ka.data_ptr()), ctypes.c_void_p(pos_d.data_ptr()),
-                     T, 16, 4, 128, ctypes.c_void_p(cos_d.data_ptr()), ctypes.c_void_p(sin_d.data_ptr()),
-                     cos_d.shape[0], sptr)
-        args_attn = (ctypes.c_void_p(qa.data_ptr()), ctypes.c_void_p(ka.data_ptr()), ctypes.c_void_p(va.data_ptr()),
-                     ctypes.c_void_p(oa.data_ptr()), ctypes.c_void_p(pos_d.data_ptr()),
-                     ctypes.c_void_p(anc_d.data_ptr()), plan.max_len, T, 16, 4, 128, attention.SLIDING_WINDOW, sptr)
-
     def step(i):
-        if c4:
-            for fn in (lambda: L.aps_gather_rows(*args_gather), lambda: L.aps_layer_norm(*args_lnin), qkv,
-                       lambda: L.aps_rope_tree(*args_rope), lambda: L.aps_attention_tree(*args_attn),
-                       lambda: L.aps_linear(*args_o)):
-                rc = fn()
-                if rc:
-                    raise RuntimeError(capi.last_error())
-        if c3:
-            rc = L.aps_add_layer_norm(*args_ln)
-            if rc:
-                raise RuntimeError(capi.last_error())
         rc = L.aps_moe_forward(*args_fwd[i % LAYERS])
         if rc:
             raise RuntimeError(capi.last_error())
@@ -338,8 +414,7 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
-    # c4: prompt tokens served (the trie rows stand for all of them)
-    tokens_per_s = (prompt_tokens if c4 else T) * args.steps / elapsed
+    tokens_per_s = T * args.steps / elapsed
 
     # ---- per-stage timing with HIP events on the launch stream ------------
     def p(t):
@@ -364,22 +439,13 @@ def main():
                   "combine"]
     else:
         stages = ["router_logits", "route_top2", "dispatch", "ffn_up", "ffn_down", "combine"]
-    if c3:
-        stages = (["gather_rows", "input_layer_norm", "qkv_proj", "rope", "attention_tree", "o_proj"] if c4 else []) + \
-            ["add_layer_norm"] + stages
-        L.aps_add_layer_norm(*args_ln)
-        xb = x.to(torch.bfloat16)  # the FFN's bf16 copy of the norm output (the fused path makes its own)
     times = {s: [] for s in stages}
     n_stage = max(args.steps, 10)
     for i in range(n_stage + 2):
         w = layers[i % LAYERS]
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
         ev[0].record(stream)
-        calls = ([lambda: L.aps_gather_rows(*args_gather), lambda: L.aps_layer_norm(*args_lnin), qkv,
-                  lambda: L.aps_rope_tree(*args_rope), lambda: L.aps_attention_tree(*args_attn),
-                  lambda: L.aps_linear(*args_o)] if c4 else [])
-        calls += [lambda: L.aps_add_layer_norm(*args_ln)] if c3 else []
-        calls += [
+        calls = [
             lambda: L.aps_router_logits(p(x), xd, p(gate), T, H, E, p(logits), sptr),
             lambda: L.aps_moe_route_top2(p(logits), T, E, p(routes), sptr),
             lambda: L.aps_moe_dispatch(p(routes), T, E, p(counts), p(offsets), p(arows), p(rpos), p(scratch),
@@ -392,19 +458,12 @@ def main():
                 lambda: L.aps_quantise_rows_e4m3(p(act), F, F, p(actq), kp, p(acts), A, sptr),
                 lambda: L.aps_moe_ffn_down_fp8(w.handle, p(actq), p(acts), T, p(offsets), p(y), sptr),
             ]
-        elif c3:
-            calls += [
-                lambda: L.aps_moe_ffn_up(w.handle, p(xb), capi.DTYPE_BF16, T, p(offsets), p(arows), p(act), None,
-                                         sptr),
-                lambda: L.aps_moe_ffn_down(w.handle, p(act), None, T, p(offsets), p(y), sptr),
-            ]
         else:
             calls += [
                 lambda: L.aps_moe_ffn_up(w.handle, p(x), xd, T, p(offsets), p(arows), p(act), None, sptr),
                 lambda: L.aps_moe_ffn_down(w.handle, p(act), None, T, p(offsets), p(y), sptr),
             ]
-        calls.append(lambda: L.aps_moe_combine(p(y), capi.DTYPE_BF16 if c3 else xd, p(rpos), T, H, p(out),
-                                               capi.DTYPE_F32 if c3 else xd, sptr))
+        calls.append(lambda: L.aps_moe_combine(p(y), xd, p(rpos), T, H, p(out), xd, sptr))
         for k, c in enumerate(calls):
             rc = c()
             if rc:
@@ -416,14 +475,12 @@ def main():
                 times[s].append(ev[k].elapsed_time(ev[k + 1]) * 1e-3)
     mean_t = {s: statistics.mean(v) for s, v in times.items()}
 
-    esz = 2 if bf16 and not c3 else 4
+    esz = 2 if bf16 else 4
     flops_up = 4.0 * A * H * F
     flops_down = 2.0 * A * F * H
     peak = PEAK_FP8 if fp8 else (PEAK_BF16 if bf16 else PEAK_F32)
     bytes_router = T * H * esz + E * H * 4 + T * E * 4
     bytes_combine = A * H * esz + T * H * esz + A * 4
-    if c3:  # bf16 expert outputs in, fp32 block output
-        bytes_combine = A * H * 2 + T * H * 4 + A * 4
     stage_report = {
         "router_logits": {"us": mean_t["router_logits"] * 1e6,
                           "GB_s": bytes_router / mean_t["router_logits"] / 1e9},
@@ -436,27 +493,6 @@ def main():
            if fp8 else {}),
         "grouped_gemm_total_TFLOP_s": (flops_up + flops_down) / (mean_t["ffn_up"] + mean_t["ffn_down"]) / 1e12,
     }
-    if c3:
-        # algorithmic bytes: attention output and residual read, both written (x += r and y)
-        stage_report["add_layer_norm"] = {"us": mean_t["add_layer_norm"] * 1e6,
-                                          "GB_s": 4.0 * T * H * 4 / mean_t["add_layer_norm"] / 1e9}
-    if c4:
-        # gather: node rows read from the embedding table and written, plus the indices
-        stage_report["gather_rows"] = {"us": mean_t["gather_rows"] * 1e6,
-                                       "GB_s": (2.0 * T * H * 4 + T * 4) / mean_t["gather_rows"] / 1e9}
-        stage_report["input_layer_norm"] = {"us": mean_t["input_layer_norm"] * 1e6,
-                                            "GB_s": 2.0 * T * H * 4 / mean_t["input_layer_norm"] / 1e9}
-        qkv_flops = 2.0 * T * H * (2048 + 512 + 512)
-        stage_report["qkv_proj"] = {"us": mean_t["qkv_proj"] * 1e6, "TFLOP_s": qkv_flops / mean_t["qkv_proj"] / 1e12}
-        stage_report["o_proj"] = {"us": mean_t["o_proj"] * 1e6,
-                                  "TFLOP_s": (proj_flops - qkv_flops) / mean_t["o_proj"] / 1e12}
-        stage_report["rope"] = {"us": mean_t["rope"] * 1e6,
-                                "GB_s": 2.0 * T * 20 * 128 * 4 / mean_t["rope"] / 1e9}
-        stage_report["attention_tree"] = {"us": mean_t["attention_tree"] * 1e6,
-                                          "TFLOP_s": attn_flops / mean_t["attention_tree"] / 1e12,
-                                          "flops": attn_flops}
-        stage_report["prefix_dedup_host"] = {"ms": statistics.median(dedup_s) * 1e3, "prompt_tokens": prompt_tokens,
-                                             "nodes": T, "threads": 1}
     achieved = flops_up / mean_t["ffn_up"]
     kname = "k_ffn_up<Fp8Fmt>" if fp8 else ("k_ffn_up<Bf16Fmt>" if bf16 else "k_ffn_up_f32")
     roofline = {"bound": "mfma", "kernel": kname,
@@ -468,7 +504,7 @@ def main():
 
     # ---- CPU baseline: the reference CPU-path algorithm on the host cores ----
     cpu = None
-    if args.cpu_baseline == "auto" and not c3:
+    if args.cpu_baseline == "auto":
         import oracle
         runs = []
         oracle.moe_forward(inp.x[:256], inp.gate, inp.w1, inp.w3, inp.w2)  # warm-up
@@ -488,19 +524,9 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "settle_steps": n_settle, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8" if fp8 else ("bf16" if bf16 else "f32"), "data": "synthetic (seeded PCG64 normals, random-init weights)",
-        "config": {"workload": (f"c4: 16 prompts x 1024 ids (groups of 4 share a 512-id prefix) deduplicated to "
-                                f"{T} prefix-trie rows; per step the embedding gather of those rows and the "
-                                f"first decoder layer on them: input LayerNorm, q/k/v projections (fp32, 16/4 "
-                                f"heads of 128), RoPE, GQA tree attention, o projection, add_layer_norm and the "
-                                f"MoE FFN block (hidden {H}, "
-                                f"{E} experts top-2, ffn {F}, bf16 experts) on them; value counts the "
-                                f"{prompt_tokens} prompt tokens; the trie itself is host code, timed in stages"
-                                if c4 else
-                                f"c3: decoder post-attention half, add_layer_norm (fp32) + MoE FFN block, {T} "
-                                f"tokens, hidden {H}, {E} experts top-2, ffn {F}, bf16 experts" if c3 else
-                                f"{args.config}: MoE FFN block, {T} tokens, hidden {H}, {E} experts top-2, "
+        "config": {"workload": (f"{args.config}: MoE FFN block, {T} tokens, hidden {H}, {E} experts top-2, "
                                 f"ffn {F}, {inp.dtype}" + (", Zipf(1.1) expert loads" if inp.zipf else "")),
-                   "tokens": prompt_tokens if c4 else T, "rows": T, "hidden": H, "experts": E, "ffn": F, "layers_rotated": LAYERS},
+                   "tokens": T, "rows": T, "hidden": H, "experts": E, "ffn": F, "layers_rotated": LAYERS},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "stages": stage_report,
