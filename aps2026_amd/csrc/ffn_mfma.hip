@@ -244,18 +244,14 @@ __device__ inline void mma_frags(const Frags<Fmt>& f, f32x16_t (&acc)[2][4]) {
 // only then issue stage kt's last MFMAs -- the barrier and the first LDS
 // latency of a stage hide behind MFMA work.  The slot freed by that barrier
 // (stage kt's) is refilled with stage kt+3 during stage kt+1's other steps.
-//   rot: the block walks its k stages starting at stage rot (mod KT); the
-// MFMA sums do not depend on the order, and blocks of different XCDs
-// starting at different stages spread their L2 misses over the kernel.
 template <bool TALL, class Fmt>
 __device__ inline void mainloop3(Ring3& ring, const Slots& sl, int KT, int wave, int lane, int aR, int bR,
-                                 f32x16_t (&acc)[2][4], int rot = 0) {
+                                 f32x16_t (&acc)[2][4]) {
     constexpr int kSub = Fmt::kSub;
     static_assert(kSub % 2 == 0, "ping-pong needs an even step count");
-    auto kof = [&](int kt) { const int k = kt + rot; return k >= KT ? k - KT : k; };
-    issue_slots<TALL>(ring.s[0], sl, kof(0), wave, 0, 12);
-    if (KT > 1) issue_slots<TALL>(ring.s[1], sl, kof(1), wave, 0, 12);
-    if (KT > 2) issue_slots<TALL>(ring.s[2], sl, kof(2), wave, 0, 12);
+    issue_slots<TALL>(ring.s[0], sl, 0, wave, 0, 12);
+    if (KT > 1) issue_slots<TALL>(ring.s[1], sl, 1, wave, 0, 12);
+    if (KT > 2) issue_slots<TALL>(ring.s[2], sl, 2, wave, 0, 12);
     if (KT > 2) wait_vm_lgkm0<24>();
     else if (KT > 1) wait_vm_lgkm0<12>();
     else wait_vm_lgkm0<0>();
@@ -272,8 +268,7 @@ __device__ inline void mainloop3(Ring3& ring, const Slots& sl, int KT, int wave,
         for (int s = 0; s + 1 < kSub; ++s) {
             wait_lgkm0();
             load_frags<Fmt>(f[(s + 1) & 1], st, s + 1, lane, aR, bR);
-            if (refill)
-                issue_slots<TALL>(ring.s[prev], sl, kof(kt + 2), wave, 12 * s / (kSub - 1), 12 * (s + 1) / (kSub - 1));
+            if (refill) issue_slots<TALL>(ring.s[prev], sl, kt + 2, wave, 12 * s / (kSub - 1), 12 * (s + 1) / (kSub - 1));
             APS_PIN();
             mma_frags<Fmt>(f[s & 1], acc);
             APS_PIN();
@@ -426,7 +421,7 @@ __device__ inline void ffn_up_block(Ring3& ring, const uint8_t* __restrict__ x, 
     const int aR = wave_a_row<TALL>(wave), bR = wave_b_row<TALL>(wave);
     f32x16_t acc[2][4];
     zero_acc(acc);
-    mainloop3<TALL, Fmt>(ring, sl, KT, wave, lane, aR, bR, acc, (blockIdx.x % kXcds) * KT / kXcds);
+    mainloop3<TALL, Fmt>(ring, sl, KT, wave, lane, aR, bR, acc);
 
     // Epilogue: scales (fp8), SwiGLU in registers (B fragments 0,1 are gate
     // columns 0..63 of the wave's column block, 2,3 the same up columns), the
