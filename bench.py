@@ -481,9 +481,19 @@ def main():
     peak = PEAK_FP8 if fp8 else (PEAK_BF16 if bf16 else PEAK_F32)
     bytes_router = T * H * esz + E * H * 4 + T * E * 4
     bytes_combine = A * H * esz + T * H * esz + A * 4
+    # The router's bound is its FMA chains, not HBM: every logit is one fp32
+    # FMA chain over H steps in the reference's order, so the floor is the
+    # longer of one chain at one VALU issue (4 cycles for a 64-wide wave on a
+    # 16-lane SIMD) per step, and all T*E chains through every SIMD's 16
+    # lanes, at the 2.4 GHz peak clock.
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    chain_cycles = max(4.0 * H, T * E * H / (n_cu * 64.0))
+    chain_floor_s = chain_cycles / 2.4e9
     stage_report = {
         "router_logits": {"us": mean_t["router_logits"] * 1e6,
-                          "GB_s": bytes_router / mean_t["router_logits"] / 1e9},
+                          "GB_s": bytes_router / mean_t["router_logits"] / 1e9,
+                          "chain_floor_us": chain_floor_s * 1e6,
+                          "frac_of_chain_floor": chain_floor_s / mean_t["router_logits"]},
         "route_top2": {"us": mean_t["route_top2"] * 1e6},
         "dispatch": {"us": mean_t["dispatch"] * 1e6},
         "ffn_up": {"us": mean_t["ffn_up"] * 1e6, "TFLOP_s": flops_up / mean_t["ffn_up"] / 1e12},
@@ -514,10 +524,13 @@ def main():
             runs.append(time.perf_counter() - t)
         total = sum(runs)
         cpu = {"value": T * len(runs) / total, "unit": "tokens/s", "cores": oracle.num_threads(), "kind": "port",
+               "host_cpus_visible": len(os.sched_getaffinity(0)),
                "sample": f"{len(runs)} runs of the full {args.config} batch ({T} tokens each, {total:.1f} s in "
                          f"all, median {statistics.median(runs):.2f} s), values upcast to fp32, reference "
                          f"CPU-path order (router, route, per-expert gather/FFN/scatter-add), after a 256-token "
-                         f"warm-up"}
+                         f"warm-up; cores = OpenMP threads used (omp_get_max_threads); the timed code is the "
+                         f"oracle's blocked, transposed restatement, faster than the reference's plain "
+                         f"omp-parallel loops"}
 
     line = {
         "metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1,
