@@ -338,8 +338,16 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
     const float q = route_quantise(acc);
     const int base = lane & ~(16 * R - 1);
     float qs[16 * R];
+    if constexpr (R == 1) {
+        // the token's 16 values sit in its 16-lane row: DPP row broadcasts
+        const int qi = __builtin_bit_cast(int, q);
+        [&]<int... K>(std::integer_sequence<int, K...>) __attribute__((always_inline)) {
+            ((qs[K] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(qi, 0x150 + K, 0xF, 0xF, false))), ...);
+        }(std::make_integer_sequence<int, 16>{});
+    } else {
 #pragma unroll
-    for (int k = 0; k < 16 * R; ++k) qs[k] = __shfl(q, base + k);
+        for (int k = 0; k < 16 * R; ++k) qs[k] = __shfl(q, base + k);
+    }
     int first, second;
     route_greedy_top2<16 * R>(qs, E, first, second);
     if (valid && lane == base) {
