@@ -131,6 +131,7 @@ __device__ inline RowTile wave_find_tile(int tile, int bm, uint32_t lo, uint32_t
 // Router GEMM; with routes != nullptr also the top-2 routes and the tile
 // histogram (tile_counts), in the same kernel; with x_copy != nullptr (fp32
 // x only) also the bf16 copy of x [rows][hidden].
+int num_cus();  // compute units of the current device
 hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t rows, int hidden,
                          int experts, float* logits, uint8_t* routes, uint32_t* tile_counts,
                          bf16_t* x_copy, hipStream_t s);
@@ -175,6 +176,11 @@ hipError_t launch_zero(float* x, int64_t n, hipStream_t s);
 
 // y = x w^T (+ bias): fp32 FMA chain over k ascending per output, bias added
 // once (in_f % 16 == 0, out_f % 4 == 0).
+// fp32 Linear on the K = 1 fp32 MFMA (same bits as the FMA chain); shapes
+// with in_f % 32 == 0
+bool linear_mfma_fits(int64_t rows, int in_f, int out_f);
+hipError_t launch_linear_mfma_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows,
+                                  int in_f, int out_f, hipStream_t s);
 hipError_t launch_linear_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows, int in_f,
                              int out_f, hipStream_t s);
 

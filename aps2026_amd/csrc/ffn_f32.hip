@@ -225,6 +225,9 @@ k_linear_f32(const float* __restrict__ x, const float* __restrict__ w, const flo
 hipError_t launch_linear_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows, int in_f,
                              int out_f, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
+    // the matrix-core kernel computes the same chains (see linear_mfma.hip);
+    // this SIMT kernel serves in_f not a multiple of 32
+    if (linear_mfma_fits(rows, in_f, out_f)) return launch_linear_mfma_f32(x, w, bias, y, rows, in_f, out_f, s);
     if (in_f % kBK != 0 || out_f % 4 != 0 || out_f <= 0) return hipErrorInvalidValue;
     const int64_t ty = ceil_div(rows, kF32BM);
     if (ty > 65535) return hipErrorInvalidValue;

@@ -118,6 +118,16 @@ __device__ inline void wait_vm_lgkm0_upto20(int n) {
     }
 }
 
+// wait_vm_lgkm0<n> for a value n in {0, 4, ..., 32} known only at run time.
+__device__ inline void wait_vm_lgkm0_upto32(int n) {
+    switch (n) {
+        case 32: wait_vm_lgkm0<32>(); break;
+        case 28: wait_vm_lgkm0<28>(); break;
+        case 24: wait_vm_lgkm0<24>(); break;
+        default: wait_vm_lgkm0_upto20(n); break;
+    }
+}
+
 // s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt left at their maximum).
 __device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x0 << 8) | (0x3 << 14)); }
 
@@ -748,9 +758,6 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
         raw_barrier();
         if (g + 2 < nstages) issue_b(g + 2);
     };
-    if (nstages > 0) issue_b(0);
-    if (nstages > 1) issue_b(1);
-
     // fp8 scales: the block's w2 column scales into LDS, its 2 x 32 row scales per lane
     float rs[2] = {1.0f, 1.0f};
     if constexpr (kFp8) {
@@ -766,6 +773,11 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
     }
 
     // ---- the row tile of act into registers, one 32 KB stage at a time ----
+    // Four act slots, so that four stages are in flight: slots 0 and 1 are
+    // the w2 ring (two images each), slots 2 and 3 the y stage.  Stage kt
+    // uses slot kt % 4; once it is read, the slot takes stage kt + 4.  The w2
+    // ring's first two stages are copied once the ring's act slot 0 has been
+    // read for the last time (act stage kt0).
     typename Fmt::frag_t areg[KTM][2][kSub];
     {
         const uint8_t* asrc[8];
@@ -776,29 +788,39 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
             p = p < u.end ? p : u.end - 1;
             asrc[s] = act + static_cast<int64_t>(p) * act_row_bytes + slot_chunk(row, lane) * 16;
         }
+        auto aslot = [&](int kt) -> uint8_t* {
+            const int j = kt & 3;
+            return j < 2 ? &lds.ring[0][0] + j * kArAStage : lds.stage + (j - 2) * kArAStage;
+        };
         auto issue_a = [&](int kt) {
-            uint8_t* st = lds.stage + (kt & 1) * kArAStage;
+            uint8_t* st = aslot(kt);
 #pragma unroll
             for (int s = 0; s < 8; ++s) dma16(asrc[s] + kt * kRowBytes, st + (32 * s + 8 * wave) * kRowBytes);
         };
-        issue_a(0);
+        constexpr int kt0 = 4 * ((KT - 1) / 4);        // the last act stage in slot 0
+        const int nbq = nstages < 2 ? nstages : 2;     // w2 stages copied after it
+#pragma unroll
+        for (int kt = 0; kt < (KT < 4 ? KT : 4); ++kt) issue_a(kt);
 #pragma unroll
         for (int kt = 0; kt < KTM; ++kt) {
             if (kt < KT) {
-                if (kt + 1 < KT) {
-                    issue_a(kt + 1);
-                    wait_vm_lgkm0<8>();
-                } else {
-                    wait_vm_lgkm0<0>();
-                }
+                // copies issued after act stage kt: act stages kt+1 .. min(KT-1, kt+3)
+                // (8 per wave each) and, past kt0, the w2 stages (4 each)
+                const int a_after = (KT - 1 < kt + 3 ? KT - 1 : kt + 3) - kt;
+                wait_vm_lgkm0_upto32(8 * a_after + (kt > kt0 ? 4 * nbq : 0));
                 raw_barrier();
-                const uint8_t* st = lds.stage + (kt & 1) * kArAStage;
+                const uint8_t* st = aslot(kt);
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
                     for (int kk = 0; kk < kSub; ++kk) areg[kt][i][kk] = Fmt::load(st, aR + 32 * i + (lane & 31), kk, lane);
                 wait_lgkm0();
-                raw_barrier();  // slot kt & 1 takes stage kt + 2; the last barrier frees the y stage
+                raw_barrier();  // slot kt % 4 is free; the last barrier frees the y stage and the ring
+                if (kt + 4 < KT) issue_a(kt + 4);
+                if (kt == kt0) {
+                    if (nstages > 0) issue_b(0);
+                    if (nstages > 1) issue_b(1);
+                }
             }
         }
     }
@@ -890,17 +912,6 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
     }
 }
 
-int num_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
 
 // The register-resident w2 kernel for KT k stages, or null when KT is past
 // the register budget (the streamed kernel serves those shapes).
@@ -938,6 +949,19 @@ int64_t max_blocks(int64_t rows, int nblk, int experts, bool all_tall) {
 dim3 grid_of(int64_t blocks) { return dim3(static_cast<unsigned>(ceil_div(blocks, kXcds) * kXcds)); }
 
 }  // namespace
+
+// Compute units of the current device (cached per device).
+int num_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
 
 hipError_t launch_ffn_up_bf16(const bf16_t* x, const uint32_t* offsets,
                               const uint32_t* assignment_rows, const bf16_t* w13,

@@ -133,7 +133,9 @@ def test_attention_errors(gpu_device):
 
 
 @pytest.mark.parametrize("rows,k,n,bias", [(10240 // 40, 4096, 2048, True), (300, 4096, 512, True),
-                                           (77, 2048, 4096, True), (64, 256, 12, False), (1, 16, 4, True)])
+                                           (77, 2048, 4096, True), (64, 256, 12, False), (1, 16, 4, True),
+                                           (129, 96, 132, True), (5, 32, 256, False), (200, 48, 20, True),
+                                           (2048, 256, 4096, True)])
 def test_linear_bit_exact(gpu_device, rows, k, n, bias):
     """aps_linear (the q/k/v/o projections) against the oracle's linear
     (one FMA chain per output, k ascending, then the bias), bit for bit."""
@@ -146,3 +148,25 @@ def test_linear_bit_exact(gpu_device, rows, k, n, bias):
     torch.cuda.synchronize()
     want = oracle.linear(x, w, b)
     np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_linear_bit_exact_wide_exponents(gpu_device):
+    """The matrix-core Linear (K = 1 fp32 MFMA chains) against the oracle's
+    FMA chain on operands whose exponents span 2^-20 .. 2^20 and on products
+    around FLT_MIN, where a product rounded before the add (no fused
+    multiply-add) or a flushed subnormal would change bits."""
+    rng = np.random.default_rng(3)
+    rows, k, n = 130, 512, 160
+    for scale in ("spread", "tiny"):
+        note(f"linear wide-exponent case {scale}")
+        if scale == "spread":
+            x = (rng.uniform(-1, 1, (rows, k)) * np.exp2(rng.integers(-20, 20, (rows, k)))).astype(np.float32)
+            w = (rng.uniform(-1, 1, (n, k)) * np.exp2(rng.integers(-20, 20, (n, k)))).astype(np.float32)
+        else:
+            x = (rng.uniform(-1, 1, (rows, k)) * 1e-19).astype(np.float32)
+            w = (rng.uniform(-1, 1, (n, k)) * 1e-19).astype(np.float32)
+        b = (0.1 * rng.standard_normal(n)).astype(np.float32)
+        got = attention.linear_gpu(dev(x, gpu_device), dev(w, gpu_device), dev(b, gpu_device))
+        torch.cuda.synchronize()
+        want = oracle.linear(x, w, b)
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
