@@ -293,9 +293,10 @@ def decoder_bench(args):
             t_plan.append(time.perf_counter() - t1)
         stages["prefix_trie_and_upload_ms"] = statistics.median(t_plan) * 1e3
     # the projections dominate: one fp32 FMA chain per output (the reference's
-    # order), on the VALU; MI355X's published fp32 rate is 157.3 TFLOP/s
+    # order) as chains of K = 1 fp32 MFMAs; MI355X's published fp32 matrix
+    # rate is 157.3 TFLOP/s
     proj_s = mt["qkv_proj"] + mt["o_proj"]
-    roofline = {"bound": "valu", "kernel": "k_linear_f32 (q/k/v/o projections)",
+    roofline = {"bound": "mfma", "kernel": "k_linear_mfma (q/k/v/o projections)",
                 "achieved": (qkv_flops + o_flops) / proj_s / 1e12, "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
                 "frac": (qkv_flops + o_flops) / proj_s / PEAK_F32, "traffic": None,
                 "flops_per_launch": (qkv_flops + o_flops) / 4, "launch_us": proj_s / 4 * 1e6}
