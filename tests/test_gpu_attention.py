@@ -98,6 +98,50 @@ def test_attention_window_past_64k_of_lds(gpu_device):
                                      q_heads=4, kv_heads=1, window=8000)
 
 
+@pytest.mark.parametrize("window", [2047, 300])
+def test_attention_long_branches_bit_exact(gpu_device, window):
+    """Three 900..1000-token prompts sharing a 600-token prefix: every row,
+    with windows longer than and shorter than the chains (keys in many
+    64-key chunks, window starts inside a chunk)."""
+    note(f"attention tree long branches window={window}")
+    rng = np.random.default_rng(window)
+    pre = rng.integers(0, 32064, 600).tolist()
+    batch = [pre + rng.integers(0, 32064, int(n)).tolist() for n in (300, 350, 400)]
+    plan, q, k, v = trie_inputs(batch, q_heads=16, kv_heads=4, seed=window + 1)
+    out = torch.empty((plan.nodes, 16 * 128), dtype=torch.float32, device=gpu_device)
+    attention.attention_tree_gpu(dev(q, gpu_device), dev(k, gpu_device), dev(v, gpu_device), out,
+                                 plan.node_depth, plan.node_anc, plan.max_len, window=window)
+    torch.cuda.synchronize()
+    want = oracle.attention_tree(q, k, v, plan.node_depth, plan.node_anc, plan.max_len, 16, 4, 128, window)
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("window", [2047, 20])
+def test_attention_spread_positions_bit_exact(gpu_device, window):
+    """One 300-node chain whose rows are numbered in random order: groups of
+    four consecutive rows lie on one chain at scattered positions, in and out
+    of order, some further apart than a window (the matrix-core group path and
+    the row path both serve such groups)."""
+    note(f"attention tree scattered chain positions window={window}")
+    n = 300
+    rng = np.random.default_rng(11)
+    order = rng.permutation(n)                 # order[p] = row at chain position p
+    pos = np.empty(n, np.uint32)
+    pos[order] = np.arange(n, dtype=np.uint32)
+    anc = np.zeros((n, n), np.uint32)
+    for r in range(n):
+        anc[r, :pos[r] + 1] = order[:pos[r] + 1]
+    q = rng.standard_normal((n, 16 * 128)).astype(np.float32)
+    k = rng.standard_normal((n, 4 * 128)).astype(np.float32)
+    v = rng.standard_normal((n, 4 * 128)).astype(np.float32)
+    out = torch.empty((n, 16 * 128), dtype=torch.float32, device=gpu_device)
+    attention.attention_tree_gpu(dev(q, gpu_device), dev(k, gpu_device), dev(v, gpu_device), out, pos, anc, n,
+                                 window=window)
+    torch.cuda.synchronize()
+    want = oracle.attention_tree(q, k, v, pos, anc, n, 16, 4, 128, window)
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
 def test_attention_nodes_equal_token_rows(gpu_device):
     note("attention tree nodes vs token rows")
     batch = shared_batch(4, groups=2, per=4, pre=60, suf=20)
