@@ -141,7 +141,7 @@ __device__ inline void rows_transpose4(af4& x) {
 // wave q / 4, so exp, the ordered denominator and p = e / den need no
 // workgroup barrier.  Values: two waves (0, 1 on even workgroups, 2, 3 on
 // odd ones, so that two resident workgroups spread them over the SIMDs) take
-// dimensions 64 w' .. 64 w' + 63, one coalesced 256-byte load per key, 32
+// dimensions 64 w' .. 64 w' + 63, one coalesced 256-byte load per key, 64
 // keys ahead; the K / V row offsets are 32-bit byte offsets off a uniform
 // base.
 template <bool PACKED>
@@ -283,10 +283,13 @@ k_attention_group(const float* __restrict__ q, const float* __restrict__ k, cons
             vb[4 * u4 + 3] = *reinterpret_cast<const float*>(vbase + (kr.w + dbytes));
         }
     };
-    float vb0[16], vb1[16];
-    if (pwave == 0 || pwave == 1) {   // the first 32 keys' values go out now
+    float vb0[16], vb1[16], vb2[16], vb3[16];
+    auto gclamp = [&](int g) { return g < ntiles ? g : ntiles - 1; };
+    if (pwave == 0 || pwave == 1) {   // the first 64 keys' values go out now
         vload(0, vb0);
-        vload(ntiles > 1 ? 1 : 0, vb1);
+        vload(gclamp(1), vb1);
+        vload(gclamp(2), vb2);
+        vload(gclamp(3), vb3);
     }
     {
         const float mq = fmaxf(fmaxf(wmx[0][qi], wmx[1][qi]), fmaxf(wmx[2][qi], wmx[3][qi]));
@@ -304,7 +307,7 @@ k_attention_group(const float* __restrict__ q, const float* __restrict__ k, cons
         }
         for (; w <= h0; w += 16) srow[w] = static_cast<float>(exp(static_cast<double>(__fsub_rn(srow[w], mq))));
         // the denominator in key order on the query's first lane (the
-        // wave's LDS accesses complete in program order)
+        // wave's LDS accesses complete in program order), 16 reads ahead
         float den = 0.0f;
         if (part == 0) {
             int x = l0;
@@ -319,8 +322,18 @@ k_attention_group(const float* __restrict__ q, const float* __restrict__ k, cons
         }
         den = __shfl(den, lane & ~15);
         // p = e / den in the window, 0 elsewhere over the tiles
-        for (int x = part; x < ntiles * kKeyTile; x += 16)
-            srow[x] = (x >= l0 && x <= h0) ? __fdiv_rn(srow[x], den) : 0.0f;
+        int x = part;
+        for (; x + 48 < ntiles * kKeyTile; x += 64) {
+            float e[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) e[u] = srow[x + 16 * u];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int xu = x + 16 * u;
+                srow[xu] = (xu >= l0 && xu <= h0) ? __fdiv_rn(e[u], den) : 0.0f;
+            }
+        }
+        for (; x < ntiles * kKeyTile; x += 16) srow[x] = (x >= l0 && x <= h0) ? __fdiv_rn(srow[x], den) : 0.0f;
     }
     __syncthreads();
 
@@ -333,7 +346,7 @@ k_attention_group(const float* __restrict__ q, const float* __restrict__ k, cons
             float vc[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) vc[u] = vb[u];
-            vload(g + 2 < ntiles ? g + 2 : ntiles - 1, vb);   // unconditional, as for the scores
+            vload(gclamp(g + 4), vb);   // unconditional, as for the scores
             if (g >= ntiles) return;                           // wave-uniform
             float pa[16];
 #pragma unroll
@@ -341,9 +354,11 @@ k_attention_group(const float* __restrict__ q, const float* __restrict__ k, cons
 #pragma unroll
             for (int u = 0; u < 16; ++u) o = __builtin_amdgcn_mfma_f32_16x16x1f32(pa[u], vc[u], o, 0, 0, 0);
         };
-        for (int g = 0; g < ntiles; g += 2) {
+        for (int g = 0; g < ntiles; g += 4) {
             group(g, vb0);
             group(g + 1, vb1);
+            group(g + 2, vb2);
+            group(g + 3, vb3);
         }
     }
 #pragma unroll
