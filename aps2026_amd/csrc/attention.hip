@@ -157,7 +157,9 @@ k_attention_group(const float* __restrict__ q, const float* __restrict__ k, cons
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t r0 = static_cast<int64_t>(blockIdx.x / kv_heads) * kGroupRows;
+    // groups in reverse row order: later rows (longer chains in trie and
+    // packed order) start first, so the short ones fill the last round
+    const int64_t r0 = static_cast<int64_t>(gridDim.x / kv_heads - 1 - blockIdx.x / kv_heads) * kGroupRows;
     const int kh = static_cast<int>(blockIdx.x % kv_heads);
     // sw = key capacity + 1; groups that are not path groups are the row kernel's
     if (!group_is_path<PACKED>(row_pos, anc, anc_stride, rows, r0, wmax, sw - 1, lane)) return;
