@@ -142,6 +142,38 @@ def test_attention_spread_positions_bit_exact(gpu_device, window):
     np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("window", [2047, 100])
+def test_attention_packed_long_sequences_bit_exact(gpu_device, window):
+    """aps_attention_packed (the reference's attention_gpu over packed
+    sequences) on sequences of 700, 333, 64, 5 and 1 tokens: every row
+    against the oracle's attention over its sequence's prefix, bit for bit
+    (the packed path-group kernel and the row kernel for rows whose group
+    crosses a sequence boundary)."""
+    from aps2026_amd import capi
+    from aps2026_amd.moe import _ptr, _stream
+    note(f"attention packed long sequences window={window}")
+    lens = [700, 333, 64, 5, 1]
+    rows, stride = sum(lens), max(lens)
+    off = np.repeat(np.cumsum([0] + lens[:-1]), lens).astype(np.uint32)
+    pos = np.concatenate([np.arange(n) for n in lens]).astype(np.uint32)
+    anc = np.zeros((rows, stride), np.uint32)
+    for r in range(rows):
+        anc[r, :pos[r] + 1] = off[r] + np.arange(pos[r] + 1)
+    rng = np.random.default_rng(window)
+    q = rng.standard_normal((rows, 16 * 128)).astype(np.float32)
+    k = rng.standard_normal((rows, 4 * 128)).astype(np.float32)
+    v = rng.standard_normal((rows, 4 * 128)).astype(np.float32)
+    qd, kd, vd = dev(q, gpu_device), dev(k, gpu_device), dev(v, gpu_device)
+    out = torch.empty((rows, 16 * 128), dtype=torch.float32, device=gpu_device)
+    od, pd = dev(off.view(np.int32), gpu_device), dev(pos.view(np.int32), gpu_device)
+    rc = capi.lib().aps_attention_packed(_ptr(qd), _ptr(kd), _ptr(vd), _ptr(out), _ptr(od), _ptr(pd), stride, rows,
+                                         16, 4, 128, window, _stream(qd.device))
+    assert rc == 0, capi.last_error()
+    torch.cuda.synchronize()
+    want = oracle.attention_tree(q, k, v, pos, anc, stride, 16, 4, 128, window)
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
 def test_attention_nodes_equal_token_rows(gpu_device):
     note("attention tree nodes vs token rows")
     batch = shared_batch(4, groups=2, per=4, pre=60, suf=20)
