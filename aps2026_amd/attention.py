@@ -82,6 +82,45 @@ def linear_gpu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor = None,
     return out
 
 
+def linear_tc_prepare(weight: torch.Tensor) -> torch.Tensor:
+    """The reference's Tensor::prepare_cuda_bf16_weight(true) (src/tensor.cu:
+    149-177): weight [out][in] fp32 -> packed bf16 hi / lo tile images on the
+    weight's device (the USE_TC Linear's operand)."""
+    n, k = weight.shape
+    if weight.dtype != torch.float32 or not weight.is_contiguous():
+        raise ValueError("linear_tc_prepare expects a contiguous fp32 matrix")
+    nbytes = capi.lib().aps_linear_tc_packed_bytes(n, k)
+    if nbytes == 0 or n % 4 != 0:
+        raise ValueError("linear_tc_prepare shape: out % 4 == 0, in % 64 == 0")
+    packed = torch.empty(nbytes, dtype=torch.uint8, device=weight.device)
+    _call(capi.lib().aps_linear_tc_prepare(_ptr(weight), n, k, _ptr(packed), nbytes, _stream(weight.device)))
+    return packed
+
+
+def linear_tc_split(x: torch.Tensor) -> torch.Tensor:
+    """x [rows][in] fp32 -> [2][rows][in] bf16 bits (x_hi, x_lo), the
+    USE_TC kernel's on-the-fly split done once per input."""
+    k = x.shape[-1]
+    rows = x.numel() // k
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("linear_tc_split expects contiguous fp32")
+    out = torch.empty((2, rows, k), dtype=torch.int16, device=x.device)
+    _call(capi.lib().aps_linear_tc_split(_ptr(x), rows, k, _ptr(out), _stream(x.device)))
+    return out
+
+
+def linear_tc_gpu(x_split: torch.Tensor, packed: torch.Tensor, out_features: int, bias: torch.Tensor = None,
+                  all_terms: bool = False, out: torch.Tensor = None) -> torch.Tensor:
+    """y = x_hi W_hi + x_hi W_lo + x_lo W_hi (+ x_lo W_lo) (+ bias): the
+    reference's USE_TC / USE_TC_ALL Linear (src/tensor.cu:514-584)."""
+    _, rows, k = x_split.shape
+    if out is None:
+        out = torch.empty((rows, out_features), dtype=torch.float32, device=x_split.device)
+    _call(capi.lib().aps_linear_tc(_ptr(x_split), rows, k, _ptr(packed), _ptr(bias), out_features, int(all_terms),
+                                   _ptr(out), _stream(x_split.device)))
+    return out
+
+
 def apply_rope_tree_gpu(q: torch.Tensor, k: torch.Tensor, row_pos, max_seq: int,
                         q_heads: int = NUM_ATTENTION_HEADS, kv_heads: int = NUM_KV_HEADS,
                         head_dim: int = HEAD_DIM, theta: float = ROPE_THETA) -> None:

@@ -14,6 +14,11 @@ Flags:
                                          quantisation step (reference semantics)
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                          no packed fp32 instructions
+
+Environment: APS_USE_TC=1 builds the C++ layer with the reference's USE_TC
+(the LM head and the last layer's attention projections on the split-bf16
+Linear), APS_USE_TC_ALL=1 with USE_TC and USE_TC_ALL (every attention
+projection, four products); both are off by default, as in the reference.
 """
 from __future__ import annotations
 
@@ -49,6 +54,10 @@ CHECK_BIN = os.path.join(REPO, "tests", "cpp", "layer_check")
 CXX = os.environ.get("CXX", "g++")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include")]
+if os.environ.get("APS_USE_TC_ALL") == "1":
+    HOST_FLAGS += ["-DUSE_TC", "-DUSE_TC_ALL"]
+elif os.environ.get("APS_USE_TC") == "1":
+    HOST_FLAGS += ["-DUSE_TC"]
 HIP_LINK = ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath," + os.path.join(ROCM, "lib")]
 
 

@@ -78,7 +78,20 @@ Linear::Linear(Tensor weight, Tensor bias) : weight_(std::move(weight)), bias_(s
 }
 
 Linear::Linear(const ModelLoader& loader, const std::string& weight, const std::string& bias)
-    : Linear(loader.load(weight), !bias.empty() && loader.has(bias) ? loader.load(bias) : Tensor()) {}
+    : Linear(loader.load(weight), !bias.empty() && loader.has(bias) ? loader.load(bias) : Tensor()) {
+#ifdef USE_TC
+    // built with USE_TC (USE_TC_ALL): the split-bf16 Linear for the LM head
+    // and the last layer's (every layer's) attention projections, the
+    // reference's selection (src/layer.cu:16-27)
+#ifdef USE_TC_ALL
+    const bool terminal_tc = weight == "lm_head.weight" ||
+                             (weight.find("model.layers.") == 0 && weight.find(".self_attn.") != std::string::npos);
+#else
+    const bool terminal_tc = weight == "lm_head.weight" || weight.find("model.layers.31.self_attn.") == 0;
+#endif
+    if (terminal_tc) weight_.prepare_cuda_bf16_weight(true);
+#endif
+}
 
 void Linear::forward(const Tensor& x, Tensor& y, bool use_gpu) const {
     if (!use_gpu) throw std::invalid_argument("Linear::forward: the CPU path (use_gpu = false) is not provided");

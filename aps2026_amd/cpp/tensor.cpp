@@ -54,6 +54,27 @@ Workspace& workspace() {
     return *w;
 }
 
+// The split-bf16 Linear (a weight with a bf16 copy, Tensor::
+// prepare_cuda_bf16_weight): x split once into hi / lo rows in a grow-only
+// buffer of its own, then aps_linear_tc; four terms when built with
+// USE_TC_ALL (reference src/tensor.cu:566-568).
+void linear_tc(const float* da, const Tensor& b, const float* dbias, std::size_t m, std::size_t k, std::size_t n,
+               float* dc, const char* op) {
+#ifdef USE_TC_ALL
+    constexpr int kAllTerms = 1;
+#else
+    constexpr int kAllTerms = 0;
+#endif
+    static Workspace* split = new Workspace();
+    std::lock_guard<std::mutex> lock(split->mu);
+    void* xs = split->get(m * k * 2 * sizeof(std::uint16_t));
+    int rc = aps_linear_tc_split(da, static_cast<int64_t>(m), static_cast<int32_t>(k), xs, nullptr);
+    if (!rc)
+        rc = aps_linear_tc(xs, static_cast<int64_t>(m), static_cast<int32_t>(k), b.cuda_bf16_weight_hi(), dbias,
+                           static_cast<int32_t>(n), kAllTerms, dc, nullptr);
+    if (rc) throw_status(rc, op);
+}
+
 }  // namespace
 
 // ---- tensor_ops ------------------------------------------------------------
@@ -67,6 +88,10 @@ void matmul_transposed_gpu(const Tensor& a, const Tensor& b, Tensor& c) {
     if (b.size(1) != k || c.size(0) != m || c.size(1) != n)
         throw std::invalid_argument("matmul_transposed_gpu shape");
     const float* da = a.cuda_data();
+    if (b.has_cuda_bf16_weight()) {   // the reference's USE_TC branch (src/tensor.cu:3042-3055)
+        linear_tc(da, b, nullptr, m, k, n, c.cuda_data_write(), "matmul_transposed_gpu");
+        return;
+    }
     const float* db = b.cuda_data();
     if (n <= 64 && k % 256 == 0) {  // the router shape: the router kernel
         const int rc = aps_router_logits(da, APS_DTYPE_F32, db, static_cast<int64_t>(m), static_cast<int32_t>(k),
@@ -87,6 +112,10 @@ void matmul_transposed_bias_gpu(const Tensor& a, const Tensor& b, const Tensor& 
     const std::size_t n = b.size(0);
     if (b.size(1) != k || c.size(0) != m || c.size(1) != n || bias.size() != n)
         throw std::invalid_argument("matmul_transposed_bias_gpu shape");
+    if (b.has_cuda_bf16_weight()) {   // the product, then the bias (reference src/tensor.cu:3121-3142)
+        linear_tc(a.cuda_data(), b, bias.cuda_data(), m, k, n, c.cuda_data_write(), "matmul_transposed_bias_gpu");
+        return;
+    }
     if (k % 16 != 0 || n % 4 != 0)
         throw std::invalid_argument("matmul_transposed_bias_gpu: this build needs k % 16 == 0 and n % 4 == 0");
     const int rc = aps_linear(a.cuda_data(), b.cuda_data(), bias.cuda_data(), static_cast<int64_t>(m),

@@ -79,11 +79,16 @@ void Tensor::swap(Tensor& other) noexcept {
     host_.swap(other.host_);
     std::swap(dev_, other.dev_);
     std::swap(fresh_, other.fresh_);
+    std::swap(bf16_, other.bf16_);
+    std::swap(bf16_bytes_, other.bf16_bytes_);
 }
 
 void Tensor::release_device() noexcept {
     if (dev_) (void)hipFreeAsync(dev_, nullptr);
+    if (bf16_) (void)hipFreeAsync(bf16_, nullptr);
     dev_ = nullptr;
+    bf16_ = nullptr;
+    bf16_bytes_ = 0;
     fresh_ &= ~kOnDevice;
     if (!fresh_) fresh_ = kOnHost;  // nothing current left: the values are gone, zeros stand in
 }
@@ -137,6 +142,26 @@ float* Tensor::cuda_data_write() {
 }
 
 void Tensor::sync_cuda_to_host() const { (void)host_current(); }
+
+void Tensor::prepare_cuda_bf16_weight(bool with_low_residual) const {
+    if (shape_.size() != 2) throw std::invalid_argument("BF16 packing requires a matrix");
+    if (bf16_) return;
+    const std::size_t bytes =
+        aps_linear_tc_packed_bytes(static_cast<int32_t>(shape_[0]), static_cast<int32_t>(shape_[1]));
+    if (bytes == 0 || shape_[0] % 4 != 0) return;   // a shape the split kernel does not take: fp32 stays
+    void* p = nullptr;
+    device_call(hipMallocAsync(&p, bytes, nullptr), "hipMallocAsync BF16 weight");
+    const int rc = aps_linear_tc_prepare(cuda_data(), static_cast<int32_t>(shape_[0]), static_cast<int32_t>(shape_[1]),
+                                         p, bytes, nullptr);
+    if (rc) {
+        (void)hipFreeAsync(p, nullptr);
+        throw std::runtime_error(std::string("prepare_cuda_bf16_weight: ") + aps_moe_last_error());
+    }
+    if (!with_low_residual)
+        device_call(hipMemsetAsync(static_cast<char*>(p) + bytes / 2, 0, bytes / 2, nullptr), "hipMemsetAsync BF16 lo");
+    bf16_ = p;
+    bf16_bytes_ = bytes;
+}
 
 float* Tensor::data() { return host_for_write(); }
 const float* Tensor::data() const { return host_current(); }

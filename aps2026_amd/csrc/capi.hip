@@ -580,6 +580,61 @@ int aps_linear(const float* x, const float* weight, const float* bias, int64_t r
     return APS_OK;
 }
 
+size_t aps_linear_tc_packed_bytes(int32_t out_features, int32_t in_features) {
+    if (out_features <= 0 || in_features <= 0 || in_features % 64 != 0) return 0;
+    return static_cast<size_t>(aps::linear_tc_packed_elems(out_features, in_features)) * sizeof(uint16_t);
+}
+
+int aps_linear_tc_prepare(const float* weight, int32_t out_features, int32_t in_features, void* packed,
+                          size_t packed_bytes, void* stream) {
+    if (out_features <= 0 || in_features <= 0 || in_features % 64 != 0 || out_features % 4 != 0)
+        return fail(APS_ERR_SHAPE, "split-bf16 weight shape: out %d (multiple of 4) in %d (multiple of 64)",
+                    out_features, in_features);
+    if (!weight || !packed) return fail(APS_ERR_ARG, "split-bf16 prepare: NULL pointer");
+    const size_t need = aps_linear_tc_packed_bytes(out_features, in_features);
+    if (packed_bytes < need)
+        return fail(APS_ERR_ARG, "split-bf16 prepare: packed buffer %zu bytes, needs %zu", packed_bytes, need);
+    if (((reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(packed)) & 15u) != 0)
+        return fail(APS_ERR_ARG, "split-bf16 prepare: arrays must be 16-byte aligned");
+    APS_HIP(aps::launch_linear_tc_prepare(weight, out_features, in_features, static_cast<uint16_t*>(packed),
+                                          static_cast<hipStream_t>(stream)),
+            "split-bf16 prepare launch");
+    return APS_OK;
+}
+
+int aps_linear_tc_split(const float* x, int64_t rows, int32_t in_features, void* x_split, void* stream) {
+    if (rows < 0 || in_features <= 0 || in_features % 64 != 0)
+        return fail(APS_ERR_SHAPE, "split-bf16 input shape: rows %lld in %d (multiple of 64)", (long long)rows,
+                    in_features);
+    if (rows == 0) return APS_OK;
+    if (!x || !x_split) return fail(APS_ERR_ARG, "split-bf16 split: NULL pointer");
+    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(x_split)) & 15u) != 0)
+        return fail(APS_ERR_ARG, "split-bf16 split: arrays must be 16-byte aligned");
+    const int64_t n = rows * in_features;
+    uint16_t* hi = static_cast<uint16_t*>(x_split);
+    APS_HIP(aps::launch_split_bf16(x, n, hi, hi + n, static_cast<hipStream_t>(stream)), "split-bf16 split launch");
+    return APS_OK;
+}
+
+int aps_linear_tc(const void* x_split, int64_t rows, int32_t in_features, const void* packed, const float* bias,
+                  int32_t out_features, int32_t all_terms, float* y, void* stream) {
+    if (rows < 0 || in_features <= 0 || in_features % 64 != 0 || out_features <= 0 || out_features % 4 != 0 ||
+        (rows + 127) / 128 > 65535)
+        return fail(APS_ERR_SHAPE, "split-bf16 linear shape: rows %lld in %d (multiple of 64) out %d (multiple of 4)",
+                    (long long)rows, in_features, out_features);
+    if (rows == 0) return APS_OK;
+    if (!x_split || !packed || !y) return fail(APS_ERR_ARG, "split-bf16 linear: NULL pointer");
+    if (((reinterpret_cast<uintptr_t>(x_split) | reinterpret_cast<uintptr_t>(packed) |
+          reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(y)) & 15u) != 0)
+        return fail(APS_ERR_ARG, "split-bf16 linear: arrays must be 16-byte aligned");
+    const int64_t n = rows * in_features;
+    const uint16_t* hi = static_cast<const uint16_t*>(x_split);
+    APS_HIP(aps::launch_linear_tc(hi, hi + n, static_cast<const uint16_t*>(packed), bias, y, rows, in_features,
+                                  out_features, all_terms != 0, static_cast<hipStream_t>(stream)),
+            "split-bf16 linear launch");
+    return APS_OK;
+}
+
 int aps_rope_table(int64_t max_seq, int32_t head_dim, float theta, float* cos_out, float* sin_out) {
     if (max_seq < 0 || head_dim <= 0 || head_dim % 2 != 0)
         return fail(APS_ERR_SHAPE, "rope table shape: max_seq %lld head_dim %d", (long long)max_seq, head_dim);

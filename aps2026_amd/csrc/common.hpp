@@ -174,6 +174,15 @@ hipError_t launch_add_bias(float* a, const float* bias, int64_t n, int h, hipStr
 hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t s);
 hipError_t launch_zero(float* x, int64_t n, hipStream_t s);
 
+// Split-bf16 Linear (the reference's optional tensor-core path): W packed
+// into hi / lo bf16 tile images, x split into hi / lo bf16 rows, products
+// hi.hi + hi.lo + lo.hi (+ lo.lo) on the bf16 MFMA (in_f % 64 == 0).
+int64_t linear_tc_packed_elems(int out_f, int in_f);
+hipError_t launch_linear_tc_prepare(const float* w, int out_f, int in_f, uint16_t* packed, hipStream_t s);
+hipError_t launch_split_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);
+hipError_t launch_linear_tc(const uint16_t* xhi, const uint16_t* xlo, const uint16_t* packed, const float* bias,
+                            float* y, int64_t rows, int in_f, int out_f, bool all_terms, hipStream_t s);
+
 // y = x w^T (+ bias): fp32 FMA chain over k ascending per output, bias added
 // once (in_f % 16 == 0, out_f % 4 == 0).
 // fp32 Linear on the K = 1 fp32 MFMA (same bits as the FMA chain); shapes

@@ -163,6 +163,15 @@ class Buffers:
     att: torch.Tensor        # attention output [rows][QD]
     post: torch.Tensor       # MoE input [rows][H]
     ws: torch.Tensor         # MoE workspace (shared by the layers)
+    xs: Optional[torch.Tensor] = None   # split-bf16 projections: x_hi, x_lo of one input
+
+    def split(self, src: torch.Tensor, stream) -> torch.Tensor:
+        """src [rows][n] fp32 -> its bf16 hi / lo split in xs (grown on demand)."""
+        n = src.numel()
+        if self.xs is None or self.xs.numel() < 2 * n:
+            self.xs = torch.empty(2 * n, dtype=torch.int16, device=src.device)
+        _call(capi.lib().aps_linear_tc_split(_p(src), self.rows, src.shape[1], _p(self.xs), stream))
+        return self.xs
 
     @staticmethod
     def allocate(rows: int, H: int, moe: MoeWeights, device) -> "Buffers":
@@ -173,17 +182,40 @@ class Buffers:
 
 
 class DecoderLayer:
-    """PhiDecoderLayer over the C ABI (reference include/layer.h:77-95)."""
+    """PhiDecoderLayer over the C ABI (reference include/layer.h:77-95).
 
-    def __init__(self, w: LayerWeights):
+    tc_terms: None for the fp32 projections (the reference's default build);
+    3 or 4 for the split-bf16 Linear on the q/k/v/o projections (the
+    reference's USE_TC / USE_TC_ALL tensor-core path, src/layer.cu:16-27,
+    src/tensor.cu:514-584), whose weights are packed here once."""
+
+    def __init__(self, w: LayerWeights, tc_terms: Optional[int] = None):
         self.w = w
         self.H = w.in_w.numel()
+        self.tc_terms = tc_terms
+        self.tc = {}
+        if tc_terms is not None:
+            from .attention import linear_tc_prepare
+            self.tc = {nm: linear_tc_prepare(wt) for nm, (wt, _) in w.proj.items()}
+
+    def _project(self, b: Buffers, src: torch.Tensor, names, stream) -> None:
+        """The projections of one input: fp32 chains, or the split products
+        (x split once for all of them)."""
+        L, T, K = capi.lib(), b.rows, src.shape[1]
+        if self.tc:
+            xs = b.split(src, stream)
+            for nm, dst, n in names:
+                _call(L.aps_linear_tc(_p(xs), T, K, _p(self.tc[nm]), _p(self.w.proj[nm][1]), n,
+                                      int(self.tc_terms == 4), _p(dst), stream))
+        else:
+            for nm, dst, n in names:
+                _call(L.aps_linear(_p(src), _p(self.w.proj[nm][0]), _p(self.w.proj[nm][1]), T, K, n, _p(dst),
+                                   stream))
 
     def attention(self, b: Buffers, plan: RowPlan, stream) -> None:
         """normed -> att (projections, RoPE, tree attention)."""
         L, T, H, w = capi.lib(), b.rows, self.H, self.w
-        for nm, dst, n in (("q_proj", b.q, QD), ("k_proj", b.k, KD), ("v_proj", b.v, KD)):
-            _call(L.aps_linear(_p(b.normed), _p(w.proj[nm][0]), _p(w.proj[nm][1]), T, H, n, _p(dst), stream))
+        self._project(b, b.normed, (("q_proj", b.q, QD), ("k_proj", b.k, KD), ("v_proj", b.v, KD)), stream)
         c, s = _device_table(b.q.device, plan.max_len, HEAD_DIM, ROPE_THETA)
         _call(L.aps_rope_tree(_p(b.q), _p(b.k), _p(plan.pos), T, NUM_ATTENTION_HEADS, NUM_KV_HEADS, HEAD_DIM,
                               _p(c), _p(s), c.shape[0], stream))
@@ -203,8 +235,7 @@ class DecoderLayer:
                                    stream))
         self.attention(b, plan, stream)
         # attn = att W_o^T + b_o into carry, then carry += x and post = LN(carry)
-        _call(L.aps_linear(_p(b.att), _p(w.proj["o_proj"][0]), _p(w.proj["o_proj"][1]), T, QD, H, _p(b.carry),
-                           stream))
+        self._project(b, b.att, (("o_proj", b.carry, H),), stream)
         _call(L.aps_add_layer_norm(_p(b.carry), _p(b.x), _p(w.post_w), _p(w.post_b), T, H, ctypes.c_float(NORM_EPS),
                                    _p(b.post), stream))
         _call(L.aps_moe_forward(w.moe.handle, _p(b.post), capi.DTYPE_F32, _p(w.gate), T, _p(b.x), capi.DTYPE_F32,
@@ -216,10 +247,25 @@ class Model:
     src/model.cu:45-159) over any number of layers."""
 
     def __init__(self, embeddings: torch.Tensor, norm_w: torch.Tensor, norm_b: torch.Tensor,
-                 lm_head_w: torch.Tensor, lm_head_b: Optional[torch.Tensor], layers: List[LayerWeights]):
+                 lm_head_w: torch.Tensor, lm_head_b: Optional[torch.Tensor], layers: List[LayerWeights],
+                 tc: str = "off"):
+        """tc: "off" (fp32 projections, the reference's default build), "tc"
+        (the split-bf16 Linear, three products, for the LM head and layer
+        31's attention projections: the reference's USE_TC) or "all" (four
+        products, the LM head and every layer's attention projections:
+        USE_TC_ALL)."""
+        if tc not in ("off", "tc", "all"):
+            raise ValueError("tc is 'off', 'tc' or 'all'")
         self.emb, self.norm_w, self.norm_b = embeddings, norm_w, norm_b
         self.head_w, self.head_b = lm_head_w, lm_head_b
-        self.layers = [DecoderLayer(w) for w in layers]
+        terms = None if tc == "off" else (4 if tc == "all" else 3)
+        self.layers = [DecoderLayer(w, terms if (tc == "all" or (tc == "tc" and i == 31)) else None)
+                       for i, w in enumerate(layers)]
+        self.head_terms = terms
+        self.head_tc = None
+        if terms is not None:
+            from .attention import linear_tc_prepare
+            self.head_tc = linear_tc_prepare(lm_head_w)
         self.H = embeddings.shape[1]
         self._bufs: Dict[int, Buffers] = {}
 
@@ -255,7 +301,13 @@ class Model:
         _call(L.aps_gather_rows(_p(b.normed), T, H, _p(plan.last_rows), batch, _p(rows_out), stream))
         V = self.head_w.shape[0]
         logits = torch.empty((batch, V), dtype=torch.float32, device=dev)
-        _call(L.aps_linear(_p(rows_out), _p(self.head_w), _p(self.head_b), batch, H, V, _p(logits), stream))
+        if self.head_tc is not None:
+            xs = torch.empty(2 * batch * H, dtype=torch.int16, device=dev)
+            _call(L.aps_linear_tc_split(_p(rows_out), batch, H, _p(xs), stream))
+            _call(L.aps_linear_tc(_p(xs), batch, H, _p(self.head_tc), _p(self.head_b), V, int(self.head_terms == 4),
+                                  _p(logits), stream))
+        else:
+            _call(L.aps_linear(_p(rows_out), _p(self.head_w), _p(self.head_b), batch, H, V, _p(logits), stream))
         return logits
 
     def generate(self, prompts: Sequence[Sequence[int]]) -> torch.Tensor:

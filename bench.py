@@ -75,6 +75,11 @@ def parse():
                          "first tens of milliseconds of sustained work (5 warm-up + 50 timed steps from idle "
                          "read about 16%% slower than the steady state)")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "load"])
+    ap.add_argument("--proj", default="fp32", choices=["fp32", "tc", "tc_all"],
+                    help="c3 / c4 attention projections: fp32 FMA chains (the reference's default build, bit-exact), "
+                         "or the reference's optional split-bf16 tensor-core Linear: tc = three products (USE_TC; "
+                         "at c4 the LM head and layer 31 as the reference selects), tc_all = four products on every "
+                         "layer (USE_TC_ALL)")
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline: repeat full-batch runs until this much time is spent (at least 2 runs)")
@@ -192,7 +197,8 @@ def decoder_bench(args):
         emb = torch.randn((V, H), generator=g, device=dev)
         head_w = (0.02 * torch.randn((V, H), generator=g, device=dev)).contiguous()
         head_b = (0.02 * torch.randn(V, generator=g, device=dev)).contiguous()
-        model = decoder.Model(emb, torch.ones(H, device=dev), torch.zeros(H, device=dev), head_w, head_b, lws)
+        model = decoder.Model(emb, torch.ones(H, device=dev), torch.zeros(H, device=dev), head_w, head_b, lws,
+                              tc={"fp32": "off", "tc": "tc", "tc_all": "all"}[args.proj])
         plan = decoder.RowPlan.from_prompts(prompts, dev)
         T, tokens = plan.rows, plan.prompt_tokens
 
@@ -206,7 +212,7 @@ def decoder_bench(args):
         plan = decoder.RowPlan.from_prompts(prompts, dev)
         T = tokens = plan.rows
         lws = [decoder.random_layer(H, F, E, dev, g) for _ in range(LAYERS)]
-        layers = [decoder.DecoderLayer(w) for w in lws]
+        layers = [decoder.DecoderLayer(w, {"fp32": None, "tc": 3, "tc_all": 4}[args.proj]) for w in lws]
         bufs = decoder.Buffers.allocate(T, H, lws[0].moe, dev)
         bufs.x.copy_(torch.randn((T, H), generator=g, device=dev))
         bufs.carry.zero_()
@@ -238,18 +244,20 @@ def decoder_bench(args):
     w = layer0.w
     eps = ctypes.c_float(NORM_EPS)
     cos_d, sin_d = decoder._device_table(dev, plan.max_len, 128, decoder.ROPE_THETA)
-    lin = lambda src, nm, dst, k, n: L.aps_linear(p(src), p(w.proj[nm][0]), p(w.proj[nm][1]), T, k, n, p(dst), sptr)
+    def proj(src, names):   # the layer's own projection path (fp32 chains or the split products)
+        layer0._project(bufs, src, names, sptr)
+        return 0
     calls = [
         ("input_layer_norm", lambda: L.aps_add_layer_norm(p(bufs.x), p(bufs.carry), p(w.in_w), p(w.in_b), T, H, eps,
                                                            p(bufs.normed), sptr)),
-        ("qkv_proj", lambda: lin(bufs.normed, "q_proj", bufs.q, H, 2048) or lin(bufs.normed, "k_proj", bufs.k, H, 512)
-         or lin(bufs.normed, "v_proj", bufs.v, H, 512)),
+        ("qkv_proj", lambda: proj(bufs.normed, (("q_proj", bufs.q, 2048), ("k_proj", bufs.k, 512),
+                                                ("v_proj", bufs.v, 512)))),
         ("rope", lambda: L.aps_rope_tree(p(bufs.q), p(bufs.k), p(plan.pos), T, 16, 4, 128, p(cos_d), p(sin_d),
                                          cos_d.shape[0], sptr)),
         ("attention_tree", lambda: L.aps_attention_tree(p(bufs.q), p(bufs.k), p(bufs.v), p(bufs.att), p(plan.pos),
                                                         p(plan.anc), plan.max_len, T, 16, 4, 128,
                                                         decoder.SLIDING_WINDOW, sptr)),
-        ("o_proj", lambda: lin(bufs.att, "o_proj", bufs.carry, 2048, H)),
+        ("o_proj", lambda: proj(bufs.att, (("o_proj", bufs.carry, H),))),
         ("add_layer_norm", lambda: L.aps_add_layer_norm(p(bufs.carry), p(bufs.x), p(w.post_w), p(w.post_b), T, H,
                                                          eps, p(bufs.post), sptr)),
         ("moe_block", lambda: L.aps_moe_forward(w.moe.handle, p(bufs.post), capi.DTYPE_F32, p(w.gate), T, p(bufs.x),
@@ -296,25 +304,42 @@ def decoder_bench(args):
     # order) as chains of K = 1 fp32 MFMAs; MI355X's published fp32 matrix
     # rate is 157.3 TFLOP/s
     proj_s = mt["qkv_proj"] + mt["o_proj"]
-    roofline = {"bound": "mfma", "kernel": "k_linear_mfma (q/k/v/o projections)",
-                "achieved": (qkv_flops + o_flops) / proj_s / 1e12, "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
-                "frac": (qkv_flops + o_flops) / proj_s / PEAK_F32, "traffic": None,
-                "flops_per_launch": (qkv_flops + o_flops) / 4, "launch_us": proj_s / 4 * 1e6}
+    if layer0.tc:
+        # the split products on the bf16 matrix cores: terms x the fp32
+        # FLOPs of bf16 MFMA work per projection (the x split included in
+        # the time), against the 2.5 PFLOP/s dense bf16 peak
+        mma = layer0.tc_terms * (qkv_flops + o_flops)
+        roofline = {"bound": "mfma", "kernel": f"k_linear_tc ({layer0.tc_terms} bf16 products, q/k/v/o projections)",
+                    "achieved": mma / proj_s / 1e12, "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                    "frac": mma / proj_s / PEAK_BF16, "traffic": None, "flops_per_launch": mma / 4,
+                    "launch_us": proj_s / 4 * 1e6, "fp32_equivalent_TFLOP_s": (qkv_flops + o_flops) / proj_s / 1e12}
+    else:
+        roofline = {"bound": "mfma", "kernel": "k_linear_mfma (q/k/v/o projections)",
+                    "achieved": (qkv_flops + o_flops) / proj_s / 1e12, "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
+                    "frac": (qkv_flops + o_flops) / proj_s / PEAK_F32, "traffic": None,
+                    "flops_per_launch": (qkv_flops + o_flops) / 4, "launch_us": proj_s / 4 * 1e6}
+    proj_text = {"fp32": "fp32 q/k/v/o projections with bias",
+                 "tc": "split-bf16 q/k/v/o projections (three bf16 products, the reference's USE_TC arithmetic"
+                       + (", on the LM head and layer 31 as USE_TC selects" if c4 else "") + ")",
+                 "tc_all": "split-bf16 q/k/v/o projections on every layer and the LM head (four bf16 products, "
+                           "USE_TC_ALL)"}[args.proj]
     workload = (f"c4: whole 32-layer random-init model prefill (generate): 16 prompts x 1024 ids, groups of 4 "
                 f"sharing a 512-id prefix, host prefix trie + upload, embedding gather of {T} node rows, 32 "
-                f"decoder layers (LayerNorm+bias, fp32 q/k/v/o projections with bias, 16/4 heads of 128, RoPE, "
+                f"decoder layers (LayerNorm+bias, {proj_text}, 16/4 heads of 128, RoPE, "
                 f"GQA tree attention, bf16 MoE: hidden {H}, {E} experts top-2, ffn {F}), final add+LayerNorm, "
                 f"last-row gather, LM head (vocab {V}); value counts the {tokens} prompt tokens"
                 if c4 else
                 f"c3: one whole decoder layer on the {T} prefix-trie rows of 8 prompts x 512 random ids "
-                f"(LayerNorm+bias, fp32 q/k/v/o projections with bias, 16/4 heads of 128, RoPE, GQA tree "
+                f"(LayerNorm+bias, {proj_text}, 16/4 heads of 128, RoPE, GQA tree "
                 f"attention, residual add+LayerNorm, bf16 MoE: hidden {H}, {E} experts top-2, ffn {F}); steps "
                 f"chain forward_carry through {LAYERS} random-init layers")
     line = {
         "metric": "whole-model prefill tokens/s" if c4 else "decoder-layer prefill tokens/s",
         "value": tokens * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "settle_steps": n_settle, "ms_per_step": ms_per_step, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32 attention, bf16 experts",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 attention, bf16 experts" + ("" if args.proj == "fp32" else
+                                                  f", split-bf16 projections ({'four' if args.proj == 'tc_all' else 'three'} products)"),
         "data": "synthetic (seeded torch normals, random-init weights)",
         "config": {"workload": workload, "tokens": tokens, "rows": T, "hidden": H, "experts": E, "ffn": F,
                    "layers": 32 if c4 else LAYERS},

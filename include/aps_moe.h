@@ -328,6 +328,33 @@ APS_API int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int
 APS_API int aps_linear(const float* x, const float* weight, const float* bias, int64_t rows, int32_t in_features,
                        int32_t out_features, float* y, void* stream);
 
+/* The reference's optional tensor-core Linear (built with USE_TC; USE_TC_ALL
+ * adds the fourth product and applies it to every attention projection,
+ * reference src/layer.cu:16-27).  Not bit-exact: the products are an
+ * approximation of the fp32 chain (see aps_linear_tc).
+ *
+ * Replaces Tensor::prepare_cuda_bf16_weight(with_low_residual = true)
+ * (reference include/tensor.h:41-46, src/tensor.cu:124-177): packs weight
+ * [out][in] fp32 into bf16 hi = bf16(w) and lo = bf16(w - hi) tile images in
+ * `packed` (aps_linear_tc_packed_bytes bytes; 0 for an invalid shape).
+ * in % 64 == 0, out % 4 == 0. */
+APS_API size_t aps_linear_tc_packed_bytes(int32_t out_features, int32_t in_features);
+APS_API int aps_linear_tc_prepare(const float* weight, int32_t out_features, int32_t in_features, void* packed,
+                                  size_t packed_bytes, void* stream);
+/* The on-the-fly split of x in k_matmul_transposed_bf16_wmma (reference
+ * src/tensor.cu:531-543), done once per input: x_split = x_hi [rows][in]
+ * then x_lo [rows][in], bf16 (rows * in * 4 bytes). */
+APS_API int aps_linear_tc_split(const float* x, int64_t rows, int32_t in_features, void* x_split, void* stream);
+/* Replaces matmul_transposed(_bias)_gpu's USE_TC branch (reference
+ * src/tensor.cu:3042-3055, kernel k_matmul_transposed_bf16_wmma :514-584,
+ * bias after the product :3121-3142): y [rows][out] = x_hi W_hi + x_hi W_lo
+ * + x_lo W_hi (+ x_lo W_lo when all_terms), fp32 accumulation on the bf16
+ * MFMA, then + bias[out] when bias is not NULL.  The result is within about
+ * 1e-5 (all_terms: 1e-6) of the fp32 product relative to its scale, not bit
+ * for bit. */
+APS_API int aps_linear_tc(const void* x_split, int64_t rows, int32_t in_features, const void* packed,
+                          const float* bias, int32_t out_features, int32_t all_terms, float* y, void* stream);
+
 /* The RoPE tables of the reference's rope_table (src/tensor.cu:2703-2735),
  * host code: cos/sin [max_seq][head_dim / 2] with inv = powf(theta,
  * (-2 j) / head_dim), cos = cosf(p * inv), sin = sinf(p * inv). */

@@ -57,6 +57,21 @@ public:
     const float* cuda_data() const;
     float* cuda_data_write();
     void sync_cuda_to_host() const;
+    // The split-bf16 weight copy of the reference's tensor-core Linear
+    // (reference include/tensor.h:41-46, src/tensor.cu:149-177): packs this
+    // [out][in] matrix into bf16 hi = bf16(w) and lo = bf16(w - hi) tile
+    // images (lo left zero without with_low_residual); matmul_transposed_gpu
+    // and matmul_transposed_bias_gpu then run the split products
+    // (aps_linear_tc; all four terms when built with USE_TC_ALL).  Matrices
+    // whose in % 64 != 0 or out % 4 != 0 keep the fp32 path (no copy is
+    // made), as the reference's dispatch falls back for shapes its kernel
+    // does not take.  The fp32 device copy is kept.
+    void prepare_cuda_bf16_weight(bool with_low_residual) const;
+    const void* cuda_bf16_weight_hi() const { return bf16_; }
+    const void* cuda_bf16_weight_lo() const {
+        return bf16_ ? static_cast<const char*>(bf16_) + bf16_bytes_ / 2 : nullptr;
+    }
+    bool has_cuda_bf16_weight() const { return bf16_ != nullptr; }
 
 private:
     // Which copies hold the current values: a bit mask of kOnHost / kOnDevice.
@@ -69,6 +84,8 @@ private:
     mutable std::vector<float> host_;
     mutable float* dev_ = nullptr;
     mutable unsigned fresh_ = kOnHost;
+    mutable void* bf16_ = nullptr;        // hi images, then lo images (aps_linear_tc_prepare)
+    mutable std::size_t bf16_bytes_ = 0;
 
     std::size_t flat_index(const std::size_t* idx, std::size_t n) const;
     float* host_current() const;      // host copy brought up to date

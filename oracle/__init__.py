@@ -341,6 +341,38 @@ def model_bin_index(data: bytes):
     return out
 
 
+def bf16_split(v: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """hi = bf16(v), lo = bf16(v - hi), round to nearest even, as fp32 arrays
+    (reference k_pack_bf16_weight and the split in
+    k_matmul_transposed_bf16_wmma, src/tensor.cu:141-145, 537-540)."""
+    def rn(a):
+        u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+        return r.view(np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    hi = rn(v)
+    lo = rn((v - hi).astype(np.float32))   # v - hi is exact in fp32
+    return hi, lo
+
+
+def linear_split_bf16(x: np.ndarray, w: np.ndarray, bias: Optional[np.ndarray] = None,
+                      all_terms: bool = False) -> np.ndarray:
+    """The reference's USE_TC Linear (src/tensor.cu:514-584, 3042-3055,
+    3121-3142): sum over k of x_hi w_hi + x_hi w_lo + x_lo w_hi (+ x_lo w_lo
+    under USE_TC_ALL), then + bias.  The tensor cores' accumulation order is
+    not specified, so this restatement sums the exact bf16 products in fp64
+    and rounds once: the value every fp32 accumulation order approximates."""
+    xh, xl = bf16_split(x)
+    wh, wl = bf16_split(w)
+    xh, xl, wh, wl = (a.astype(np.float64) for a in (xh, xl, wh, wl))
+    y = xh @ wh.T + xh @ wl.T + xl @ wh.T
+    if all_terms:
+        y += xl @ wl.T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    return y.astype(np.float32)
+
+
 SLIDING_WINDOW = 2047   # reference include/config.h:17
 ROPE_THETA = 10000.0    # reference include/config.h:18
 

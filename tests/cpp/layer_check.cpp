@@ -12,6 +12,7 @@
 // and row gather (both overloads) of include/prefix.h and include/tensor.h.  Exit status 0 means every in-process check passed.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -412,6 +413,40 @@ int main(int argc, char** argv) {
             [&] { tensor_ops::attention_tree_gpu(aq, ak, av, ao, pos.data(), anc.data(), trie.max_len, n, 4096, 16, 2,
                                                  hd); },
             "attention_tree_gpu expects GQA-4", "GQA-4 check");
+    }
+
+    // --- the split-bf16 Linear (Tensor::prepare_cuda_bf16_weight) ------------
+    {
+        const std::size_t m = 70, k = 256, n = 132;
+        Tensor lx = random_tensor({m, k}, rng, 1.0f), lw = random_tensor({n, k}, rng, 0.05f),
+               lb = random_tensor({n}, rng, 0.1f);
+        Tensor y32({m, n}), ytc({m, n}), ytc0({m, n});
+        tensor_ops::matmul_transposed_bias_gpu(lx, lw, lb, y32);
+        Tensor lw_tc = lw;                       // a copy does not carry the bf16 images
+        expect(!lw_tc.has_cuda_bf16_weight(), "fresh weight has no bf16 copy");
+        lw_tc.prepare_cuda_bf16_weight(true);
+        expect(lw_tc.has_cuda_bf16_weight() && lw_tc.cuda_bf16_weight_lo() != nullptr, "bf16 copy prepared");
+        tensor_ops::matmul_transposed_bias_gpu(lx, lw_tc, lb, ytc);
+        tensor_ops::matmul_transposed_gpu(lx, lw_tc, ytc0);
+        double worst = 0.0, worst0 = 0.0;
+        bool differs = false;
+        for (std::size_t i = 0; i < m; ++i)
+            for (std::size_t j = 0; j < n; ++j) {
+                double sc = std::fabs(lb.at(j));
+                for (std::size_t q = 0; q < k; ++q) sc += std::fabs(static_cast<double>(lx.at(i, q)) * lw.at(j, q));
+                const double d = std::fabs(static_cast<double>(ytc.at(i, j)) - y32.at(i, j));
+                const double d0 = std::fabs(static_cast<double>(ytc0.at(i, j)) + lb.at(j) - y32.at(i, j));
+                worst = std::max(worst, d / sc);
+                worst0 = std::max(worst0, d0 / sc);
+                differs = differs || ytc.at(i, j) != y32.at(i, j);
+            }
+        expect(worst < 3e-5 && worst0 < 3e-5, "split-bf16 Linear within 3e-5 of the fp32 chain");
+        expect(differs, "the split-bf16 path ran (results differ from the fp32 chain in some bits)");
+        Tensor moved = std::move(lw_tc);
+        expect(moved.has_cuda_bf16_weight() && !lw_tc.has_cuda_bf16_weight(), "a move carries the bf16 copy");
+        Tensor v3({4});
+        expect_throw<std::invalid_argument>([&] { v3.prepare_cuda_bf16_weight(true); },
+                                            "BF16 packing requires a matrix", "bf16 packing of a vector");
     }
 
     // --- Tensor synchronisation rules ----------------------------------------

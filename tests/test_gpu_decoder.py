@@ -132,6 +132,59 @@ def test_c3_decoder_layer_parity(gpu_device):
     lw.release()
 
 
+def test_decoder_layer_split_bf16_projections(gpu_device):
+    """The layer with the reference's optional split-bf16 projections
+    (USE_TC_ALL's four products): q, k, v and o equal the oracle's split
+    products within fp32 accumulation error and the fp32 chain within the
+    split's error; the layer output stays with the fp32-projection layer's
+    (routes agree but for near ties, outputs of agreeing rows within the bf16
+    block's tolerance)."""
+    import ctypes
+    H = 4096
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, 32064, 256).tolist() for _ in range(2)]
+    note("decoder layer, split-bf16 projections (four products): 2 prompts x 256")
+    W = c3_layer_weights(H, seed=31)
+    Wd = {k: torch.from_numpy(v).to(gpu_device) for k, v in W.items()}
+    lw = decoder.layer_from_tensors(Wd, 0, moe_dtype=torch.bfloat16)
+    del Wd
+    plan = decoder.RowPlan.from_prompts(prompts, gpu_device)
+    x = rng.standard_normal((plan.rows, H), dtype=np.float32)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(gpu_device).cuda_stream)
+    outs = {}
+    for terms in (None, 4):
+        layer = decoder.DecoderLayer(lw, terms)
+        b = decoder.Buffers.allocate(plan.rows, H, lw.moe, gpu_device)
+        b.x.copy_(torch.from_numpy(x))
+        layer.forward_carry(b, plan, False, stream)
+        torch.cuda.synchronize()
+        outs[terms] = ({nm: getattr(b, nm).cpu().numpy() for nm in ("x", "normed", "v", "att", "carry")},
+                       decoder.routes_view(b, lw.moe).cpu().numpy().astype(np.int32))
+    got, routes = outs[4]
+    ref, ref_routes = outs[None]
+    L = model_chain.layer_weights(W, 0)
+    normed = got["normed"]
+    assert np.array_equal(bits(normed), bits(ref["normed"])), "the input LayerNorm does not depend on the mode"
+    wv, bv = L["attn"]["v_proj"]
+    scale = np.abs(normed).astype(np.float64) @ np.abs(wv).astype(np.float64).T + np.abs(bv)
+    e_split = (np.abs(got["v"] - oracle.linear_split_bf16(normed, wv, bv, all_terms=True)) / scale).max()
+    e_f32 = (np.abs(got["v"] - oracle.linear(normed, wv, bv)) / scale).max()
+    note(f"v projection: max error / scale vs split products {e_split:.2e}, vs fp32 chain {e_f32:.2e}")
+    assert e_split < 2e-6 and e_f32 < 5e-6
+    wo, bo = L["attn"]["o_proj"]
+    att = got["att"]
+    o_want = oracle.linear_split_bf16(att, wo, bo, all_terms=True) + x
+    o_scale = np.abs(att).astype(np.float64) @ np.abs(wo).astype(np.float64).T + np.abs(bo) + np.abs(x)
+    e_o = (np.abs(got["carry"] - o_want) / o_scale).max()
+    note(f"o projection + residual: max error / scale vs split products {e_o:.2e}")
+    assert e_o < 2e-6
+    agree = (routes == ref_routes).all(axis=1)
+    err = rowwise_err(got["x"][agree], ref["x"][agree])
+    note(f"routes agree on {agree.mean():.4f} of rows; output vs fp32-projection layer max normwise {err.max():.2e}")
+    assert agree.mean() > 0.99 and err.max() < 2e-2
+    lw.release()
+
+
 def _c4_model_weights(device, H=4096, F=448, E=16, V=32064, layers=32, seed=5):
     """Random-init model weights drawn on the device (name -> tensor): linear
     and expert weights, projection and LM-head biases ~N(0, 0.02), LayerNorm
@@ -201,4 +254,31 @@ def test_c4_whole_model_dedup_and_routing_agreement(gpu_device):
     assert agree[0] == 1.0  # identical router inputs: identical routes
     assert min(agree) > 0.5
     for lw in lw32:
+        lw.release()
+
+
+def test_model_split_bf16_projections_and_lm_head(gpu_device):
+    """Model(tc="all"): every layer's projections and the LM head on the
+    split-bf16 Linear (four products).  Two layers, vocab 1000: the logits
+    stay with the fp32-projection model's (normwise, routes agree but for
+    near ties), and the LM head alone equals the oracle's split products."""
+    layers, V = 2, 1000
+    prompts = [list(range(1, 40)), list(range(1, 25)) + [7, 8, 9], [500, 3, 2]]
+    note("model with split-bf16 projections and LM head (four products): 2 layers, vocab 1000")
+    W = _c4_model_weights(gpu_device, V=V, layers=layers, seed=8)
+    lws = [decoder.layer_from_tensors(W, i, moe_dtype=torch.bfloat16) for i in range(layers)]
+    args = (W["model.embed_tokens.weight"], W["model.norm.weight"], W["model.norm.bias"], W["lm_head.weight"],
+            W["lm_head.bias"], lws)
+    plan = decoder.RowPlan.from_prompts(prompts, gpu_device)
+    m32, mtc = decoder.Model(*args), decoder.Model(*args, tc="all")
+    assert all(l.tc_terms == 4 for l in mtc.layers) and mtc.head_tc is not None
+    l32 = m32.prefill(plan)
+    ltc = mtc.prefill(plan)
+    torch.cuda.synchronize()
+    err = rowwise_err(ltc.cpu().numpy(), l32.cpu().numpy())
+    note(f"logits split-bf16 vs fp32 projections: max normwise err {err.max():.2e}")
+    assert err.max() < 2e-2 and np.isfinite(ltc.cpu().numpy()).all()
+    with pytest.raises(ValueError):
+        decoder.Model(*args, tc="bf16")
+    for lw in lws:
         lw.release()
