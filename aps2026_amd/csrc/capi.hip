@@ -635,6 +635,41 @@ int aps_linear_tc(const void* x_split, int64_t rows, int32_t in_features, const 
     return APS_OK;
 }
 
+int aps_linear_tc_multi(const void* x_split, int64_t rows, int32_t in_features, int32_t count,
+                        const void* const* packed, const float* const* biases, const int32_t* out_features,
+                        int32_t all_terms, float* const* ys, void* stream) {
+    if (count < 1 || count > 3 || !out_features)
+        return fail(APS_ERR_SHAPE, "split-bf16 linear multi: count %d (1..3)", count);
+    if (rows < 0 || in_features <= 0 || in_features % 64 != 0 || (rows + 127) / 128 > 65535)
+        return fail(APS_ERR_SHAPE, "split-bf16 linear multi shape: rows %lld in %d (multiple of 64)",
+                    (long long)rows, in_features);
+    for (int32_t j = 0; j < count; ++j)
+        if (out_features[j] <= 0 || out_features[j] % 4 != 0)
+            return fail(APS_ERR_SHAPE, "split-bf16 linear multi: out %d of output %d (multiple of 4)",
+                        out_features[j], j);
+    if (rows == 0) return APS_OK;
+    if (!x_split || !packed || !ys) return fail(APS_ERR_ARG, "split-bf16 linear multi: NULL pointer");
+    const uint16_t* pk[3] = {};
+    const float* bs[3] = {};
+    for (int32_t j = 0; j < count; ++j) {
+        pk[j] = static_cast<const uint16_t*>(packed[j]);
+        bs[j] = biases ? biases[j] : nullptr;
+        if (!pk[j] || !ys[j]) return fail(APS_ERR_ARG, "split-bf16 linear multi: NULL pointer (output %d)", j);
+        if (((reinterpret_cast<uintptr_t>(pk[j]) | reinterpret_cast<uintptr_t>(bs[j]) |
+              reinterpret_cast<uintptr_t>(ys[j]) | reinterpret_cast<uintptr_t>(x_split)) & 15u) != 0)
+            return fail(APS_ERR_ARG, "split-bf16 linear multi: arrays must be 16-byte aligned");
+        for (int32_t i = 0; i < j; ++i)
+            if (ys[i] == ys[j])
+                return fail(APS_ERR_ARG, "split-bf16 linear multi: outputs %d and %d are the same array", i, j);
+    }
+    const int64_t n = rows * in_features;
+    const uint16_t* hi = static_cast<const uint16_t*>(x_split);
+    APS_HIP(aps::launch_linear_tc_multi(hi, hi + n, count, pk, bs, ys, out_features, rows, in_features,
+                                        all_terms != 0, static_cast<hipStream_t>(stream)),
+            "split-bf16 linear multi launch");
+    return APS_OK;
+}
+
 int aps_rope_table(int64_t max_seq, int32_t head_dim, float theta, float* cos_out, float* sin_out) {
     if (max_seq < 0 || head_dim <= 0 || head_dim % 2 != 0)
         return fail(APS_ERR_SHAPE, "rope table shape: max_seq %lld head_dim %d", (long long)max_seq, head_dim);

@@ -182,6 +182,10 @@ hipError_t launch_linear_tc_prepare(const float* w, int out_f, int in_f, uint16_
 hipError_t launch_split_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t s);
 hipError_t launch_linear_tc(const uint16_t* xhi, const uint16_t* xlo, const uint16_t* packed, const float* bias,
                             float* y, int64_t rows, int in_f, int out_f, bool all_terms, hipStream_t s);
+// up to three outputs of one split input in one launch
+hipError_t launch_linear_tc_multi(const uint16_t* xhi, const uint16_t* xlo, int count, const uint16_t* const* packed,
+                                  const float* const* bias, float* const* y, const int* out_f, int64_t rows, int in_f,
+                                  bool all_terms, hipStream_t s);
 
 // y = x w^T (+ bias): fp32 FMA chain over k ascending per output, bias added
 // once (in_f % 16 == 0, out_f % 4 == 0).

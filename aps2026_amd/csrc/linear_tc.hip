@@ -105,15 +105,35 @@ k_pack_split(const float* __restrict__ w, uint16_t* __restrict__ img, int N, int
     img[per_set + i] = l;
 }
 
+// Up to three outputs of one input (q, k and v): segment j is y[j]
+// [M][n[j]] from packed weights w[j], column blocks t0[j] .. t0[j + 1] - 1 of
+// the grid's x dimension.
+struct TcSegs {
+    const uint16_t* w[3];
+    const float* b[3];
+    float* y[3];
+    int64_t per_set[3];
+    int n[3];
+    int t0[4];
+};
+
 template <bool ALL>
 __global__ void __launch_bounds__(256, 1)
-k_linear_tc(const uint16_t* __restrict__ xhi, const uint16_t* __restrict__ xlo, const uint16_t* __restrict__ img,
-            int64_t per_set, const float* __restrict__ bias, float* __restrict__ y, int64_t M, int K, int N) {
+k_linear_tc(const uint16_t* __restrict__ xhi, const uint16_t* __restrict__ xlo, const TcSegs segs, int64_t M,
+            int K) {
     __shared__ __align__(16) uint8_t ring[2][kTcStageBytes];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kTcRows;
-    const int nb = blockIdx.x;
+    // this block's segment (selects, so the argument block stays in scalar registers)
+    const int bx = blockIdx.x;
+    const int sg = (bx >= segs.t0[1]) + (bx >= segs.t0[2]);
+    const uint16_t* __restrict__ img = sg == 0 ? segs.w[0] : sg == 1 ? segs.w[1] : segs.w[2];
+    const float* __restrict__ bias = sg == 0 ? segs.b[0] : sg == 1 ? segs.b[1] : segs.b[2];
+    float* __restrict__ y = sg == 0 ? segs.y[0] : sg == 1 ? segs.y[1] : segs.y[2];
+    const int64_t per_set = sg == 0 ? segs.per_set[0] : sg == 1 ? segs.per_set[1] : segs.per_set[2];
+    const int N = sg == 0 ? segs.n[0] : sg == 1 ? segs.n[1] : segs.n[2];
+    const int nb = bx - (sg == 0 ? segs.t0[0] : sg == 1 ? segs.t0[1] : segs.t0[2]);
     const int KT = K / 64;
     const int64_t row_bytes = static_cast<int64_t>(K) * 2;
 
@@ -233,20 +253,36 @@ hipError_t launch_split_bf16(const float* x, int64_t n, uint16_t* hi, uint16_t* 
     return hipGetLastError();
 }
 
+hipError_t launch_linear_tc_multi(const uint16_t* xhi, const uint16_t* xlo, int count, const uint16_t* const* packed,
+                                  const float* const* bias, float* const* y, const int* out_f, int64_t rows, int in_f,
+                                  bool all_terms, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (count < 1 || count > 3 || in_f <= 0 || in_f % 64 != 0 || ceil_div(rows, kTcRows) > 65535)
+        return hipErrorInvalidValue;
+    TcSegs segs{};
+    int t = 0;
+    for (int j = 0; j < 3; ++j) {
+        segs.t0[j] = t;
+        const int jj = j < count ? j : 0;   // unused segments: never selected (their t0 is the tile count)
+        if (out_f[jj] <= 0 || out_f[jj] % 4 != 0) return hipErrorInvalidValue;
+        segs.w[j] = packed[jj];
+        segs.b[j] = bias[jj];
+        segs.y[j] = y[jj];
+        segs.n[j] = out_f[jj];
+        segs.per_set[j] = linear_tc_packed_elems(out_f[jj], in_f) / 2;
+        if (j < count) t += static_cast<int>(ceil_div(out_f[j], kTcCols));
+    }
+    segs.t0[3] = t;
+    for (int j = count; j < 3; ++j) segs.t0[j] = t;
+    const dim3 grid(static_cast<unsigned>(t), static_cast<unsigned>(ceil_div(rows, kTcRows)));
+    if (all_terms) hipLaunchKernelGGL(k_linear_tc<true>, grid, dim3(256), 0, s, xhi, xlo, segs, rows, in_f);
+    else hipLaunchKernelGGL(k_linear_tc<false>, grid, dim3(256), 0, s, xhi, xlo, segs, rows, in_f);
+    return hipGetLastError();
+}
+
 hipError_t launch_linear_tc(const uint16_t* xhi, const uint16_t* xlo, const uint16_t* packed, const float* bias,
                             float* y, int64_t rows, int in_f, int out_f, bool all_terms, hipStream_t s) {
-    if (rows <= 0) return hipSuccess;
-    if (in_f <= 0 || in_f % 64 != 0 || out_f <= 0 || out_f % 4 != 0 || ceil_div(rows, kTcRows) > 65535)
-        return hipErrorInvalidValue;
-    const int64_t per_set = linear_tc_packed_elems(out_f, in_f) / 2;
-    const dim3 grid(static_cast<unsigned>(ceil_div(out_f, kTcCols)), static_cast<unsigned>(ceil_div(rows, kTcRows)));
-    if (all_terms)
-        hipLaunchKernelGGL(k_linear_tc<true>, grid, dim3(256), 0, s, xhi, xlo, packed, per_set, bias, y, rows, in_f,
-                           out_f);
-    else
-        hipLaunchKernelGGL(k_linear_tc<false>, grid, dim3(256), 0, s, xhi, xlo, packed, per_set, bias, y, rows, in_f,
-                           out_f);
-    return hipGetLastError();
+    return launch_linear_tc_multi(xhi, xlo, 1, &packed, &bias, &y, &out_f, rows, in_f, all_terms, s);
 }
 
 }  // namespace aps

@@ -203,10 +203,14 @@ class DecoderLayer:
         (x split once for all of them)."""
         L, T, K = capi.lib(), b.rows, src.shape[1]
         if self.tc:
+            # every output of the input in one launch (their column blocks share the grid)
             xs = b.split(src, stream)
-            for nm, dst, n in names:
-                _call(L.aps_linear_tc(_p(xs), T, K, _p(self.tc[nm]), _p(self.w.proj[nm][1]), n,
-                                      int(self.tc_terms == 4), _p(dst), stream))
+            cnt = len(names)
+            vp = ctypes.c_void_p * cnt
+            _call(L.aps_linear_tc_multi(_p(xs), T, K, cnt, vp(*[_p(self.tc[nm]) for nm, _, _ in names]),
+                                        vp(*[_p(self.w.proj[nm][1]) for nm, _, _ in names]),
+                                        (ctypes.c_int32 * cnt)(*[n for _, _, n in names]), int(self.tc_terms == 4),
+                                        vp(*[_p(dst) for _, dst, _ in names]), stream))
         else:
             for nm, dst, n in names:
                 _call(L.aps_linear(_p(src), _p(self.w.proj[nm][0]), _p(self.w.proj[nm][1]), T, K, n, _p(dst),

@@ -354,6 +354,15 @@ APS_API int aps_linear_tc_split(const float* x, int64_t rows, int32_t in_feature
  * for bit. */
 APS_API int aps_linear_tc(const void* x_split, int64_t rows, int32_t in_features, const void* packed,
                           const float* bias, int32_t out_features, int32_t all_terms, float* y, void* stream);
+/* PhiAttention's q, k and v projections on the split-bf16 Linear (the
+ * reference's q_proj_.forward, then k_proj_ / v_proj_.forward when their
+ * weights carry the bf16 copy, src/layer.cu:159-172) in one launch:
+ * aps_linear_tc for each of `count` (1..3) outputs of the same x_split,
+ * whose column blocks share the grid (the narrow k / v outputs alone would
+ * fill few CUs).  Outputs distinct; biases or biases[j] may be NULL. */
+APS_API int aps_linear_tc_multi(const void* x_split, int64_t rows, int32_t in_features, int32_t count,
+                                const void* const* packed, const float* const* biases, const int32_t* out_features,
+                                int32_t all_terms, float* const* ys, void* stream);
 
 /* The RoPE tables of the reference's rope_table (src/tensor.cu:2703-2735),
  * host code: cos/sin [max_seq][head_dim / 2] with inv = powf(theta,

@@ -86,3 +86,32 @@ def test_linear_tc_gpu_matches_the_split_products(gpu_device, rows, k, n, all_te
     assert err_emu < 2e-6
     assert err_f32 < (3e-5 if not all_terms else 5e-6)
     assert np.isfinite(got).all()
+
+
+@pytest.mark.gpu
+def test_linear_tc_multi_equals_single_launches(gpu_device):
+    """aps_linear_tc_multi (q, k and v of one split input in one launch)
+    equals one aps_linear_tc per output bit for bit."""
+    import ctypes
+    from aps2026_amd import attention, capi
+    from aps2026_amd.moe import _ptr, _stream
+    rows, k, ns = 300, 512, (256, 132, 64)
+    print(f"[case] linear tc multi rows={rows} k={k} ns={ns}", flush=True)
+    rng = np.random.default_rng(4)
+    x = torch.from_numpy(rng.standard_normal((rows, k)).astype(np.float32)).to(gpu_device)
+    ws = [torch.from_numpy((0.02 * rng.standard_normal((n, k))).astype(np.float32)).to(gpu_device) for n in ns]
+    bs = [torch.from_numpy((0.1 * rng.standard_normal(n)).astype(np.float32)).to(gpu_device) for n in ns]
+    bs[1] = None
+    packed = [attention.linear_tc_prepare(w) for w in ws]
+    xs = attention.linear_tc_split(x)
+    for all_terms in (False, True):
+        want = [attention.linear_tc_gpu(xs, p, n, b, all_terms) for p, n, b in zip(packed, ns, bs)]
+        got = [torch.empty_like(w_) for w_ in want]
+        vp = ctypes.c_void_p * 3
+        rc = capi.lib().aps_linear_tc_multi(_ptr(xs), rows, k, 3, vp(*[_ptr(p) for p in packed]),
+                                            vp(*[_ptr(b) for b in bs]), (ctypes.c_int32 * 3)(*ns), int(all_terms),
+                                            vp(*[_ptr(g) for g in got]), _stream(x.device))
+        assert rc == 0, capi.last_error()
+        torch.cuda.synchronize()
+        for g, w_ in zip(got, want):
+            assert torch.equal(g.view(torch.int32), w_.view(torch.int32))
