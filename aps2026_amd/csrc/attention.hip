@@ -309,7 +309,10 @@ k_attention_group(const float* __restrict__ q, const float* __restrict__ k, cons
         }
         for (; w <= h0; w += 16) srow[w] = static_cast<float>(exp(static_cast<double>(__fsub_rn(srow[w], mq))));
         // the denominator in key order on the query's first lane (the
-        // wave's LDS accesses complete in program order), 16 reads ahead
+        // wave's LDS accesses complete in program order), 16 reads ahead;
+        // the wave barrier keeps the compiler from moving the other lanes'
+        // stores past that lane's reads (they communicate through LDS)
+        __builtin_amdgcn_wave_barrier();
         float den = 0.0f;
         if (part == 0) {
             int x = l0;

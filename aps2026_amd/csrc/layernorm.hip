@@ -81,6 +81,10 @@ k_layer_norm(float* __restrict__ x, const float* __restrict__ residual, const fl
             }
             *reinterpret_cast<lf4*>(&stage[c & 1][rr][4 * lane]) = v;
         }
+        // every lane stages its pieces, then the chain lanes read whole
+        // rows: the wave barrier keeps the compiler from running the two on
+        // divergent paths one after the other (a data race between lanes)
+        __builtin_amdgcn_wave_barrier();
     };
     // one staged pass over the rows; step(acc, v) folds four values in order
     auto pass = [&](bool with_residual, auto step) {
