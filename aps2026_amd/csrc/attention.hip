@@ -134,7 +134,7 @@ __device__ inline void rows_transpose4(af4& x) {
 // at its +0 start.
 //   K and V go from global memory straight to registers (LDS holds only the
 // scores and the chain's key rows, so two workgroups fit a CU at 1,024-key
-// windows).  Scores: wave w takes the 16-key tiles w, w + 4, ..; a lane
+// windows, and three, MINB = 3 with 168 registers, at key spans up to 784).  Scores: wave w takes the 16-key tiles w, w + 4, ..; a lane
 // (key lane % 16, row j = lane / 16) loads 16 bytes of elements 16 a + 4 j ..
 // per a < 8 and a 4 x 4 transpose across the rows gives it d = 4 i + j,
 // tiles two ahead in flight.  Softmax: the 16 threads of query q are in
@@ -144,8 +144,8 @@ __device__ inline void rows_transpose4(af4& x) {
 // dimensions 64 w' .. 64 w' + 63, one coalesced 256-byte load per key, 64
 // keys ahead; the K / V row offsets are 32-bit byte offsets off a uniform
 // base.
-template <bool PACKED>
-__global__ void __launch_bounds__(256, 2)
+template <bool PACKED, int MINB>
+__global__ void __launch_bounds__(256, MINB)
 k_attention_group(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
                   float* __restrict__ out, const uint32_t* __restrict__ row_pos, const uint32_t* __restrict__ anc,
                   int64_t anc_stride, int64_t rows, int q_heads, int kv_heads, int wmax, float scale, int sw) {
@@ -555,7 +555,13 @@ hipError_t launch_attention_tree(const float* q, const float* k, const float* v,
                        ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                          reinterpret_cast<uintptr_t>(v)) & 15u) == 0;
     if (group) {
-        auto gk = packed ? &k_attention_group<true> : &k_attention_group<false>;
+        // three workgroups per CU (registers trimmed to 168) when three key
+        // ranges fit the LDS, else two.  (Splitting one launch into a long-
+        // and a short-range launch lost more to the first one's tail than
+        // the short ranges gained.)
+        const bool three = 3 * (glds + 384) <= 160 * 1024;
+        auto gk = three ? (packed ? &k_attention_group<true, 3> : &k_attention_group<false, 3>)
+                        : (packed ? &k_attention_group<true, 2> : &k_attention_group<false, 2>);
         if (glds > 65536) {
             const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gk),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(glds));
