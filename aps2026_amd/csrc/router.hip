@@ -200,8 +200,11 @@ __device__ inline uint32_t r_pack2_bf16(float lo, float hi) {
 // stage holds GW windows; H is a multiple of GW * 128, so every stage is full
 // and the step sequence has no run-time bounds (the compiler can then count
 // the LDS reads in flight instead of draining them).
-template <bool XBF16, int R, int GW, bool XCOPY = false>
-__global__ void __launch_bounds__(256 * R)
+// NWV waves per 16 R lanes of experts: 4 (16 tokens per workgroup) or, for
+// R = 1 and large batches, 8 (32 tokens): the gate then streams once per 32
+// tokens instead of once per 16, half the gate copies per CU.
+template <bool XBF16, int R, int GW, bool XCOPY = false, int NWV = 4>
+__global__ void __launch_bounds__(64 * NWV * R)
 k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, int E,
          float* __restrict__ logits, uint8_t* __restrict__ routes, uint8_t* __restrict__ tile_bytes,
          bf16_t* __restrict__ xcopy) {
@@ -216,17 +219,21 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
     // the stage being read as distinct memory
     __shared__ __align__(16) uint8_t ring0[kStageBytes];
     __shared__ __align__(16) uint8_t ring1[kStageBytes];
-    __shared__ uint32_t cnt[16 * R];
+    constexpr int kWaves = NWV * R;            // waves per workgroup
+    constexpr int kTok = 4 * NWV;              // tokens per workgroup
+    constexpr int kQ = kTok / kRTokens;        // routing-tile quarters per workgroup
+    static_assert(R == 1 || NWV == 4, "eight-wave workgroups for E <= 16");
+    __shared__ uint32_t cnt[kQ][16 * R];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gr = 4 * w + (lane >> 4);        // row of the workgroup, 0 .. 16R-1
     const int e = (gr % R) * 16 + (lane & 15); // this lane's expert
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kRTokens + gr / R;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kTok + gr / R;
     const int NW = H / kRWin;
     const int NG = NW / kGW;
-    if (tid < 16 * R) cnt[tid] = 0u;
+    if (tid < kQ * 16 * R) cnt[tid / (16 * R)][tid % (16 * R)] = 0u;
 
     // x: lane i of a row reads elements 8i .. 8i+7 of every window of its
     // token (rows past the end re-read the last row; their results are
@@ -234,15 +241,17 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
     const uint8_t* xsrc = static_cast<const uint8_t*>(xv) +
                           ((t < rows ? t : rows - 1) * static_cast<int64_t>(H) + 8 * (lane & 15)) * kElt;
     bf16_t* xdst = XCOPY ? xcopy + (t < rows ? t : rows - 1) * static_cast<int64_t>(H) + 8 * (lane & 15) : nullptr;
-    // gate copies: copy i of a stage (i = 0 .. 2 kGW - 1) is instruction
-    // a = w + 4R i of the stage and fills bytes [a KB, a KB + 1 KB): window
-    // i / 2 of the stage, piece (w + 4R (i % 2)) * 64 + lane of the window,
-    // i.e. k/4 = piece / 16R and expert piece % 16R.  Padding experts read
-    // row E-1 (unused).
-    const float* gsrc[2];
+    // gate copies: a window is 8 R copies of 1 KB; copy i of a stage
+    // (i = 0 .. 8 R kGW / kWaves - 1) is instruction a = w + kWaves i of the
+    // stage and fills bytes [a KB, a KB + 1 KB): window a / 8R of the stage,
+    // piece (a % 8R) * 64 + lane of the window, i.e. k/4 = piece / 16R and
+    // expert piece % 16R.  Padding experts read row E-1 (unused).
+    constexpr int kPieces = 8 * R / kWaves > 0 ? 8 * R / kWaves : 1;   // distinct pieces per lane
+    constexpr int kCopies = 8 * R * kGW / kWaves;                     // copies per wave per stage
+    const float* gsrc[kPieces];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int piece = (w + 4 * R * p) * 64 + lane;
+    for (int p = 0; p < kPieces; ++p) {
+        const int piece = (w + kWaves * p) * 64 + lane;
         const int ge = piece % (16 * R);
         gsrc[p] = gate + static_cast<int64_t>(ge < E ? ge : E - 1) * H + 4 * (piece / (16 * R));
     }
@@ -250,9 +259,9 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
         uint8_t* slot = decltype(par)::value ? ring1 : ring0;
         const int v0 = g * kGW;
 #pragma unroll
-        for (int i = 0; i < 2 * kGW; ++i)
-            __builtin_amdgcn_global_load_lds(APS_RGP(gsrc[i & 1] + (v0 + i / 2) * kRWin),
-                                             APS_RLP(slot + (w + 4 * R * i) * 1024), 16, 0, 0);
+        for (int i = 0; i < kCopies; ++i)
+            __builtin_amdgcn_global_load_lds(APS_RGP(gsrc[i % kPieces] + (v0 + i / kPieces) * kRWin),
+                                             APS_RLP(slot + (w + kWaves * i) * 1024), 16, 0, 0);
     };
     ru32x4_t xr[2][kGW][kXv];
     auto issue_x = [&](ru32x4_t (&dst)[kGW][kXv], int g) {
@@ -316,14 +325,14 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
         if (g + 2 < NG) issue_gate(par, g + 2);
     };
 
-    // stage 0 needs its gate and x; stage 1's gate copies (the last 2 kGW
+    // stage 0 needs its gate and x; stage 1's gate copies (the last kCopies
     // per wave) may stay in flight.  With a single stage the second slot is
     // filled with stage 0 again (unused), so the wait is the same on every
     // path and the compiler sees the x registers complete.
     issue_gate(RInt<0>{}, 0);
     issue_x(xr[0], 0);
     issue_gate(RInt<1>{}, NG > 1 ? 1 : 0);
-    r_wait_vm<2 * kGW>();
+    r_wait_vm<kCopies>();
     r_barrier();
     for (int g = 0; g < NG; g += 2) {
         run_stage(RInt<0>{}, g);
@@ -354,15 +363,17 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
         routes[2 * t] = static_cast<uint8_t>(first);
         routes[2 * t + 1] = static_cast<uint8_t>(second);
     }
-    if (valid && e < E && (e == first || e == second)) atomicAdd(&cnt[e], 1u);
+    if (valid && e < E && (e == first || e == second)) atomicAdd(&cnt[(gr / R) / kRTokens][e], 1u);
     __syncthreads();
-    if (tid < E) {
-        // byte (blockIdx % 4) of word [tile][expert]; the last workgroup also
+    if (tid < kQ * E) {
+        // byte (quarter % 4) of word [tile][expert]; the last workgroup also
         // zeroes the bytes of quarters past the end
-        const int sub = blockIdx.x % 4;
-        uint8_t* word = tile_bytes + (static_cast<int64_t>(blockIdx.x / 4) * E + tid) * 4;
-        word[sub] = static_cast<uint8_t>(cnt[tid]);
-        if (blockIdx.x == gridDim.x - 1)
+        const int qi = tid / E, ex = tid % E;
+        const int64_t quarter = static_cast<int64_t>(blockIdx.x) * kQ + qi;
+        const int sub = static_cast<int>(quarter % 4);
+        uint8_t* word = tile_bytes + ((quarter / 4) * E + ex) * 4;
+        word[sub] = static_cast<uint8_t>(cnt[qi][ex]);
+        if (blockIdx.x == gridDim.x - 1 && qi == kQ - 1)
             for (int s2 = sub + 1; s2 < 4; ++s2) word[s2] = 0;
     }
 }
@@ -410,30 +421,38 @@ hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t 
         return hipErrorInvalidValue;
     if (routes && (experts < 2 || !tile_counts)) return hipErrorInvalidValue;
     if (x_copy && x_bf16) return hipErrorInvalidValue;
-    const dim3 grid(static_cast<unsigned>(ceil_div(rows, kRTokens)));
     auto* tb = reinterpret_cast<uint8_t*>(tile_counts);
-#define APS_ROUTER_LAUNCH(XB, R, GW)                                                                      \
-    do {                                                                                                  \
-        if (!(XB) && x_copy)                                                                             \
-            hipLaunchKernelGGL((k_router<false, R, GW, true>), grid, dim3(256 * R), 0, s, x, gate, rows, \
-                               hidden, experts, logits, routes, tb, x_copy);                             \
-        else                                                                                             \
-            hipLaunchKernelGGL((k_router<XB, R, GW>), grid, dim3(256 * R), 0, s, x, gate, rows, hidden,  \
-                               experts, logits, routes, tb, nullptr);                                    \
-    } while (0)
     // windows per stage: 512 steps of 16 R experts (32 KB) when H allows
     const int R = experts <= 16 ? 1 : experts <= 32 ? 2 : 4;
     const bool wide = hidden % (4 * kRWin) == 0;
+    // 32-token workgroups when 16-token ones would put two on some CU and
+    // 32-token ones at most one on each (C5's 8,192 tokens): the CU then
+    // streams the gate once for its 32 tokens.  Past that (C4's 10,240 rows)
+    // some CUs would hold two 32-token workgroups, which measured slower.
+    const int64_t cus = num_cus();
+    const bool eight = R == 1 && wide && rows > kRTokens * cus && ceil_div(rows, 2 * kRTokens) <= cus;
+    const dim3 grid(static_cast<unsigned>(ceil_div(rows, eight ? 2 * kRTokens : kRTokens)));
+#define APS_ROUTER_LAUNCH(XB, R, GW, NWV)                                                                     \
+    do {                                                                                                      \
+        if (!(XB) && x_copy)                                                                                 \
+            hipLaunchKernelGGL((k_router<false, R, GW, true, NWV>), grid, dim3(64 * NWV * R), 0, s, x, gate, \
+                               rows, hidden, experts, logits, routes, tb, x_copy);                           \
+        else                                                                                                 \
+            hipLaunchKernelGGL((k_router<XB, R, GW, false, NWV>), grid, dim3(64 * NWV * R), 0, s, x, gate,   \
+                               rows, hidden, experts, logits, routes, tb, nullptr);                          \
+    } while (0)
     if (x_bf16) {
-        if (R == 1 && wide) APS_ROUTER_LAUNCH(true, 1, 4);
-        else if (R == 1) APS_ROUTER_LAUNCH(true, 1, 2);
-        else if (R == 2) APS_ROUTER_LAUNCH(true, 2, 2);
-        else APS_ROUTER_LAUNCH(true, 4, 1);
+        if (eight) APS_ROUTER_LAUNCH(true, 1, 4, 8);
+        else if (R == 1 && wide) APS_ROUTER_LAUNCH(true, 1, 4, 4);
+        else if (R == 1) APS_ROUTER_LAUNCH(true, 1, 2, 4);
+        else if (R == 2) APS_ROUTER_LAUNCH(true, 2, 2, 4);
+        else APS_ROUTER_LAUNCH(true, 4, 1, 4);
     } else {
-        if (R == 1 && wide) APS_ROUTER_LAUNCH(false, 1, 4);
-        else if (R == 1) APS_ROUTER_LAUNCH(false, 1, 2);
-        else if (R == 2) APS_ROUTER_LAUNCH(false, 2, 2);
-        else APS_ROUTER_LAUNCH(false, 4, 1);
+        if (eight) APS_ROUTER_LAUNCH(false, 1, 4, 8);
+        else if (R == 1 && wide) APS_ROUTER_LAUNCH(false, 1, 4, 4);
+        else if (R == 1) APS_ROUTER_LAUNCH(false, 1, 2, 4);
+        else if (R == 2) APS_ROUTER_LAUNCH(false, 2, 2, 4);
+        else APS_ROUTER_LAUNCH(false, 4, 1, 4);
     }
 #undef APS_ROUTER_LAUNCH
     return hipGetLastError();

@@ -220,6 +220,37 @@ def test_router_kernel_shapes(gpu_device, E, H):
         w.release()
 
 
+@pytest.mark.parametrize("E,T", [(16, 8192), (16, 5000), (8, 4097), (2, 7777)])
+def test_router_32_token_workgroups(gpu_device, E, T):
+    """Batches of 4,097 .. 8,192 tokens with E <= 16 (on a 256-CU MI355X)
+    take the eight-wave router, 32 tokens per workgroup, two quarter-tile
+    bytes of the histogram each (7,777 leaves a partial workgroup and a
+    partial tile).  Logits bit-exact from the staged entry point; logits,
+    routes, counts and permutation bit-exact from the fused forward; fp32 x
+    with bf16 experts (the router also writes the FFN's bf16 copy of x)
+    gives the same output as the grouped entry point, which converts x on
+    its own."""
+    H = 1024
+    for dtype, compute in (("bf16", None), ("f32", torch.float32), ("f32", torch.bfloat16)):
+        note(f"router 32-token workgroups T={T} E={E} x {dtype} experts {compute}")
+        inp = synth.make_moe_inputs(T=T, H=H, E=E, F=64, dtype=dtype, seed=11 * E + T)
+        x, gate = x_for(inp, gpu_device), torch.from_numpy(inp.gate).to(gpu_device)
+        ref = oracle_routing(inp)
+        logits = torch.full((T, E), float("nan"), dtype=torch.float32, device=gpu_device)
+        moe.matmul_transposed_gpu(x, gate, logits)
+        w = weights_for(inp, gpu_device, compute=compute)
+        fused = moe.moe_forward_gpu(x, gate, w).clone()
+        plan = w.plan_views(T)
+        grouped = moe.moe_forward_grouped_gpu(x, logits, w)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(logits.cpu().numpy().view(np.uint32), ref["logits"].view(np.uint32))
+        np.testing.assert_array_equal(plan["logits"].cpu().numpy().view(np.uint32), ref["logits"].view(np.uint32))
+        check_plan(plan, ref, T)
+        assert torch.equal(fused.view(torch.int32 if fused.dtype == torch.float32 else torch.int16),
+                           grouped.view(torch.int32 if grouped.dtype == torch.float32 else torch.int16))
+        w.release()
+
+
 @pytest.mark.parametrize("E,T", [(16, 20000), (24, 5000), (64, 9000), (2, 3000), (16, 1 << 20)])
 def test_dispatch_many_tiles(gpu_device, E, T):
     """The staged dispatch on random routes over many 64-token tiles (more
