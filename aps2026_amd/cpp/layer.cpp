@@ -132,8 +132,19 @@ void PhiAttention::forward(const Tensor& x, Tensor& y, const std::vector<std::si
     }
     Tensor q, k, v;
     q_proj_.forward(x, q, true);
-    k_proj_.forward(x, k, true);
-    v_proj_.forward(x, v, true);
+    // k and v as one pair when neither carries the bf16 copy (reference
+    // src/layer.cu:161-172); the pair needs both biases
+    const std::size_t nk = k_proj_.weight().size(0), nv = v_proj_.weight().size(0);
+    const bool fuse_kv = !k_proj_.weight().has_cuda_bf16_weight() && !v_proj_.weight().has_cuda_bf16_weight() &&
+                         nk == nv && k_proj_.bias().size() == nk && v_proj_.bias().size() == nv;
+    if (fuse_kv) {
+        k = Tensor({s, nk});
+        v = Tensor({s, nv});
+        tensor_ops::matmul_pair_bias_gpu(x, k_proj_.weight(), k_proj_.bias(), k, v_proj_.weight(), v_proj_.bias(), v);
+    } else {
+        k_proj_.forward(x, k, true);
+        v_proj_.forward(x, v, true);
+    }
     Tensor out({s, apss26::NUM_ATTENTION_HEADS * apss26::HEAD_DIM});
     if (expansion.active()) {
         // rows are trie nodes: RoPE at the node depth, keys along the chain

@@ -512,8 +512,22 @@ void matmul_pair_bias_gpu(const Tensor& a, const Tensor& first_weight, const Ten
         first_bias.size() != n || second_bias.size() != n || first_out.size(0) != m || first_out.size(1) != n ||
         second_out.size(0) != m || second_out.size(1) != n)
         throw std::invalid_argument("matmul_pair_bias_gpu shape");
-    matmul_transposed_bias_gpu(a, first_weight, first_bias, first_out);
-    matmul_transposed_bias_gpu(a, second_weight, second_bias, second_out);
+    if (first_weight.has_cuda_bf16_weight() || second_weight.has_cuda_bf16_weight()) {
+        // the split-bf16 Linear (USE_TC) per output
+        matmul_transposed_bias_gpu(a, first_weight, first_bias, first_out);
+        matmul_transposed_bias_gpu(a, second_weight, second_bias, second_out);
+        return;
+    }
+    if (k % 16 != 0 || n % 4 != 0)
+        throw std::invalid_argument("matmul_pair_bias_gpu: this build needs k % 16 == 0 and n % 4 == 0");
+    // both outputs in one grid (their column blocks share it)
+    const float* ws[2] = {first_weight.cuda_data(), second_weight.cuda_data()};
+    const float* bs[2] = {first_bias.cuda_data(), second_bias.cuda_data()};
+    float* ys[2] = {first_out.cuda_data_write(), second_out.cuda_data_write()};
+    const std::int32_t ns[2] = {static_cast<std::int32_t>(n), static_cast<std::int32_t>(n)};
+    const int rc = aps_linear_multi(a.cuda_data(), static_cast<std::int64_t>(m), static_cast<std::int32_t>(k), 2, ws,
+                                    bs, ns, ys, nullptr);
+    if (rc) throw_status(rc, "matmul_pair_bias_gpu");
 }
 
 }  // namespace tensor_ops

@@ -580,6 +580,44 @@ int aps_linear(const float* x, const float* weight, const float* bias, int64_t r
     return APS_OK;
 }
 
+int aps_linear_multi(const float* x, int64_t rows, int32_t in_features, int32_t count, const float* const* weights,
+                     const float* const* biases, const int32_t* out_features, float* const* ys, void* stream) {
+    if (count < 1 || count > 3 || !out_features) return fail(APS_ERR_SHAPE, "linear multi: count %d (1..3)", count);
+    if (rows < 0 || in_features <= 0 || in_features % 16 != 0 || (rows + 63) / 64 > 65535)
+        return fail(APS_ERR_SHAPE, "linear multi shape: rows %lld in %d (multiple of 16)", (long long)rows,
+                    in_features);
+    for (int32_t j = 0; j < count; ++j)
+        if (out_features[j] <= 0 || out_features[j] % 4 != 0)
+            return fail(APS_ERR_SHAPE, "linear multi: out %d of output %d (multiple of 4)", out_features[j], j);
+    if (rows == 0) return APS_OK;
+    if (!x || !weights || !ys) return fail(APS_ERR_ARG, "linear multi: NULL pointer");
+    const float* ws[3] = {};
+    const float* bs[3] = {};
+    bool fits = aps::linear_mfma_fits(rows, in_features, out_features[0]);
+    for (int32_t j = 0; j < count; ++j) {
+        ws[j] = weights[j];
+        bs[j] = biases ? biases[j] : nullptr;
+        if (!ws[j] || !ys[j]) return fail(APS_ERR_ARG, "linear multi: NULL pointer (output %d)", j);
+        if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(ws[j]) | reinterpret_cast<uintptr_t>(bs[j]) |
+              reinterpret_cast<uintptr_t>(ys[j])) & 15u) != 0)
+            return fail(APS_ERR_ARG, "linear multi: arrays must be 16-byte aligned");
+        if (ys[j] == x) return fail(APS_ERR_ARG, "linear multi: output %d aliases x", j);
+        for (int32_t i = 0; i < j; ++i)
+            if (ys[i] == ys[j]) return fail(APS_ERR_ARG, "linear multi: outputs %d and %d are the same array", i, j);
+        fits = fits && aps::linear_mfma_fits(rows, in_features, out_features[j]);
+    }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (fits) {
+        APS_HIP(aps::launch_linear_mfma_multi(x, rows, in_features, count, ws, bs, ys, out_features, s),
+                "linear multi launch");
+    } else {
+        for (int32_t j = 0; j < count; ++j)
+            APS_HIP(aps::launch_linear_f32(x, ws[j], bs[j], ys[j], rows, in_features, out_features[j], s),
+                    "linear multi launch");
+    }
+    return APS_OK;
+}
+
 size_t aps_linear_tc_packed_bytes(int32_t out_features, int32_t in_features) {
     if (out_features <= 0 || in_features <= 0 || in_features % 64 != 0) return 0;
     return static_cast<size_t>(aps::linear_tc_packed_elems(out_features, in_features)) * sizeof(uint16_t);

@@ -194,6 +194,9 @@ hipError_t launch_linear_tc_multi(const uint16_t* xhi, const uint16_t* xlo, int 
 bool linear_mfma_fits(int64_t rows, int in_f, int out_f);
 hipError_t launch_linear_mfma_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows,
                                   int in_f, int out_f, hipStream_t s);
+// count (1..3) outputs of one x in one grid, every shape linear_mfma_fits
+hipError_t launch_linear_mfma_multi(const float* x, int64_t rows, int in_f, int count, const float* const* w,
+                                    const float* const* bias, float* const* y, const int* out_f, hipStream_t s);
 hipError_t launch_linear_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows, int in_f,
                              int out_f, hipStream_t s);
 

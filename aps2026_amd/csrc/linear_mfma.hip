@@ -57,12 +57,22 @@ struct LInt {
     static constexpr int value = V;
 };
 
+// Up to three outputs of one x in one grid (the reference's
+// matmul_pair_bias_gpu pairs k and v): segment s owns column tiles
+// t0[s] .. t0[s + 1] - 1 of the grid's x dimension.
+struct LinSegs {
+    const float* w[3];
+    const float* b[3];
+    float* y[3];
+    int n[3];
+    int t0[4];
+};
+
 // WN: columns per wave (64: two MFMAs per k; 32: one, for grids that would
 // otherwise leave CUs idle).  A block is 128 rows x 2 WN columns.
 template <int WN>
 __global__ void __launch_bounds__(256, 2)
-k_linear_mfma(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
-              float* __restrict__ y, int64_t M, int K, int N) {
+k_linear_mfma(const float* __restrict__ x, const LinSegs segs, int64_t M, int K) {
     constexpr int kBRows = 2 * WN;                        // weight rows per block
     constexpr int kStageRows = kLRows + kBRows;
     constexpr int kLStageBytes = kStageRows * 128;
@@ -75,7 +85,12 @@ k_linear_mfma(const float* __restrict__ x, const float* __restrict__ w, const fl
     uint8_t* const slot0 = ring[0];
     uint8_t* const slot1 = ring[1];
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kLRows;
-    const int n0 = blockIdx.x * kBRows;
+    const int sg = blockIdx.x >= static_cast<unsigned>(segs.t0[1]) ? (blockIdx.x >= static_cast<unsigned>(segs.t0[2]) ? 2 : 1) : 0;
+    const float* __restrict__ w = segs.w[sg];
+    const float* __restrict__ bias = segs.b[sg];
+    float* __restrict__ y = segs.y[sg];
+    const int N = segs.n[sg];
+    const int n0 = (blockIdx.x - segs.t0[sg]) * kBRows;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int KT = K / kLStageK;
@@ -177,21 +192,47 @@ bool linear_mfma_fits(int64_t rows, int in_f, int out_f) {
     return rows > 0 && in_f > 0 && in_f % kLStageK == 0 && out_f > 0 && (rows + kLRows - 1) / kLRows <= 65535;
 }
 
+hipError_t launch_linear_mfma_multi(const float* x, int64_t rows, int in_f, int count, const float* const* w,
+                                    const float* const* bias, float* const* y, const int* out_f, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (count < 1 || count > 3) return hipErrorInvalidValue;
+    for (int i = 0; i < count; ++i)
+        if (!linear_mfma_fits(rows, in_f, out_f[i])) return hipErrorInvalidValue;
+    // 128- or 64-column blocks, whichever gives the busiest CU less work:
+    // blocks per CU (rounded up) x width, the 64-column block charged 5% for
+    // its lower FLOP rate and either charged 30% when the grid leaves CUs
+    // fewer than two workgroups (no latency hiding between them)
+    const int64_t cus = num_cus(), rt = ceil_div(rows, kLRows);
+    auto cost = [&](int bc, double rate) {
+        int64_t tiles = 0;
+        for (int i = 0; i < count; ++i) tiles += ceil_div(out_f[i], bc) * rt;
+        return static_cast<double>(ceil_div(tiles, cus) * bc) * rate * (tiles < 2 * cus ? 1.3 : 1.0);
+    };
+    const bool wide = cost(128, 1.0) <= cost(64, 1.05);
+    const int bc = wide ? 128 : 64;
+    LinSegs segs{};
+    int t = 0;
+    for (int i = 0; i < 3; ++i) {
+        segs.t0[i] = t;
+        if (i < count) {
+            segs.w[i] = w[i];
+            segs.b[i] = bias[i];
+            segs.y[i] = y[i];
+            segs.n[i] = out_f[i];
+            t += static_cast<int>(ceil_div(out_f[i], bc));
+        }
+    }
+    segs.t0[3] = t;
+    for (int i = count; i < 3; ++i) segs.t0[i] = t;   // empty segments past the last
+    const dim3 grid(static_cast<unsigned>(t), static_cast<unsigned>(ceil_div(rows, kLRows)));
+    if (wide) hipLaunchKernelGGL(k_linear_mfma<64>, grid, dim3(256), 0, s, x, segs, rows, in_f);
+    else hipLaunchKernelGGL(k_linear_mfma<32>, grid, dim3(256), 0, s, x, segs, rows, in_f);
+    return hipGetLastError();
+}
+
 hipError_t launch_linear_mfma_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows,
                                   int in_f, int out_f, hipStream_t s) {
-    if (rows <= 0) return hipSuccess;
-    if (!linear_mfma_fits(rows, in_f, out_f)) return hipErrorInvalidValue;
-    // 128-column blocks when they give every CU two (the occupancy), else
-    // 64-column blocks
-    const int64_t tiles = ceil_div(out_f, 128) * ceil_div(rows, kLRows);
-    if (tiles >= 2 * static_cast<int64_t>(num_cus())) {
-        const dim3 grid(static_cast<unsigned>(ceil_div(out_f, 128)), static_cast<unsigned>(ceil_div(rows, kLRows)));
-        hipLaunchKernelGGL(k_linear_mfma<64>, grid, dim3(256), 0, s, x, w, bias, y, rows, in_f, out_f);
-    } else {
-        const dim3 grid(static_cast<unsigned>(ceil_div(out_f, 64)), static_cast<unsigned>(ceil_div(rows, kLRows)));
-        hipLaunchKernelGGL(k_linear_mfma<32>, grid, dim3(256), 0, s, x, w, bias, y, rows, in_f, out_f);
-    }
-    return hipGetLastError();
+    return launch_linear_mfma_multi(x, rows, in_f, 1, &w, &bias, &y, &out_f, s);
 }
 
 }  // namespace aps

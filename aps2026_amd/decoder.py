@@ -212,9 +212,21 @@ class DecoderLayer:
                                         (ctypes.c_int32 * cnt)(*[n for _, _, n in names]), int(self.tc_terms == 4),
                                         vp(*[_p(dst) for _, dst, _ in names]), stream))
         else:
-            for nm, dst, n in names:
+            # an output wide enough to fill the grid alone (q, o) by itself;
+            # the narrow ones (k and v) share one grid, so that no CU holds a
+            # third workgroup of one while others hold two
+            wide = [x for x in names if x[2] >= 2048]
+            narrow = [x for x in names if x[2] < 2048]
+            for nm, dst, n in wide:
                 _call(L.aps_linear(_p(src), _p(self.w.proj[nm][0]), _p(self.w.proj[nm][1]), T, K, n, _p(dst),
                                    stream))
+            if narrow:
+                cnt = len(narrow)
+                vp = ctypes.c_void_p * cnt
+                _call(L.aps_linear_multi(_p(src), T, K, cnt, vp(*[_p(self.w.proj[nm][0]) for nm, _, _ in narrow]),
+                                         vp(*[_p(self.w.proj[nm][1]) for nm, _, _ in narrow]),
+                                         (ctypes.c_int32 * cnt)(*[n for _, _, n in narrow]),
+                                         vp(*[_p(dst) for _, dst, _ in narrow]), stream))
 
     def attention(self, b: Buffers, plan: RowPlan, stream) -> None:
         """normed -> att (projections, RoPE, tree attention)."""

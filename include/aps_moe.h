@@ -327,6 +327,16 @@ APS_API int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int
  * aliasing x. */
 APS_API int aps_linear(const float* x, const float* weight, const float* bias, int64_t rows, int32_t in_features,
                        int32_t out_features, float* y, void* stream);
+/* Replaces tensor_ops::matmul_pair_bias_gpu (reference include/tensor.h:
+ * 77-81, src/tensor.cu:3172-3200), the k and v projections of one input
+ * (src/layer.cu:163-166): aps_linear for each of `count` (1..3) outputs of
+ * the same x, whose column blocks share one grid (k and v alone would each
+ * leave some CUs a third workgroup while others hold two).  Every output
+ * is aps_linear's, bit for bit.  Outputs distinct and not x; biases or
+ * biases[j] may be NULL. */
+APS_API int aps_linear_multi(const float* x, int64_t rows, int32_t in_features, int32_t count,
+                             const float* const* weights, const float* const* biases, const int32_t* out_features,
+                             float* const* ys, void* stream);
 
 /* The reference's optional tensor-core Linear (built with USE_TC; USE_TC_ALL
  * adds the fourth product and applies it to every attention projection,

@@ -226,6 +226,38 @@ def test_linear_bit_exact(gpu_device, rows, k, n, bias):
     np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,k,ns,bias", [(10240 // 20, 4096, (512, 512), (True, True)),
+                                            (300, 256, (2048, 512, 132), (True, False, True)),
+                                            (129, 96, (64, 20), (False, True)), (7, 48, (4, 8, 12), (True, True, True)),
+                                            (2048, 256, (4096,), (True,))])
+def test_linear_multi_bit_exact(gpu_device, rows, k, ns, bias):
+    """aps_linear_multi (k and v of one input in one grid, the reference's
+    matmul_pair_bias_gpu) against the oracle's linear per output, bit for
+    bit: one and two and three outputs, the 128- and the 64-column block
+    grid, outputs of unequal width, k = 48 (the vector-FMA fallback) and
+    missing biases."""
+    import ctypes
+    from aps2026_amd import capi
+    from aps2026_amd.moe import _ptr, _stream
+    note(f"linear multi rows={rows} k={k} ns={ns}")
+    rng = np.random.default_rng(rows + k + sum(ns))
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    ws = [(0.02 * rng.standard_normal((n, k))).astype(np.float32) for n in ns]
+    bs = [(0.1 * rng.standard_normal(n)).astype(np.float32) if b else None for n, b in zip(ns, bias)]
+    xd = dev(x, gpu_device)
+    wd = [dev(w, gpu_device) for w in ws]
+    bd = [dev(b, gpu_device) if b is not None else None for b in bs]
+    ys = [torch.full((rows, n), float("nan"), dtype=torch.float32, device=gpu_device) for n in ns]
+    cnt = len(ns)
+    vp = ctypes.c_void_p * cnt
+    rc = capi.lib().aps_linear_multi(_ptr(xd), rows, k, cnt, vp(*[_ptr(w) for w in wd]), vp(*[_ptr(b) for b in bd]),
+                                     (ctypes.c_int32 * cnt)(*ns), vp(*[_ptr(y) for y in ys]), _stream(xd.device))
+    assert rc == 0, capi.last_error()
+    torch.cuda.synchronize()
+    for y, w, b in zip(ys, ws, bs):
+        np.testing.assert_array_equal(y.cpu().numpy().view(np.uint32), oracle.linear(x, w, b).view(np.uint32))
+
+
 def test_linear_bit_exact_wide_exponents(gpu_device):
     """The matrix-core Linear (K = 1 fp32 MFMA chains) against the oracle's
     FMA chain on operands whose exponents span 2^-20 .. 2^20 and on products
