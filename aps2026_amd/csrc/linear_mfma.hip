@@ -57,6 +57,8 @@ struct LInt {
     static constexpr int value = V;
 };
 
+constexpr int kLXcds = 8;   // XCDs of an MI355X
+
 // Up to three outputs of one x in one grid (the reference's
 // matmul_pair_bias_gpu pairs k and v): segment s owns column tiles
 // t0[s] .. t0[s + 1] - 1 of the grid's x dimension.
@@ -70,9 +72,17 @@ struct LinSegs {
 
 // WN: columns per wave (64: two MFMAs per k; 32: one, for grids that would
 // otherwise leave CUs idle).  A block is 128 rows x 2 WN columns.
+// The grid is one-dimensional over the row-tile-major tile order.
+// Workgroups are dealt to the 8 XCDs round robin (workgroup b runs on XCD
+// b % 8).  Taken in launch order (tile b), XCD x holds the column tiles
+// c = x mod 8 of every row tile: it reads an eighth of W and all of x.  With
+// xcd_rows, workgroup b takes tile (b % 8) * per + b / 8 instead: XCD x holds
+// a contiguous run of tiles, the column tiles of a row tile sharing its x
+// rows in one L2, and reads about an eighth of x and all of W.  The
+// launcher picks xcd_rows when x is the larger operand by 3x or more.
 template <int WN>
 __global__ void __launch_bounds__(256, 2)
-k_linear_mfma(const float* __restrict__ x, const LinSegs segs, int64_t M, int K) {
+k_linear_mfma(const float* __restrict__ x, const LinSegs segs, int64_t M, int K, int row_tiles, int xcd_rows) {
     constexpr int kBRows = 2 * WN;                        // weight rows per block
     constexpr int kStageRows = kLRows + kBRows;
     constexpr int kLStageBytes = kStageRows * 128;
@@ -84,13 +94,19 @@ k_linear_mfma(const float* __restrict__ x, const LinSegs segs, int64_t M, int K)
     __shared__ __align__(16) uint8_t ring[2][kLStageBytes];
     uint8_t* const slot0 = ring[0];
     uint8_t* const slot1 = ring[1];
-    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kLRows;
-    const int sg = blockIdx.x >= static_cast<unsigned>(segs.t0[1]) ? (blockIdx.x >= static_cast<unsigned>(segs.t0[2]) ? 2 : 1) : 0;
+    const int ncol = segs.t0[3];
+    const int64_t per = (static_cast<int64_t>(row_tiles) * ncol + kLXcds - 1) / kLXcds;
+    const int64_t t = xcd_rows ? static_cast<int64_t>(blockIdx.x % kLXcds) * per + blockIdx.x / kLXcds
+                               : static_cast<int64_t>(blockIdx.x);
+    if (t >= static_cast<int64_t>(row_tiles) * ncol) return;
+    const int tc = static_cast<int>(t % ncol);
+    const int64_t m0 = (t / ncol) * kLRows;
+    const int sg = tc >= segs.t0[1] ? (tc >= segs.t0[2] ? 2 : 1) : 0;
     const float* __restrict__ w = segs.w[sg];
     const float* __restrict__ bias = segs.b[sg];
     float* __restrict__ y = segs.y[sg];
     const int N = segs.n[sg];
-    const int n0 = (blockIdx.x - segs.t0[sg]) * kBRows;
+    const int n0 = (tc - segs.t0[sg]) * kBRows;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int KT = K / kLStageK;
@@ -224,9 +240,13 @@ hipError_t launch_linear_mfma_multi(const float* x, int64_t rows, int in_f, int 
     }
     segs.t0[3] = t;
     for (int i = count; i < 3; ++i) segs.t0[i] = t;   // empty segments past the last
-    const dim3 grid(static_cast<unsigned>(t), static_cast<unsigned>(ceil_div(rows, kLRows)));
-    if (wide) hipLaunchKernelGGL(k_linear_mfma<64>, grid, dim3(256), 0, s, x, segs, rows, in_f);
-    else hipLaunchKernelGGL(k_linear_mfma<32>, grid, dim3(256), 0, s, x, segs, rows, in_f);
+    const int64_t tiles = static_cast<int64_t>(t) * rt;
+    int64_t wcols = 0;
+    for (int i = 0; i < count; ++i) wcols += out_f[i];
+    const int xr = rows >= 3 * wcols ? 1 : 0;   // x bytes >= 3 x W bytes (both rows x in_f fp32)
+    const dim3 grid(static_cast<unsigned>(ceil_div(tiles, kLXcds) * kLXcds));
+    if (wide) hipLaunchKernelGGL(k_linear_mfma<64>, grid, dim3(256), 0, s, x, segs, rows, in_f, static_cast<int>(rt), xr);
+    else hipLaunchKernelGGL(k_linear_mfma<32>, grid, dim3(256), 0, s, x, segs, rows, in_f, static_cast<int>(rt), xr);
     return hipGetLastError();
 }
 

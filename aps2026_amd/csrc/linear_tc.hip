@@ -117,16 +117,27 @@ struct TcSegs {
     int t0[4];
 };
 
+// One-dimensional grid over the row-tile-major tile order, dealt to XCDs as
+// k_linear_mfma's (workgroup b on XCD b % 8): tile b, or with xcd_rows tile
+// (b % 8) * per + b / 8, so that the column tiles of a row tile share its x
+// rows in one L2 (picked when x is the larger operand by 3x or more).
+constexpr int kTcXcds = 8;
+
 template <bool ALL>
 __global__ void __launch_bounds__(256, 1)
 k_linear_tc(const uint16_t* __restrict__ xhi, const uint16_t* __restrict__ xlo, const TcSegs segs, int64_t M,
-            int K) {
+            int K, int row_tiles, int xcd_rows) {
     __shared__ __align__(16) uint8_t ring[2][kTcStageBytes];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kTcRows;
+    const int ncol = segs.t0[3];
+    const int64_t per = (static_cast<int64_t>(row_tiles) * ncol + kTcXcds - 1) / kTcXcds;
+    const int64_t t = xcd_rows ? static_cast<int64_t>(blockIdx.x % kTcXcds) * per + blockIdx.x / kTcXcds
+                               : static_cast<int64_t>(blockIdx.x);
+    if (t >= static_cast<int64_t>(row_tiles) * ncol) return;
+    const int64_t m0 = (t / ncol) * kTcRows;
     // this block's segment (selects, so the argument block stays in scalar registers)
-    const int bx = blockIdx.x;
+    const int bx = static_cast<int>(t % ncol);
     const int sg = (bx >= segs.t0[1]) + (bx >= segs.t0[2]);
     const uint16_t* __restrict__ img = sg == 0 ? segs.w[0] : sg == 1 ? segs.w[1] : segs.w[2];
     const float* __restrict__ bias = sg == 0 ? segs.b[0] : sg == 1 ? segs.b[1] : segs.b[2];
@@ -274,9 +285,15 @@ hipError_t launch_linear_tc_multi(const uint16_t* xhi, const uint16_t* xlo, int 
     }
     segs.t0[3] = t;
     for (int j = count; j < 3; ++j) segs.t0[j] = t;
-    const dim3 grid(static_cast<unsigned>(t), static_cast<unsigned>(ceil_div(rows, kTcRows)));
-    if (all_terms) hipLaunchKernelGGL(k_linear_tc<true>, grid, dim3(256), 0, s, xhi, xlo, segs, rows, in_f);
-    else hipLaunchKernelGGL(k_linear_tc<false>, grid, dim3(256), 0, s, xhi, xlo, segs, rows, in_f);
+    const int64_t rt = ceil_div(rows, kTcRows);
+    int64_t wcols = 0;
+    for (int j = 0; j < count; ++j) wcols += out_f[j];
+    const int xr = rows >= 3 * wcols ? 1 : 0;   // x bytes >= 3 x W bytes (both hi + lo bf16)
+    const dim3 grid(static_cast<unsigned>(ceil_div(rt * t, kTcXcds) * kTcXcds));
+    if (all_terms)
+        hipLaunchKernelGGL(k_linear_tc<true>, grid, dim3(256), 0, s, xhi, xlo, segs, rows, in_f, static_cast<int>(rt), xr);
+    else
+        hipLaunchKernelGGL(k_linear_tc<false>, grid, dim3(256), 0, s, xhi, xlo, segs, rows, in_f, static_cast<int>(rt), xr);
     return hipGetLastError();
 }
 
