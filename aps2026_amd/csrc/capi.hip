@@ -561,6 +561,19 @@ int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int64_t bat
     return APS_OK;
 }
 
+int aps_prefix_ancestors(const uint32_t* node_parent, const uint32_t* node_depth, const uint32_t* run_start,
+                         int64_t nodes, int64_t anc_stride, uint32_t* node_anc, void* stream) {
+    if (nodes < 0 || anc_stride <= 0 || nodes > 0xFFFFFFFFll || anc_stride > (1ll << 24) ||
+        nodes > (1ll << 38) / anc_stride)
+        return fail(APS_ERR_SHAPE, "prefix ancestors: nodes %lld stride %lld", (long long)nodes, (long long)anc_stride);
+    if (nodes == 0) return APS_OK;
+    if (!node_parent || !node_depth || !run_start || !node_anc) return fail(APS_ERR_ARG, "prefix ancestors: NULL pointer");
+    APS_HIP(aps::launch_prefix_ancestors(node_parent, node_depth, run_start, nodes, anc_stride, node_anc,
+                                         static_cast<hipStream_t>(stream)),
+            "prefix ancestors launch");
+    return APS_OK;
+}
+
 int aps_linear(const float* x, const float* weight, const float* bias, int64_t rows, int32_t in_features,
                int32_t out_features, float* y, void* stream) {
     if (rows < 0 || in_features <= 0 || out_features <= 0 || in_features % 16 != 0 || out_features % 4 != 0 ||

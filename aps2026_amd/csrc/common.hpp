@@ -153,6 +153,10 @@ hipError_t launch_gather_rows(const float* x, int64_t x_rows, int64_t hidden, co
 int prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int64_t batch, int64_t vocab, int64_t max_positions,
                  uint32_t* token_node, uint32_t* node_token, uint32_t* node_depth, uint32_t* node_anc,
                  int64_t anc_stride, int64_t* nodes_out, std::string& err);
+// The ancestor table [nodes][stride] of a trie from its parent, depth and
+// run-start arrays (device memory); see prefix.hip.
+hipError_t launch_prefix_ancestors(const uint32_t* parent, const uint32_t* depth, const uint32_t* run_start,
+                                   int64_t nodes, int64_t stride, uint32_t* anc, hipStream_t s);
 
 // RoPE in place on x [rows][heads][head_dim] at each row's position (pairs
 // j, j + head_dim / 2); rows whose position is >= max_seq are left as they are.

@@ -1,4 +1,5 @@
-// Prefix deduplication of a prompt batch (host code).
+// Prefix deduplication of a prompt batch (host code), and the device build of
+// its ancestor table.
 //
 // Reference: PhiTinyMoEModel::generate (src/model.cu:44-117).  Attention is
 // causal and the sequences are independent, so a token's hidden state is a
@@ -93,6 +94,58 @@ int prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int64_t batch, 
     }
     *nodes_out = nodes;
     return 0;
+}
+
+// ---------------------------------------------------------------------------
+// The ancestor table on the device.  Node ids are creation order, so a node
+// created right after its parent (the common case: a sequence's tokens past
+// the point where it leaves every earlier sequence's prefix) is parent + 1,
+// and a trie path is a few runs of consecutive ids: run_start[n] is the
+// first node of n's run (n itself when parent(n) != n - 1 or n has depth 0),
+// and within a run depth(s + i) = depth(s) + i.  The ancestor of n at depth
+// d <= depth(n) is therefore s + (d - depth(s)) for the first run start s on
+// the way up (s = run_start[n], then run_start[parent[s]], ..) with depth(s)
+// <= d: as many steps as the path has branch points.  One thread per (node,
+// depth) entry; entries past the node's depth are 0, as in the host table.
+namespace {
+__global__ void __launch_bounds__(256)
+k_prefix_ancestors(const uint32_t* __restrict__ parent, const uint32_t* __restrict__ depth,
+                   const uint32_t* __restrict__ run_start, int64_t nodes, int64_t stride, uint32_t* __restrict__ anc) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= nodes * stride) return;
+    const int64_t n = i / stride;
+    const uint32_t d = static_cast<uint32_t>(i - n * stride);
+    uint32_t v = 0u;
+    if (d <= depth[n]) {
+        // indices clamped to the table for memory safety only (a consistent
+        // trie never needs it); each step moves to a strictly shallower run,
+        // so at most depth(n) steps
+        const uint32_t last = static_cast<uint32_t>(nodes - 1);
+        uint32_t s = run_start[n];
+        s = s < last ? s : last;
+        for (uint32_t guard = 0; d < depth[s] && guard <= depth[n]; ++guard) {
+            uint32_t p = parent[s];
+            p = p < last ? p : last;
+            s = run_start[p];
+            s = s < last ? s : last;
+        }
+        v = d >= depth[s] ? s + (d - depth[s]) : 0u;
+        // an ancestor is created before its descendants: never above n, so
+        // the table only names rows below the node count whatever the input
+        v = v < static_cast<uint32_t>(n) ? v : static_cast<uint32_t>(n);
+    }
+    anc[i] = v;
+}
+}  // namespace
+
+hipError_t launch_prefix_ancestors(const uint32_t* parent, const uint32_t* depth, const uint32_t* run_start,
+                                   int64_t nodes, int64_t stride, uint32_t* anc, hipStream_t s) {
+    if (nodes <= 0) return hipSuccess;
+    if (stride <= 0 || stride > (int64_t(1) << 24) || nodes > (int64_t(1) << 38) / stride) return hipErrorInvalidValue;
+    const int64_t n = nodes * stride;
+    hipLaunchKernelGGL(k_prefix_ancestors, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, s, parent,
+                       depth, run_start, nodes, stride, anc);
+    return hipGetLastError();
 }
 
 }  // namespace aps

@@ -112,13 +112,16 @@ class RowPlan:
 
     @staticmethod
     def from_prompts(prompts: Sequence[Sequence[int]], device) -> "RowPlan":
-        plan = prefix.prefix_dedup(prompts)
+        # the trie on the host, its ancestor table on the device (the host
+        # table is nodes x max_len words: 42 MB at C4, which took longer to
+        # fill, copy and upload than a layer of the model)
+        plan = prefix.prefix_dedup(prompts, with_ancestors=False)
         depth = np.asarray(plan.node_depth, np.uint32)
-        anc = np.asarray(plan.node_anc, np.uint32).reshape(plan.nodes, plan.max_len)
-        if depth.size and (int(depth.max()) >= plan.max_len or int(anc.max()) >= plan.nodes):
+        if depth.size and int(depth.max()) >= plan.max_len:
             raise ValueError("prefix plan out of range")
         to_dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(device)
-        return RowPlan(rows=plan.nodes, max_len=plan.max_len, pos=to_dev(depth), anc=to_dev(anc),
+        anc = prefix.ancestors_gpu(plan, device)
+        return RowPlan(rows=plan.nodes, max_len=plan.max_len, pos=to_dev(depth), anc=anc,
                        node_token=to_dev(np.asarray(plan.node_token, np.uint32)),
                        last_rows=to_dev(np.asarray(plan.last_rows, np.uint32)),
                        prompt_tokens=int(np.asarray(plan.token_node).shape[0]))

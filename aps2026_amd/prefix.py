@@ -57,6 +57,37 @@ class PrefixPlan:
         return self.token_node[self.offsets + self.seq_lens - 1]
 
 
+def node_parents_and_runs(plan: PrefixPlan):
+    """Each node's parent (the node of the previous token of a sequence that
+    contains it; 0 for depth-0 nodes) and the first node of its run of
+    consecutive ids (n itself when n has depth 0 or its parent is not
+    n - 1): the inputs of the device ancestor table (aps_prefix_ancestors)."""
+    n = plan.nodes
+    parent = np.zeros(max(n, 1), np.uint32)[:n]
+    tn = plan.token_node.astype(np.int64)
+    starts = np.zeros(tn.shape[0], bool)
+    starts[plan.offsets] = True
+    inner = np.nonzero(~starts)[0]
+    parent[tn[inner]] = tn[inner - 1]
+    idx = np.arange(n, dtype=np.int64)
+    is_start = (plan.node_depth == 0) | (parent.astype(np.int64) != idx - 1)
+    run_start = np.maximum.accumulate(np.where(is_start, idx, 0)).astype(np.uint32) if n else parent.copy()
+    return parent, run_start
+
+
+def ancestors_gpu(plan: PrefixPlan, device, stream=None):
+    """The ancestor table [nodes][max_len] (int32 view of uint32) built on
+    the device from the plan's parents and runs, equal to the host table."""
+    parent, run_start = node_parents_and_runs(plan)
+    n, stride = plan.nodes, max(plan.max_len, 1)
+    to_dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(device)
+    p_d, d_d, r_d = to_dev(parent), to_dev(plan.node_depth), to_dev(run_start)
+    anc = torch.empty((n, stride), dtype=torch.int32, device=device)
+    _call(capi.lib().aps_prefix_ancestors(_ptr(p_d), _ptr(d_d), _ptr(r_d), n, stride, _ptr(anc),
+                                          _stream(anc.device) if stream is None else stream))
+    return anc
+
+
 def prefix_dedup(input_ids: Sequence[Sequence[int]], with_ancestors: bool = True,
                  vocab_size: int = VOCAB_SIZE, max_positions: int = MAX_POSITION_EMBEDDINGS) -> PrefixPlan:
     """The prefix trie of a prompt batch (reference src/model.cu:44-117)."""

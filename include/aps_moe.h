@@ -316,6 +316,19 @@ APS_API int aps_prefix_dedup(const int32_t* ids, const int64_t* seq_offsets, int
                              int64_t max_positions, uint32_t* token_node, uint32_t* node_token, uint32_t* node_depth,
                              uint32_t* node_anc, int64_t anc_stride, int64_t* nodes);
 
+/* The ancestor table of aps_prefix_dedup's node_anc, built on the device
+ * (the table generate() builds on the host and uploads, reference
+ * src/model.cu:64-117): node_anc [nodes][anc_stride], row n = the ancestor
+ * chain root .. n, then zeros, equal to the host table bit for bit.  All
+ * arrays in device memory: node_parent[n] (the node before n on its
+ * sequence; any value for depth-0 nodes), node_depth[n], and run_start[n]
+ * = n when node_depth[n] == 0 or node_parent[n] != n - 1, else
+ * run_start[n - 1].  anc_stride >= the longest sequence, at most 2^24,
+ * and nodes * anc_stride at most 2^38.  Every entry of row n is at most n,
+ * whatever the inputs hold.  Asynchronous on `stream`. */
+APS_API int aps_prefix_ancestors(const uint32_t* node_parent, const uint32_t* node_depth, const uint32_t* run_start,
+                                 int64_t nodes, int64_t anc_stride, uint32_t* node_anc, void* stream);
+
 /* ---- attention over the prefix trie (scope row f4) --------------------- */
 
 /* Replaces Linear::forward's GPU path (reference src/layer.cu:30-42 ->

@@ -12,7 +12,7 @@ from aps2026_amd import capi, moe
 def test_library_exports_every_declared_symbol():
     L = capi.lib()
     names = capi.declared_symbols()
-    assert len(names) == 41
+    assert len(names) == 42
     for n in names:
         assert hasattr(L, n), n
     assert L.aps_moe_abi_version() == 1

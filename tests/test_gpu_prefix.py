@@ -58,6 +58,39 @@ def test_gather_rows_index_checks(gpu_device):
     assert torch.equal(out[1], torch.zeros(64, device=gpu_device))
 
 
+def _ancestor_batches():
+    rng = np.random.default_rng(11)
+    yield "c4", c4_prompts()
+    yield "single", [rng.integers(0, 32064, 700).tolist()]
+    yield "identical", [[5] * 64] * 6
+    yield "tiny-vocab", [rng.integers(0, 3, rng.integers(1, 90)).tolist() for _ in range(40)]
+    yield "varied", [rng.integers(0, 40, rng.integers(1, 300)).tolist() for _ in range(25)]
+    yield "nested", [[9] * k for k in (1, 200, 3, 64, 4096)]
+
+
+@pytest.mark.parametrize("name,batch", list(_ancestor_batches()), ids=lambda v: v if isinstance(v, str) else "")
+def test_ancestors_gpu_equal_host_table(gpu_device, name, batch):
+    """aps_prefix_ancestors builds [nodes][max_len] on the device bit for bit
+    equal to the host table (reference src/model.cu:107-116), zero padding
+    past each node's depth included."""
+    plan = prefix.prefix_dedup(batch)
+    note(f"ancestors {name}: {plan.nodes} nodes, stride {plan.max_len}")
+    anc = prefix.ancestors_gpu(plan, gpu_device)
+    torch.cuda.synchronize()
+    assert tuple(anc.shape) == plan.node_anc.shape
+    np.testing.assert_array_equal(anc.cpu().numpy().view(np.uint32), plan.node_anc)
+
+
+def test_ancestors_gpu_argument_checks(gpu_device):
+    d = torch.zeros(4, dtype=torch.int32, device=gpu_device)
+    lib = capi.lib()
+    p = ctypes.c_void_p(d.data_ptr())
+    assert lib.aps_prefix_ancestors(p, p, p, 4, 0, p, None) != 0
+    assert lib.aps_prefix_ancestors(p, p, p, -1, 4, p, None) != 0
+    assert lib.aps_prefix_ancestors(None, p, p, 4, 1, p, None) != 0
+    assert lib.aps_prefix_ancestors(None, None, None, 0, 1, None, None) == 0
+
+
 def test_c4_dedup_rows_equal_full_rows(gpu_device):
     """The invariant the reference's dedup rests on (src/model.cu:64-69), on
     this build's row-wise ops: embedding rows gathered per trie node, then

@@ -85,6 +85,56 @@ def test_library_matches_oracle(seed):
     assert plan.last_rows.tolist() == [tn[e] for e in ends]
 
 
+def ancestor_walk(depth, parent, run_start, n, d):
+    """The device ancestor kernel's walk for entry (n, d), on the host: hop
+    from the start of n's run of consecutive ids to the parent of that start
+    until the run holds depth d; counts hops so the kernel's bound is checked."""
+    s, hops = int(run_start[n]), 0
+    while d < depth[s]:
+        s, hops = int(run_start[parent[s]]), hops + 1
+    return s + (d - int(depth[s])), hops
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_ancestor_inputs_against_brute_force(seed):
+    """Parents and runs (aps_prefix_ancestors' inputs) from the plan equal
+    what the brute-force chains fix, and the walk over them rebuilds every
+    chain within depth hops (the kernel's loop bound)."""
+    rng = np.random.default_rng(200 + seed)
+    vocab = [3, 6, 32064][seed % 3]
+    batch = [rng.integers(0, vocab, rng.integers(1, 50)).tolist() for _ in range(rng.integers(1, 14))]
+    batch += shared_prefix_batch(rng, 2, 3, 9, 6, vocab)
+    if seed == 5:
+        batch = [[7] * 30, [7] * 30, [7] * 12 + [8] * 5]
+    rng.shuffle(batch)
+    _, _, nd, na = brute_force(batch)
+    plan = prefix.prefix_dedup(batch, with_ancestors=False)
+    parent, run_start = prefix.node_parents_and_runs(plan)
+    want_parent = [c[-2] if len(c) > 1 else 0 for c in na]
+    want_run = []
+    for n in range(len(na)):
+        want_run.append(n if nd[n] == 0 or want_parent[n] != n - 1 else want_run[n - 1])
+    assert parent.tolist() == want_parent and run_start.tolist() == want_run
+    for n, chain in enumerate(na):
+        for d, a in enumerate(chain):
+            got, hops = ancestor_walk(nd, parent, run_start, n, d)
+            assert got == a and hops <= nd[n]
+
+
+def test_ancestor_inputs_c4():
+    """At C4 there are 16 runs, one per prompt (a group's first prompt
+    continues its shared prefix's run), so any ancestor is at most one hop
+    away (suffix run -> group prefix run)."""
+    plan = prefix.prefix_dedup(c4_prompts(), with_ancestors=False)
+    parent, run_start = prefix.node_parents_and_runs(plan)
+    assert np.unique(run_start).shape[0] == 16
+    rng = np.random.default_rng(0)
+    for n in rng.integers(0, plan.nodes, 200):
+        for d in (0, int(plan.node_depth[n]) // 2, int(plan.node_depth[n])):
+            _, hops = ancestor_walk(plan.node_depth, parent, run_start, n, d)
+            assert hops <= 1
+
+
 def test_library_c4():
     batch = c4_prompts()
     plan = prefix.prefix_dedup(batch, with_ancestors=False)
