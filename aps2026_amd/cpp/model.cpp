@@ -39,13 +39,15 @@ PhiTinyMoEModel::PhiTinyMoEModel(Tensor embeddings, Tensor final_norm_weight, Te
 
 void PhiTinyMoEModel::generate(const std::vector<std::vector<int>>& input_ids, Tensor& logits) const {
     // validation and messages: the trie walk's (src/model.cu:47-117)
-    const PrefixTrie trie = build_prefix_trie(input_ids);
+    const PrefixTrie trie = build_prefix_trie(input_ids, false);
     const std::size_t batch = input_ids.size(), hidden_size = embeddings_.size(1);
 
     // one row per trie node: the embedding rows of the node tokens
     Tensor hidden({trie.nodes(), hidden_size});
     tensor_ops::gather_rows_gpu(embeddings_, trie.node_token, hidden);
-    const tensor_ops::RowIndexBuffer node_pos(trie.node_depth), node_anc(trie.node_anc);
+    // the ancestor table is nodes x max_len words: built on the device from
+    // 12 bytes per node rather than filled on the host and uploaded
+    const tensor_ops::RowIndexBuffer node_pos(trie.node_depth), node_anc(prefix_ancestors_gpu(trie));
     PrefixExpansion expansion;
     expansion.node_pos = &node_pos;
     expansion.node_anc = &node_anc;

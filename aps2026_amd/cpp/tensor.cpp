@@ -330,6 +330,16 @@ RowIndexBuffer::RowIndexBuffer(const std::vector<std::size_t>& rows) : size_(row
               "copy RowIndexBuffer");
 }
 
+RowIndexBuffer RowIndexBuffer::allocate(std::size_t size, std::size_t max_row) {
+    if (max_row > 0xFFFFFFFFull) throw std::invalid_argument("RowIndexBuffer row index");
+    RowIndexBuffer b;
+    if (size == 0) return b;
+    hip_check(hipMalloc(&b.ptr_, size * sizeof(std::uint32_t)), "hipMalloc RowIndexBuffer");
+    b.size_ = size;
+    b.max_row_ = max_row;
+    return b;
+}
+
 RowIndexBuffer::~RowIndexBuffer() {
     if (ptr_) (void)hipFree(ptr_);
 }

@@ -12,6 +12,8 @@
 #include <cstddef>
 #include <vector>
 
+#include "tensor.h"
+
 struct PrefixTrie {
     std::vector<std::size_t> seq_lens;    // [batch]
     std::vector<std::size_t> offsets;     // [batch]: packed row of each sequence's first token
@@ -29,4 +31,13 @@ struct PrefixTrie {
 // Throws std::runtime_error("generate received an empty input batch") for
 // an empty batch and std::invalid_argument with the reference's messages
 // ("empty input", "sequence is too long", "token out of vocabulary").
-PrefixTrie build_prefix_trie(const std::vector<std::vector<int>>& input_ids);
+// with_ancestors = false leaves node_anc empty (prefix_ancestors_gpu builds
+// the table on the device instead).
+PrefixTrie build_prefix_trie(const std::vector<std::vector<int>>& input_ids, bool with_ancestors = true);
+
+// The ancestor table [nodes][max_len] of a trie (node_anc's layout and
+// values) built on the device by aps_prefix_ancestors from each node's
+// parent, depth and run of consecutive ids: 12 bytes per node cross the bus
+// instead of 4 x max_len.  Needs only token_node, node_depth, offsets and
+// max_len, so a trie built without ancestors serves.  Synchronous.
+tensor_ops::RowIndexBuffer prefix_ancestors_gpu(const PrefixTrie& trie);

@@ -204,7 +204,11 @@ public:
     RowIndexBuffer& operator=(const RowIndexBuffer&) = delete;
     RowIndexBuffer(RowIndexBuffer&& other) noexcept;
     RowIndexBuffer& operator=(RowIndexBuffer&& other) noexcept;
+    // `size` entries left for the caller to fill on the device (through
+    // mutable_data()), each at most max_row.
+    static RowIndexBuffer allocate(std::size_t size, std::size_t max_row);
     const std::uint32_t* data() const { return ptr_; }
+    std::uint32_t* mutable_data() { return ptr_; }
     std::size_t size() const { return size_; }
     bool empty() const { return size_ == 0; }
     std::size_t max_row() const { return max_row_; }  // largest index (0 when empty)

@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <random>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -365,6 +366,30 @@ int main(int argc, char** argv) {
         expect(std::vector<std::size_t>(trie.node_anc.begin() + 16, trie.node_anc.begin() + 20) ==
                    std::vector<std::size_t>({4, 0, 0, 0}), "trie ancestor chain of node 4");
         expect(trie.last_rows() == std::vector<std::size_t>({2, 3, 4, 5}), "trie last rows");
+        // the device-built table equals the host one, on this trie and on
+        // branchier ones (tiny vocabularies, repeated and nested prompts)
+        std::mt19937 trng(17);
+        const std::vector<std::vector<std::vector<int>>> tries = {
+            {{1, 2, 3}, {1, 2, 4}, {5}, {1, 2, 3, 6}},
+            {std::vector<int>(50, 7), std::vector<int>(50, 7), std::vector<int>(9, 7), {7, 8}},
+            [&] {
+                std::vector<std::vector<int>> b(30);
+                for (auto& q : b) {
+                    q.resize(1 + trng() % 70);
+                    for (int& tok : q) tok = static_cast<int>(trng() % 3);
+                }
+                return b;
+            }()};
+        for (const auto& batch : tries) {
+            const PrefixTrie tt = build_prefix_trie(batch);
+            const tensor_ops::RowIndexBuffer dev = prefix_ancestors_gpu(build_prefix_trie(batch, false));
+            std::vector<std::uint32_t> got(dev.size());
+            expect(hipMemcpy(got.data(), dev.data(), got.size() * 4, hipMemcpyDeviceToHost) == hipSuccess,
+                   "copy device ancestor table");
+            expect(got.size() == tt.node_anc.size() && std::equal(got.begin(), got.end(), tt.node_anc.begin()),
+                   "prefix_ancestors_gpu equals the host ancestor table");
+            expect(dev.max_row() == tt.nodes() - 1, "device ancestor table row bound");
+        }
         expect_throw<std::runtime_error>([] { build_prefix_trie({}); }, "generate received an empty input batch",
                                          "empty batch");
         expect_throw<std::invalid_argument>([] { build_prefix_trie({{1}, {}}); }, "empty input", "empty sequence");
