@@ -167,6 +167,45 @@ def test_fp8_staged_entry_points_are_rejected(gpu_device):
     w.release()
 
 
+@pytest.mark.parametrize("n,stride,rows_cap", [(448, 512, None), (512, 512, 4097), (8, 8, 3), (64, 128, 1)])
+def test_quantiser_short_rows(gpu_device, n, stride, rows_cap):
+    """Rows of at most 512 values (the activations' path: several rows per
+    wave) bit for bit against the oracle's quantiser: every finite bf16 value
+    at 6 row scales, zero rows, zero padding past n, and row counts that are
+    not a multiple of the rows per wave."""
+    from aps2026_amd import capi
+    allv = synth.bf16_bits_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    allv = allv[np.isfinite(allv)]
+    rows = []
+    for e in (-133, -85, -20, 0, 60, 127):
+        amax = np.float32(np.ldexp(np.float32(1.5 if e < 127 else 1.0), e))
+        amax = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(np.array([amax], np.float32)))[0]
+        vals = allv[np.abs(allv) <= amax]
+        for i in range(0, vals.size, n - 1):
+            row = np.zeros(n, np.float32)
+            row[0] = amax
+            chunk = vals[i:i + n - 1]
+            row[1:1 + chunk.size] = chunk
+            rows.append(row)
+    rows.append(np.zeros(n, np.float32))
+    x = np.stack(rows)
+    if rows_cap is not None:
+        x = np.resize(x, (rows_cap, n))
+    note(f"short quantiser n={n} stride={stride} rows={x.shape[0]}")
+    want_q, want_s = oracle.quantise_rows_e4m3(x)
+    xd = to_dev_bf16(synth.f32_to_bf16_bits(x), gpu_device)
+    q = torch.full((x.shape[0], stride), 0x7F, dtype=torch.uint8, device=gpu_device)
+    sc = torch.empty(x.shape[0], dtype=torch.float32, device=gpu_device)
+    rc = capi.lib().aps_quantise_rows_e4m3(xd.data_ptr(), n, n, q.data_ptr(), stride, sc.data_ptr(), x.shape[0],
+                                           None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), want_s.view(np.uint32))
+    got = q.cpu().numpy()
+    np.testing.assert_array_equal(got[:, :n], want_q)
+    assert not got[:, n:].any()
+
+
 def test_quantiser_every_bf16_value_at_many_scales(gpu_device):
     """Every finite bf16 value through aps_quantise_rows_e4m3 at 40 row scales
     (amax from 2^-133, a subnormal scale, through 2^-80, the smallest scale of
