@@ -220,12 +220,13 @@ def test_router_kernel_shapes(gpu_device, E, H):
         w.release()
 
 
-@pytest.mark.parametrize("E,T", [(16, 8192), (16, 5000), (8, 4097), (2, 7777)])
+@pytest.mark.parametrize("E,T", [(16, 8192), (16, 5000), (8, 4097), (2, 7777), (16, 10240), (12, 12345)])
 def test_router_32_token_workgroups(gpu_device, E, T):
     """Batches of 4,097 .. 8,192 tokens with E <= 16 (on a 256-CU MI355X)
     take the eight-wave router, 32 tokens per workgroup, two quarter-tile
     bytes of the histogram each (7,777 leaves a partial workgroup and a
-    partial tile).  Logits bit-exact from the staged entry point; logits,
+    partial tile); the larger batches (10,240 and 12,345 tokens) go back to
+    16-token workgroups.  Logits bit-exact from the staged entry point; logits,
     routes, counts and permutation bit-exact from the fused forward; fp32 x
     with bf16 experts (the router also writes the FFN's bf16 copy of x)
     gives the same output as the grouped entry point, which converts x on
