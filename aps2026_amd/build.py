@@ -71,10 +71,30 @@ def _run(cmd, verbose):
         print(err, file=sys.stderr)
 
 
+OBJ_DIR = os.path.join(HERE, "_build")
+
+
+def build_hip(out: str = LIB, defines=(), verbose: bool = False, jobs: int = 0) -> str:
+    """Compile every csrc/*.hip to an object (in parallel) and link them into
+    the shared library `out`.  `defines` are extra -D flags (A/B builds)."""
+    from concurrent.futures import ThreadPoolExecutor
+    tag = "_".join(d.replace("=", "-") for d in defines) or "default"
+    odir = os.path.join(OBJ_DIR, tag)
+    os.makedirs(odir, exist_ok=True)
+    cflags = [f for f in FLAGS if f not in ("-shared",)] + ["-D" + d for d in defines]
+    srcs = sources()
+    objs = [os.path.join(odir, os.path.basename(src)[:-4] + ".o") for src in srcs]
+    jobs = jobs or max(1, min(len(srcs), os.cpu_count() or 1, 16))
+    with ThreadPoolExecutor(jobs) as ex:
+        list(ex.map(lambda so: _run([HIPCC, *cflags, "-c", "-o", so[1], so[0]], verbose), zip(srcs, objs)))
+    tmp = out + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> str:
-    tmp = LIB + ".tmp"
-    _run([HIPCC, *FLAGS, "-o", tmp, *sources()], verbose)
-    os.replace(tmp, LIB)
+    build_hip(LIB, verbose=verbose)
     # C++ host API over the C ABI
     tmp = LAYERS_LIB + ".tmp"
     cpp = sorted(glob.glob(os.path.join(HERE, "cpp", "*.cpp")))

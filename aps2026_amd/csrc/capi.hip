@@ -115,8 +115,11 @@ void make_layout(const WeightSet& w, int64_t rows, aps_moe_ws_layout* L) {
     L->xq = 0;
     L->xq_scale = 0;
     if (w.compute == APS_DTYPE_BF16) {
-        // bf16 copy of x for the fused entry points when x arrives as fp32
-        L->xq = take(T * static_cast<size_t>(w.H) * 2);
+        // bf16 copy of x for the fused entry points when x arrives as fp32:
+        // written by the router, last read by the w1||w3 GEMM, so it shares
+        // the bytes of y (first written by the w2 GEMM, after it); nothing is
+        // reserved for it, whatever the dtype of x
+        L->xq = L->y;
     } else if (w.compute == APS_DTYPE_E4M3) {
         L->xq = take(T * static_cast<size_t>(w.H));
         L->xq_scale = take(T * 4);

@@ -146,6 +146,11 @@ struct Bf16Fmt {
     __device__ static frag_t load(const uint8_t* st, int row, int kk, int lane) {
         return __builtin_bit_cast(frag_t, *reinterpret_cast<const u32x4_t*>(st + swz(row, 2 * kk + (lane >> 5))));
     }
+    // a fragment is one ds_read_b128; load_part(.., 0) is load()
+    static constexpr int kParts = 1;
+    __device__ static void load_part(frag_t& f, const uint8_t* st, int row, int kk, int lane, int) {
+        f = load(st, row, kk, lane);
+    }
     __device__ static f32x16_t mma(const frag_t& a, const frag_t& b, f32x16_t c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
@@ -169,6 +174,17 @@ struct Fp8Fmt {
         const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(st + swz(row, c));
         const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(st + swz(row, c + 1));
         return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+    // a fragment is two ds_read_b128 (its low and high 16 bytes), issued
+    // separately by the interleaved main loop
+    static constexpr int kParts = 2;
+    __device__ static void load_part(frag_t& f, const uint8_t* st, int row, int kk, int lane, int part) {
+        const int c = 4 * kk + 2 * (lane >> 5) + part;
+        const i32x4_t v = *reinterpret_cast<const i32x4_t*>(st + swz(row, c));
+        const i32x4_t lo = __builtin_shufflevector(f, f, 0, 1, 2, 3);
+        const i32x4_t hi = __builtin_shufflevector(f, f, 4, 5, 6, 7);
+        f = part == 0 ? __builtin_shufflevector(v, hi, 0, 1, 2, 3, 4, 5, 6, 7)
+                      : __builtin_shufflevector(lo, v, 0, 1, 2, 3, 4, 5, 6, 7);
     }
     // e4m3 x e4m3 (format code 0 for both operands), unit scales
     __device__ static f32x16_t mma(const frag_t& a, const frag_t& b, f32x16_t c) {
@@ -297,6 +313,152 @@ __device__ inline void mainloop3(Ring3& ring, const Slots& sl, int KT, int wave,
         prev = cur;
         cur = nxt;
     }
+}
+
+// s_waitcnt lgkmcnt(n) for n in 0..15 known only after unrolling.
+__device__ inline void wait_lgkm(int n) {
+    switch (n) {
+        case 15: wait_lgkm_n<15>(); break;
+        case 14: wait_lgkm_n<14>(); break;
+        case 13: wait_lgkm_n<13>(); break;
+        case 12: wait_lgkm_n<12>(); break;
+        case 11: wait_lgkm_n<11>(); break;
+        case 10: wait_lgkm_n<10>(); break;
+        case 9: wait_lgkm_n<9>(); break;
+        case 8: wait_lgkm_n<8>(); break;
+        case 7: wait_lgkm_n<7>(); break;
+        case 6: wait_lgkm_n<6>(); break;
+        case 5: wait_lgkm_n<5>(); break;
+        case 4: wait_lgkm_n<4>(); break;
+        case 3: wait_lgkm_n<3>(); break;
+        case 2: wait_lgkm_n<2>(); break;
+        case 1: wait_lgkm_n<1>(); break;
+        default: wait_lgkm_n<0>(); break;
+    }
+}
+
+// Part `part` of fragment o of a wave's step-kk operands, fragments in the
+// order the step's MFMAs first need them: a0, b0, b1, b2, b3, a1.
+template <class Fmt>
+__device__ inline void load_frag_o(Frags<Fmt>& f, const uint8_t* st, int kk, int lane, int aR, int bR, int o,
+                                   int part) {
+    if (o == 0) Fmt::load_part(f.a[0], st, aR + (lane & 31), kk, lane, part);
+    else if (o == 5) Fmt::load_part(f.a[1], st, aR + 32 + (lane & 31), kk, lane, part);
+    else Fmt::load_part(f.b[o - 1], st, bR + (o - 1) * 32 + (lane & 31), kk, lane, part);
+}
+
+// MFMA q (0..7) of a step: acc[q / 4][q % 4] += b[q % 4] x a[q / 4].
+template <class Fmt>
+__device__ inline void mma_q(const Frags<Fmt>& f, f32x16_t (&acc)[2][4], int q) {
+    acc[q >> 2][q & 3] = Fmt::mma(f.b[q & 3], f.a[q >> 2], acc[q >> 2][q & 3]);
+}
+
+// One stage of the interleaved main loop.  Every MFMA is issued with the
+// fragment reads and stage copies of its shadow after it, so that the matrix
+// pipe keeps working while the wave issues them (issued in a burst between
+// groups of eight MFMAs, they left the pipe idle for about a quarter of each
+// step).  A step s < kSub - 1 issues MFMA q (q = 0..7) and then:
+//   q = 0, 1, 2: two fragments of step s + 1 (2P ds_read_b128, P = reads per
+//                fragment), in the order the next step's MFMAs need them;
+//   q = 3 .. 7 : this step's share of the refill copies (REFILL).
+// The compiler drains lgkmcnt before a step's first MFMA (it cannot count
+// LDS reads past in-flight LDS DMA), so the reads go early, five MFMAs
+// before that wait.  The last step (the stage hand-over) issues MFMAs 0, 1,
+// waits for stage kt + 1 (vmcnt) and its own fragments, passes one
+// s_barrier, and reads stage kt + 1's first fragments in the shadow of
+// MFMAs 2..4.  REFILL: this stage refills the slot of stage kt - 1 with
+// stage kt + 2; NEXT: a stage kt + 1 exists; PEND: stage kt + 2's copies are
+// in flight at the hand-over (vmcnt(12) instead of 0).  Every output element
+// still accumulates k ascending: only issue order changes, not arithmetic.
+template <bool TALL, class Fmt, bool REFILL, bool NEXT, bool PEND>
+__device__ inline void stage_il(Ring3& ring, const Slots& sl, int kt, int wave, int lane, int aR, int bR,
+                                Frags<Fmt> (&f)[2], f32x16_t (&acc)[2][4]) {
+    constexpr int kSub = Fmt::kSub, P = Fmt::kParts;
+    const uint8_t* st = ring.s[kt % 3];
+#pragma unroll
+    for (int s = 0; s < kSub; ++s) {
+        const Frags<Fmt>& fc = f[s & 1];
+        Frags<Fmt>& fn = f[(s + 1) & 1];
+        if (s + 1 < kSub) {
+            const int c0 = 12 * s / (kSub - 1), nc = 12 * (s + 1) / (kSub - 1) - c0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                mma_q<Fmt>(fc, acc, q);
+                APS_PIN();
+                if (q < 3) {
+#pragma unroll
+                    for (int o = 2 * q; o < 2 * q + 2; ++o)
+#pragma unroll
+                        for (int part = 0; part < P; ++part) load_frag_o<Fmt>(fn, st, s + 1, lane, aR, bR, o, part);
+                } else if (REFILL) {
+#pragma unroll
+                    for (int c = 0; c < nc; ++c)
+                        if (3 + c * 5 / nc == q)
+                            issue_slots<TALL>(ring.s[(kt + 2) % 3], sl, kt + 2, wave, c0 + c, c0 + c + 1);
+                }
+                APS_PIN();
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                mma_q<Fmt>(fc, acc, q);
+                APS_PIN();
+            }
+            if (NEXT) {
+                if (PEND) wait_vm_lgkm0<12>();
+                else wait_vm_lgkm0<0>();
+                raw_barrier();
+            } else {
+                wait_lgkm0();
+            }
+            APS_PIN();
+            const uint8_t* sn = ring.s[(kt + 1) % 3];
+#pragma unroll
+            for (int q = 2; q < 8; ++q) {
+                mma_q<Fmt>(fc, acc, q);
+                APS_PIN();
+                if (NEXT && q < 5) {
+#pragma unroll
+                    for (int o = 2 * (q - 2); o < 2 * (q - 2) + 2; ++o)
+#pragma unroll
+                        for (int part = 0; part < P; ++part) load_frag_o<Fmt>(f[0], sn, 0, lane, aR, bR, o, part);
+                }
+                APS_PIN();
+            }
+        }
+    }
+}
+
+// acc[i][j] += stage rows aR + 32i (A) x stage rows bR + 32j (B) over KT
+// stages, on the three-stage ring, with the interleaved stage bodies above.
+// Stage kt lives in slot kt % 3; stages 0..2 are copied up front, stage
+// kt + 2 during stage kt (1 <= kt <= KT - 3).
+template <bool TALL, class Fmt>
+__device__ inline void mainloop_il(Ring3& ring, const Slots& sl, int KT, int wave, int lane, int aR, int bR,
+                                   f32x16_t (&acc)[2][4]) {
+    constexpr int P = Fmt::kParts;
+    issue_slots<TALL>(ring.s[0], sl, 0, wave, 0, 12);
+    if (KT > 1) issue_slots<TALL>(ring.s[1], sl, 1, wave, 0, 12);
+    if (KT > 2) issue_slots<TALL>(ring.s[2], sl, 2, wave, 0, 12);
+    if (KT > 2) wait_vm_lgkm0<24>();
+    else if (KT > 1) wait_vm_lgkm0<12>();
+    else wait_vm_lgkm0<0>();
+    raw_barrier();
+    Frags<Fmt> f[2];
+#pragma unroll
+    for (int o = 0; o < 6; ++o)
+#pragma unroll
+        for (int part = 0; part < P; ++part) load_frag_o<Fmt>(f[0], ring.s[0], 0, lane, aR, bR, o, part);
+    APS_PIN();
+    if (KT == 1) {
+        stage_il<TALL, Fmt, false, false, false>(ring, sl, 0, wave, lane, aR, bR, f, acc);
+        return;
+    }
+    if (KT > 2) stage_il<TALL, Fmt, false, true, true>(ring, sl, 0, wave, lane, aR, bR, f, acc);
+    else stage_il<TALL, Fmt, false, true, false>(ring, sl, 0, wave, lane, aR, bR, f, acc);
+    for (int kt = 1; kt + 2 < KT; ++kt) stage_il<TALL, Fmt, true, true, true>(ring, sl, kt, wave, lane, aR, bR, f, acc);
+    if (KT > 2) stage_il<TALL, Fmt, false, true, false>(ring, sl, KT - 2, wave, lane, aR, bR, f, acc);
+    stage_il<TALL, Fmt, false, false, false>(ring, sl, KT - 1, wave, lane, aR, bR, f, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -431,7 +593,7 @@ __device__ inline void ffn_up_block(Ring3& ring, const uint8_t* __restrict__ x, 
     const int aR = wave_a_row<TALL>(wave), bR = wave_b_row<TALL>(wave);
     f32x16_t acc[2][4];
     zero_acc(acc);
-    mainloop3<TALL, Fmt>(ring, sl, KT, wave, lane, aR, bR, acc);
+    mainloop_il<TALL, Fmt>(ring, sl, KT, wave, lane, aR, bR, acc);
 
     // Epilogue: scales (fp8), SwiGLU in registers (B fragments 0,1 are gate
     // columns 0..63 of the wave's column block, 2,3 the same up columns), the

@@ -100,7 +100,9 @@ typedef struct aps_moe_ws_layout {
     size_t y;               /* [2*rows][hidden], f32 (F32 path) or bf16 */
     size_t xq;              /* x in the compute dtype when the caller
                                passes another one: bf16 [rows][hidden]
-                               (bf16 weights, fp32 x), e4m3 (fp8 path) */
+                               (bf16 weights, fp32 x; it shares y's
+                               bytes: dead before y is written), e4m3
+                               (fp8 path, its own bytes) */
     size_t xq_scale;        /* fp8 path: f32 [rows] per-token scale */
     size_t actq;            /* fp8 path: e4m3 act [2*rows][ffn rounded
                                up to 128], zero padded              */
