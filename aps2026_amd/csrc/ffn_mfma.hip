@@ -315,152 +315,6 @@ __device__ inline void mainloop3(Ring3& ring, const Slots& sl, int KT, int wave,
     }
 }
 
-// s_waitcnt lgkmcnt(n) for n in 0..15 known only after unrolling.
-__device__ inline void wait_lgkm(int n) {
-    switch (n) {
-        case 15: wait_lgkm_n<15>(); break;
-        case 14: wait_lgkm_n<14>(); break;
-        case 13: wait_lgkm_n<13>(); break;
-        case 12: wait_lgkm_n<12>(); break;
-        case 11: wait_lgkm_n<11>(); break;
-        case 10: wait_lgkm_n<10>(); break;
-        case 9: wait_lgkm_n<9>(); break;
-        case 8: wait_lgkm_n<8>(); break;
-        case 7: wait_lgkm_n<7>(); break;
-        case 6: wait_lgkm_n<6>(); break;
-        case 5: wait_lgkm_n<5>(); break;
-        case 4: wait_lgkm_n<4>(); break;
-        case 3: wait_lgkm_n<3>(); break;
-        case 2: wait_lgkm_n<2>(); break;
-        case 1: wait_lgkm_n<1>(); break;
-        default: wait_lgkm_n<0>(); break;
-    }
-}
-
-// Part `part` of fragment o of a wave's step-kk operands, fragments in the
-// order the step's MFMAs first need them: a0, b0, b1, b2, b3, a1.
-template <class Fmt>
-__device__ inline void load_frag_o(Frags<Fmt>& f, const uint8_t* st, int kk, int lane, int aR, int bR, int o,
-                                   int part) {
-    if (o == 0) Fmt::load_part(f.a[0], st, aR + (lane & 31), kk, lane, part);
-    else if (o == 5) Fmt::load_part(f.a[1], st, aR + 32 + (lane & 31), kk, lane, part);
-    else Fmt::load_part(f.b[o - 1], st, bR + (o - 1) * 32 + (lane & 31), kk, lane, part);
-}
-
-// MFMA q (0..7) of a step: acc[q / 4][q % 4] += b[q % 4] x a[q / 4].
-template <class Fmt>
-__device__ inline void mma_q(const Frags<Fmt>& f, f32x16_t (&acc)[2][4], int q) {
-    acc[q >> 2][q & 3] = Fmt::mma(f.b[q & 3], f.a[q >> 2], acc[q >> 2][q & 3]);
-}
-
-// One stage of the interleaved main loop.  Every MFMA is issued with the
-// fragment reads and stage copies of its shadow after it, so that the matrix
-// pipe keeps working while the wave issues them (issued in a burst between
-// groups of eight MFMAs, they left the pipe idle for about a quarter of each
-// step).  A step s < kSub - 1 issues MFMA q (q = 0..7) and then:
-//   q = 0, 1, 2: two fragments of step s + 1 (2P ds_read_b128, P = reads per
-//                fragment), in the order the next step's MFMAs need them;
-//   q = 3 .. 7 : this step's share of the refill copies (REFILL).
-// The compiler drains lgkmcnt before a step's first MFMA (it cannot count
-// LDS reads past in-flight LDS DMA), so the reads go early, five MFMAs
-// before that wait.  The last step (the stage hand-over) issues MFMAs 0, 1,
-// waits for stage kt + 1 (vmcnt) and its own fragments, passes one
-// s_barrier, and reads stage kt + 1's first fragments in the shadow of
-// MFMAs 2..4.  REFILL: this stage refills the slot of stage kt - 1 with
-// stage kt + 2; NEXT: a stage kt + 1 exists; PEND: stage kt + 2's copies are
-// in flight at the hand-over (vmcnt(12) instead of 0).  Every output element
-// still accumulates k ascending: only issue order changes, not arithmetic.
-template <bool TALL, class Fmt, bool REFILL, bool NEXT, bool PEND>
-__device__ inline void stage_il(Ring3& ring, const Slots& sl, int kt, int wave, int lane, int aR, int bR,
-                                Frags<Fmt> (&f)[2], f32x16_t (&acc)[2][4]) {
-    constexpr int kSub = Fmt::kSub, P = Fmt::kParts;
-    const uint8_t* st = ring.s[kt % 3];
-#pragma unroll
-    for (int s = 0; s < kSub; ++s) {
-        const Frags<Fmt>& fc = f[s & 1];
-        Frags<Fmt>& fn = f[(s + 1) & 1];
-        if (s + 1 < kSub) {
-            const int c0 = 12 * s / (kSub - 1), nc = 12 * (s + 1) / (kSub - 1) - c0;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                mma_q<Fmt>(fc, acc, q);
-                APS_PIN();
-                if (q < 3) {
-#pragma unroll
-                    for (int o = 2 * q; o < 2 * q + 2; ++o)
-#pragma unroll
-                        for (int part = 0; part < P; ++part) load_frag_o<Fmt>(fn, st, s + 1, lane, aR, bR, o, part);
-                } else if (REFILL) {
-#pragma unroll
-                    for (int c = 0; c < nc; ++c)
-                        if (3 + c * 5 / nc == q)
-                            issue_slots<TALL>(ring.s[(kt + 2) % 3], sl, kt + 2, wave, c0 + c, c0 + c + 1);
-                }
-                APS_PIN();
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                mma_q<Fmt>(fc, acc, q);
-                APS_PIN();
-            }
-            if (NEXT) {
-                if (PEND) wait_vm_lgkm0<12>();
-                else wait_vm_lgkm0<0>();
-                raw_barrier();
-            } else {
-                wait_lgkm0();
-            }
-            APS_PIN();
-            const uint8_t* sn = ring.s[(kt + 1) % 3];
-#pragma unroll
-            for (int q = 2; q < 8; ++q) {
-                mma_q<Fmt>(fc, acc, q);
-                APS_PIN();
-                if (NEXT && q < 5) {
-#pragma unroll
-                    for (int o = 2 * (q - 2); o < 2 * (q - 2) + 2; ++o)
-#pragma unroll
-                        for (int part = 0; part < P; ++part) load_frag_o<Fmt>(f[0], sn, 0, lane, aR, bR, o, part);
-                }
-                APS_PIN();
-            }
-        }
-    }
-}
-
-// acc[i][j] += stage rows aR + 32i (A) x stage rows bR + 32j (B) over KT
-// stages, on the three-stage ring, with the interleaved stage bodies above.
-// Stage kt lives in slot kt % 3; stages 0..2 are copied up front, stage
-// kt + 2 during stage kt (1 <= kt <= KT - 3).
-template <bool TALL, class Fmt>
-__device__ inline void mainloop_il(Ring3& ring, const Slots& sl, int KT, int wave, int lane, int aR, int bR,
-                                   f32x16_t (&acc)[2][4]) {
-    constexpr int P = Fmt::kParts;
-    issue_slots<TALL>(ring.s[0], sl, 0, wave, 0, 12);
-    if (KT > 1) issue_slots<TALL>(ring.s[1], sl, 1, wave, 0, 12);
-    if (KT > 2) issue_slots<TALL>(ring.s[2], sl, 2, wave, 0, 12);
-    if (KT > 2) wait_vm_lgkm0<24>();
-    else if (KT > 1) wait_vm_lgkm0<12>();
-    else wait_vm_lgkm0<0>();
-    raw_barrier();
-    Frags<Fmt> f[2];
-#pragma unroll
-    for (int o = 0; o < 6; ++o)
-#pragma unroll
-        for (int part = 0; part < P; ++part) load_frag_o<Fmt>(f[0], ring.s[0], 0, lane, aR, bR, o, part);
-    APS_PIN();
-    if (KT == 1) {
-        stage_il<TALL, Fmt, false, false, false>(ring, sl, 0, wave, lane, aR, bR, f, acc);
-        return;
-    }
-    if (KT > 2) stage_il<TALL, Fmt, false, true, true>(ring, sl, 0, wave, lane, aR, bR, f, acc);
-    else stage_il<TALL, Fmt, false, true, false>(ring, sl, 0, wave, lane, aR, bR, f, acc);
-    for (int kt = 1; kt + 2 < KT; ++kt) stage_il<TALL, Fmt, true, true, true>(ring, sl, kt, wave, lane, aR, bR, f, acc);
-    if (KT > 2) stage_il<TALL, Fmt, false, true, false>(ring, sl, KT - 2, wave, lane, aR, bR, f, acc);
-    stage_il<TALL, Fmt, false, false, false>(ring, sl, KT - 1, wave, lane, aR, bR, f, acc);
-}
-
 // ---------------------------------------------------------------------------
 // Work list, expert by expert.  `nblk` column blocks per row (F/64 for
 // w1||w3, H/128 for w2); pairs = nblk / 2 wide blocks per 128-row tile and,
@@ -557,56 +411,294 @@ __device__ inline float4 col_scales(const float* __restrict__ s, int c0, int j, 
     return *reinterpret_cast<const float4*>(s + c0 + 32 * j + 8 * q + 4 * (lane >> 5));
 }
 
+// s_waitcnt lgkmcnt(n) for n in 0..15 known only after unrolling.
+__device__ inline void wait_lgkm(int n) {
+    switch (n) {
+        case 15: wait_lgkm_n<15>(); break;
+        case 14: wait_lgkm_n<14>(); break;
+        case 13: wait_lgkm_n<13>(); break;
+        case 12: wait_lgkm_n<12>(); break;
+        case 11: wait_lgkm_n<11>(); break;
+        case 10: wait_lgkm_n<10>(); break;
+        case 9: wait_lgkm_n<9>(); break;
+        case 8: wait_lgkm_n<8>(); break;
+        case 7: wait_lgkm_n<7>(); break;
+        case 6: wait_lgkm_n<6>(); break;
+        case 5: wait_lgkm_n<5>(); break;
+        case 4: wait_lgkm_n<4>(); break;
+        case 3: wait_lgkm_n<3>(); break;
+        case 2: wait_lgkm_n<2>(); break;
+        case 1: wait_lgkm_n<1>(); break;
+        default: wait_lgkm_n<0>(); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// w1||w3 pieces.  A piece is a rectangle of one expert's act output: RA of
+// its positions x a range of act columns, computed by one 4-wave block over
+// the whole K.  The waves form a WM x WN grid; wave (wm, wn) = (w % WM,
+// w / WM) owns MI 32-row A fragments and NJ 32-row B fragments: NJ / 2 gate
+// and the same NJ / 2 up columns, so that SwiGLU closes inside each lane.
+//   W: 128 rows x 2 column blocks  (WM 2, WN 2, MI 2, NJ 4)  stage 384 rows
+//   T: 256 rows x 1 column block   (WM 4, WN 1, MI 2, NJ 4)  stage 384 rows
+//   S: 128 rows x 1 column block   (WM 2, WN 2, MI 2, NJ 2)  stage 256 rows
+//   Q: 128 rows x 1/2 column block (WM 4, WN 1, MI 1, NJ 2)  stage 192 rows
+// A column block is 64 act columns (128 packed rows: 64 gate, then the same
+// 64 up).  NJ = 2 waves own half h of one (32 gate + 32 up columns): S's
+// wave wn takes half wn, a Q piece one half for all four waves.  A position
+// always sits at the same lane and fragment row, a column at the same
+// fragment column, and every output element accumulates the same MFMA
+// sequence over k ascending, whichever piece computes it: the shapes are
+// interchangeable bit for bit, and the scheduler below picks them freely.
+enum PieceKind { kPieceW = 0, kPieceT = 1, kPieceS = 2, kPieceQ = 3 };
+
+template <int KIND>
+struct PShape;
+template <>
+struct PShape<kPieceW> { static constexpr int WM = 2, WN = 2, MI = 2, NJ = 4; };
+template <>
+struct PShape<kPieceT> { static constexpr int WM = 4, WN = 1, MI = 2, NJ = 4; };
+template <>
+struct PShape<kPieceS> { static constexpr int WM = 2, WN = 2, MI = 2, NJ = 2; };
+template <>
+struct PShape<kPieceQ> { static constexpr int WM = 4, WN = 1, MI = 1, NJ = 2; };
+
+template <class Sh>
+struct PDims {
+    static constexpr int RA = Sh::WM * Sh::MI * 32;      // A rows (positions) per stage
+    static constexpr int RB = Sh::WN * Sh::NJ * 32;      // B rows (packed weight rows) per stage
+    static constexpr int NA = RA / 32;                   // A load slots per wave
+    static constexpr int NS = (RA + RB) / 32;            // load slots per wave
+    static constexpr int M = Sh::MI * Sh::NJ;            // MFMAs per step
+    static constexpr int NR = Sh::MI + Sh::NJ;           // fragments per step
+    static constexpr int kCols = Sh::WN * Sh::NJ / 2 * 32;  // act columns of the piece
+    static_assert(RA + RB <= kStageRows, "stage fits the ring");
+};
+
+struct Piece {
+    int kind, expert, cb0, half;   // half: the column-block half of a Q piece
+    uint32_t m0, end;              // first position of the piece, expert's end
+};
+
+template <class Fmt, class Sh>
+struct PFrags {
+    typename Fmt::frag_t a[Sh::MI];
+    typename Fmt::frag_t b[Sh::NJ];
+};
+
+// Part `part` of fragment o of a wave's step-kk operands, in the order the
+// step's MFMAs first need them: a0, b0 .. b(NJ-1), a1 .. a(MI-1).
+template <class Fmt, class Sh>
+__device__ inline void pload(PFrags<Fmt, Sh>& f, const uint8_t* st, int kk, int lane, int aR, int bR, int o,
+                             int part) {
+    if (o == 0) Fmt::load_part(f.a[0], st, aR + (lane & 31), kk, lane, part);
+    else if (o <= Sh::NJ) Fmt::load_part(f.b[o - 1], st, bR + (o - 1) * 32 + (lane & 31), kk, lane, part);
+    else Fmt::load_part(f.a[o - Sh::NJ], st, aR + (o - Sh::NJ) * 32 + (lane & 31), kk, lane, part);
+}
+
+// MFMA q of a step: acc[q / NJ][q % NJ] += b[q % NJ] x a[q / NJ].
+template <class Fmt, class Sh>
+__device__ inline void pmma(const PFrags<Fmt, Sh>& f, f32x16_t (&acc)[Sh::MI][Sh::NJ], int q) {
+    acc[q / Sh::NJ][q % Sh::NJ] = Fmt::mma(f.b[q % Sh::NJ], f.a[q / Sh::NJ], acc[q / Sh::NJ][q % Sh::NJ]);
+}
+
+// Copies of load slots [lo, hi) of stage kt (A slots advance one 128-byte
+// row chunk per stage, B slots one 16 KB tile image).
+template <class Sh>
+__device__ inline void pissue(uint8_t* stage, const Slots& sl, int kt, int wave, int lo, int hi) {
+#pragma unroll
+    for (int s = lo; s < hi; ++s) {
+        const int64_t adv = s < PDims<Sh>::NA ? static_cast<int64_t>(kt) * kRowBytes
+                                              : static_cast<int64_t>(kt) * kImageBytes;
+        dma16(sl.p[s] + adv, stage + (32 * s + 8 * wave) * kRowBytes);
+    }
+}
+
+// One stage of the three-stage ring.  Every MFMA is issued with the fragment
+// reads and stage copies of its shadow after it, so that the matrix pipe
+// keeps working while the wave issues them (issued in a burst between groups
+// of MFMAs, they left the pipe idle for about a quarter of each step).  A
+// step s < kSub - 1 issues MFMA q and then: for q < MR, its share of the
+// next step's fragments (MR = 3 of 8 MFMAs, fewer for small pieces); for
+// q >= MR, its share of this step's refill copies (REFILL).  The compiler
+// drains lgkmcnt before a step's first MFMA (it cannot count LDS reads past
+// in-flight LDS DMA), so the reads go first, well before that wait.  The
+// last step (the stage hand-over) issues MFMAs 0 .. MB - 1, waits for stage
+// kt + 1 (vmcnt) and its own fragments, passes one s_barrier, and reads
+// stage kt + 1's first fragments in the shadow of the remaining MFMAs.
+// REFILL: this stage refills the slot of stage kt - 1 with stage kt + 2;
+// NEXT: a stage kt + 1 exists; PEND: stage kt + 2's copies are in flight at
+// the hand-over.  Only the issue order is chosen here: every output element
+// accumulates its MFMAs in k order.
+template <class Sh, class Fmt, bool REFILL, bool NEXT, bool PEND>
+__device__ inline void pstage(Ring3& ring, const Slots& sl, int kt, int wave, int lane, int aR, int bR,
+                              PFrags<Fmt, Sh> (&f)[2], f32x16_t (&acc)[Sh::MI][Sh::NJ]) {
+    typedef PDims<Sh> D;
+    constexpr int kSub = Fmt::kSub, P = Fmt::kParts;
+    constexpr int M = D::M, NR = D::NR, NS = D::NS;
+    constexpr int MR = M >= 8 ? 3 : (M >= 4 ? 2 : 1);   // MFMAs carrying the reads
+    constexpr int MB = M >= 8 ? 2 : 1;                  // MFMAs before the hand-over barrier
+    const uint8_t* st = ring.s[kt % 3];
+#pragma unroll
+    for (int s = 0; s < kSub; ++s) {
+        const PFrags<Fmt, Sh>& fc = f[s & 1];
+        PFrags<Fmt, Sh>& fn = f[(s + 1) & 1];
+        if (s + 1 < kSub) {
+            const int c0 = NS * s / (kSub - 1), nc = NS * (s + 1) / (kSub - 1) - c0;
+#pragma unroll
+            for (int q = 0; q < M; ++q) {
+                pmma<Fmt, Sh>(fc, acc, q);
+                APS_PIN();
+                if (q < MR) {
+#pragma unroll
+                    for (int o = q * NR / MR; o < (q + 1) * NR / MR; ++o)
+#pragma unroll
+                        for (int part = 0; part < P; ++part) pload<Fmt, Sh>(fn, st, s + 1, lane, aR, bR, o, part);
+                }
+                if (REFILL) {
+#pragma unroll
+                    for (int c = 0; c < nc; ++c) {
+                        const int qc = M > MR ? MR + c * (M - MR) / nc : M - 1;
+                        if (qc == q) pissue<Sh>(ring.s[(kt + 2) % 3], sl, kt + 2, wave, c0 + c, c0 + c + 1);
+                    }
+                }
+                APS_PIN();
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < MB; ++q) {
+                pmma<Fmt, Sh>(fc, acc, q);
+                APS_PIN();
+            }
+            if (NEXT) {
+                if (PEND) wait_vm_lgkm0<NS>();
+                else wait_vm_lgkm0<0>();
+                raw_barrier();
+            } else {
+                wait_lgkm0();
+            }
+            APS_PIN();
+            const uint8_t* sn = ring.s[(kt + 1) % 3];
+            constexpr int MRn = M - MB < 3 ? M - MB : 3;  // MFMAs carrying the next stage's reads
+#pragma unroll
+            for (int q = MB; q < M; ++q) {
+                pmma<Fmt, Sh>(fc, acc, q);
+                APS_PIN();
+                if (NEXT && q - MB < MRn) {
+                    const int k = q - MB;
+#pragma unroll
+                    for (int o = k * NR / MRn; o < (k + 1) * NR / MRn; ++o)
+#pragma unroll
+                        for (int part = 0; part < P; ++part) pload<Fmt, Sh>(f[0], sn, 0, lane, aR, bR, o, part);
+                }
+                APS_PIN();
+            }
+        }
+    }
+}
+
+// acc += A x B over KT stages of the three-stage ring.  Stage kt lives in
+// slot kt % 3; stages 0..2 are copied up front, stage kt + 2 during stage kt
+// (1 <= kt <= KT - 3).
+template <class Sh, class Fmt>
+__device__ inline void pmainloop(Ring3& ring, const Slots& sl, int KT, int wave, int lane, int aR, int bR,
+                                 f32x16_t (&acc)[Sh::MI][Sh::NJ]) {
+    typedef PDims<Sh> D;
+    constexpr int P = Fmt::kParts, NS = D::NS;
+    pissue<Sh>(ring.s[0], sl, 0, wave, 0, NS);
+    if (KT > 1) pissue<Sh>(ring.s[1], sl, 1, wave, 0, NS);
+    if (KT > 2) pissue<Sh>(ring.s[2], sl, 2, wave, 0, NS);
+    if (KT > 2) wait_vm_lgkm0<2 * NS>();
+    else if (KT > 1) wait_vm_lgkm0<NS>();
+    else wait_vm_lgkm0<0>();
+    raw_barrier();
+    PFrags<Fmt, Sh> f[2];
+#pragma unroll
+    for (int o = 0; o < D::NR; ++o)
+#pragma unroll
+        for (int part = 0; part < P; ++part) pload<Fmt, Sh>(f[0], ring.s[0], 0, lane, aR, bR, o, part);
+    APS_PIN();
+    if (KT == 1) {
+        pstage<Sh, Fmt, false, false, false>(ring, sl, 0, wave, lane, aR, bR, f, acc);
+        return;
+    }
+    if (KT > 2) pstage<Sh, Fmt, false, true, true>(ring, sl, 0, wave, lane, aR, bR, f, acc);
+    else pstage<Sh, Fmt, false, true, false>(ring, sl, 0, wave, lane, aR, bR, f, acc);
+    for (int kt = 1; kt + 2 < KT; ++kt) pstage<Sh, Fmt, true, true, true>(ring, sl, kt, wave, lane, aR, bR, f, acc);
+    if (KT > 2) pstage<Sh, Fmt, false, true, false>(ring, sl, KT - 2, wave, lane, aR, bR, f, acc);
+    pstage<Sh, Fmt, false, false, false>(ring, sl, KT - 1, wave, lane, aR, bR, f, acc);
+}
+
 // ---------------------------------------------------------------------------
 // act[p][n] = silu(g) * u with, t = assignment_rows[p],
 //   bf16: g = x[t] . w1[e][n], u = x[t] . w3[e][n]             (fp32 accumulate)
 //   fp8 : g = (xq[t] . w1q[e][n]) * sx[t] * s1[e][n], u likewise with w3
 //         (codes multiplied exactly, fp32 accumulate, then the two scales)
-// act is stored as bf16.
-template <bool TALL, class Fmt>
-__device__ inline void ffn_up_block(Ring3& ring, const uint8_t* __restrict__ x, int64_t x_row_bytes,
-                                    const uint32_t* __restrict__ assignment_rows,
-                                    const uint8_t* __restrict__ w13, bf16_t* __restrict__ act, int H, int F,
-                                    const float* __restrict__ sx, const float* __restrict__ s1,
-                                    const float* __restrict__ s3, const Tile& u) {
+// act is stored as bf16.  One piece of shape Sh (see PShape).
+template <class Sh, class Fmt>
+__device__ inline void up_piece(Ring3& ring, const uint8_t* __restrict__ x, int64_t x_row_bytes,
+                                const uint32_t* __restrict__ assignment_rows, const uint8_t* __restrict__ w13,
+                                bf16_t* __restrict__ act, int H, int F, const float* __restrict__ sx,
+                                const float* __restrict__ s1, const float* __restrict__ s3, const Piece& u) {
+    typedef PDims<Sh> D;
     constexpr bool kFp8 = Fmt::kElt == 1;
+    constexpr int MI = Sh::MI, NJ = Sh::NJ;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % Sh::WM, wn = wave / Sh::WM;
     const int KT = H * Fmt::kElt / kRowBytes;
     const int nblk = F / 64;
-    // A: gathered token rows; positions past the expert's end reuse its last
-    // row (a valid address; those rows are never stored).
+    // A slots: gathered token rows; positions past the expert's end reuse its
+    // last row (a valid address; those rows are never stored).  B slots: 8
+    // rows of a packed tile image, copied verbatim (the images are stored
+    // pre-swizzled and every 32-row fragment group maps to 32 consecutive
+    // image rows, so a stage row and its image row share their swizzle).
     Slots sl;
     const int64_t block_bytes = static_cast<int64_t>(KT) * kImageBytes;
     const uint8_t* image0 = w13 + static_cast<int64_t>(u.expert) * nblk * block_bytes;
 #pragma unroll
-    for (int s = 0; s < 12; ++s) {
-        if (s < Shape<TALL>::NA) {
+    for (int s = 0; s < D::NS; ++s) {
+        if (s < D::NA) {
             const int row = slot_row(s, wave, lane);
             uint32_t p = u.m0 + row;
             p = p < u.end ? p : u.end - 1;
             sl.p[s] = x + static_cast<int64_t>(assignment_rows[p]) * x_row_bytes + slot_chunk(row, lane) * 16;
         } else {
-            sl.p[s] = b_slot<TALL>(image0, block_bytes, u.nb0, s, wave, lane);
+            const int rb = 32 * (s - D::NA) + 8 * wave;   // first B row of the slot
+            int cb, ir;
+            if (NJ == 4) {
+                cb = u.cb0 + rb / 128;
+                ir = rb % 128;
+            } else {
+                const int g = rb / 64, r = rb % 64, h = Sh::WN == 2 ? g : u.half;
+                cb = u.cb0;
+                ir = r < 32 ? 32 * h + r : 64 + 32 * h + (r - 32);
+            }
+            sl.p[s] = image0 + static_cast<int64_t>(cb) * block_bytes + ir * kRowBytes + lane * 16;
         }
     }
-    const int aR = wave_a_row<TALL>(wave), bR = wave_b_row<TALL>(wave);
-    f32x16_t acc[2][4];
-    zero_acc(acc);
-    mainloop_il<TALL, Fmt>(ring, sl, KT, wave, lane, aR, bR, acc);
+    const int aR = wm * MI * 32, bR = D::RA + wn * NJ * 32;
+    f32x16_t acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    pmainloop<Sh, Fmt>(ring, sl, KT, wave, lane, aR, bR, acc);
 
-    // Epilogue: scales (fp8), SwiGLU in registers (B fragments 0,1 are gate
-    // columns 0..63 of the wave's column block, 2,3 the same up columns), the
-    // bf16 act tile staged in the idle ring, then written as 16-byte row
-    // chunks.
-    constexpr int kCols = TALL ? 64 : 128;   // act columns of the block tile
-    constexpr int kPitch = kCols + 8;        // elements; 16-byte aligned rows, banks staggered
+    // Epilogue: scales (fp8), SwiGLU in registers (gate fragment j pairs with
+    // up fragment j + NJ/2), the bf16 act tile staged in the idle ring, then
+    // written as 16-byte row chunks.
+    constexpr int kPitch = D::kCols + 8;      // elements; 16-byte aligned rows, banks staggered
     bf16_t* stage = reinterpret_cast<bf16_t*>(ring.s[0]);
     raw_barrier();
-    const int cbase = TALL ? 0 : (wave >> 1) * 64;
-    const int c0 = u.expert * F + u.nb0 * 64 + cbase;   // this wave's first gate/up column in s1 / s3
+    const int hc = NJ == 4 ? 0 : (Sh::WN == 2 ? wn : u.half);  // column-block half (NJ = 2)
+    const int gcol0 = (u.cb0 + (NJ == 4 ? wn : 0)) * 64 + (NJ == 4 ? 0 : 32 * hc);  // wave's first act column
+    const int lcol0 = NJ == 4 ? wn * 64 : (Sh::WN == 2 ? wn * 32 : 0);             // ... within the piece
+    const int c0 = u.expert * F + gcol0;      // its gate/up scale index (fp8)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < MI; ++i) {
         const int row = aR + i * 32 + (lane & 31);
         float rs = 1.0f;
         if constexpr (kFp8) {
@@ -615,21 +707,21 @@ __device__ inline void ffn_up_block(Ring3& ring, const uint8_t* __restrict__ x, 
             rs = sx[assignment_rows[p]];
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ / 2; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 float g[4], up[4];
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     g[v] = acc[i][j][4 * q + v];
-                    up[v] = acc[i][j + 2][4 * q + v];
+                    up[v] = acc[i][j + NJ / 2][4 * q + v];
                 }
                 if constexpr (kFp8) {
                     const float4 a1 = col_scales(s1, c0, j, q, lane), a3 = col_scales(s3, c0, j, q, lane);
                     g[0] = g[0] * rs * a1.x; g[1] = g[1] * rs * a1.y; g[2] = g[2] * rs * a1.z; g[3] = g[3] * rs * a1.w;
                     up[0] = up[0] * rs * a3.x; up[1] = up[1] * rs * a3.y; up[2] = up[2] * rs * a3.z; up[3] = up[3] * rs * a3.w;
                 }
-                const int col = cbase + 32 * j + 8 * q + 4 * (lane >> 5);
+                const int col = lcol0 + 32 * j + 8 * q + 4 * (lane >> 5);
                 const u32x2_t v = {pack2_bf16(swiglu(g[0], up[0]), swiglu(g[1], up[1])),
                                    pack2_bf16(swiglu(g[2], up[2]), swiglu(g[3], up[3]))};
                 *reinterpret_cast<u32x2_t*>(stage + row * kPitch + col) = v;
@@ -637,15 +729,147 @@ __device__ inline void ffn_up_block(Ring3& ring, const uint8_t* __restrict__ x, 
     }
     wait_vm_lgkm0<0>();
     raw_barrier();
-    constexpr int kChunks = kCols / 8;       // 16-byte chunks per row
+    constexpr int kChunks = D::kCols / 8;     // 16-byte chunks per row
+    const int acol = u.cb0 * 64 + (Sh::WN == 1 && NJ == 2 ? 32 * u.half : 0);  // piece's first act column
 #pragma unroll
-    for (int c = 0; c < Shape<TALL>::RA * kChunks / 256; ++c) {
+    for (int c = 0; c < D::RA * kChunks / 256; ++c) {
         const int id = tid + 256 * c;
         const int r = id / kChunks, cc = id % kChunks;
         const uint32_t p = u.m0 + r;
         if (p < u.end)
-            *reinterpret_cast<u32x4_t*>(act + static_cast<int64_t>(p) * F + u.nb0 * 64 + cc * 8) =
+            *reinterpret_cast<u32x4_t*>(act + static_cast<int64_t>(p) * F + acol + cc * 8) =
                 *reinterpret_cast<const u32x4_t*>(stage + r * kPitch + cc * 8);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-expert tile scheduler of the w1||w3 GEMM (the reference's work list,
+// src/tensor.cu:1337-1374, with its grid sized by max_tall, :2846-2853),
+// computed on the device from offsets[] by every block, identically.
+//   Base list, expert by expert: each 256-row group of an expert's positions
+// contributes the wide pieces W of its 128-row tiles (tile major) and, when
+// the column-block count is odd, one piece for the last column block: T for
+// the whole group, S when the group has at most 128 rows (the old tall
+// block's empty half is never loaded).  Pieces sharing token rows or weights
+// are adjacent in the list.
+//   The grid is G persistent blocks (about one per CU, a multiple of the XCD
+// count); workgroup b runs on XCD b % 8, as block l = b / 8 of its GX = G / 8.
+// XCD x takes the contiguous slice [x * per, x * per + n) of the list (per =
+// ceil(t / 8)), so blocks sharing token rows and weights share an L2, and
+// deals it to its blocks in R = n / GX full rounds: round i gives block l
+// the piece x * per + i * GX + l.  The r = n % GX pieces of the last round
+// are split into s = 4, 2 or 1 pieces each (W -> 4 Q or 2 S, T -> 4 Q or
+// 2 S by rows, S -> 2 Q), the largest s with r * s <= GX, and dealt the same
+// way, siblings on adjacent blocks: a list just over one round then costs
+// one W plus one Q per block instead of two rounds, and a small batch
+// spreads over the whole chip.  Skewed experts simply own more of the list.
+// Every block leaves after its at most R + 1 pieces.
+struct UpSched {
+    int E, nblk, pairs, odd, GX, l, first, R, r, s;
+    uint32_t lo, hi;   // this lane's expert (lane = expert id): position range
+    int r128, incl;    // its 128-row tiles; inclusive prefix count of base pieces
+};
+
+__device__ inline void up_sched(const uint32_t* __restrict__ offsets, int E, int nblk, UpSched& sc) {
+    const int lane = threadIdx.x & 63;
+    sc.E = E;
+    sc.nblk = nblk;
+    sc.pairs = nblk / 2;
+    sc.odd = nblk & 1;
+    sc.lo = lane < E ? offsets[lane] : 0u;
+    sc.hi = __shfl_down(sc.lo, 1);
+    if (lane == E - 1) sc.hi = offsets[E];
+    const uint32_t cnt = lane < E ? sc.hi - sc.lo : 0u;
+    sc.r128 = static_cast<int>((cnt + 127) / 128);
+    int incl = sc.pairs * sc.r128 + sc.odd * static_cast<int>((cnt + 255) / 256);
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d);
+        if (lane >= d) incl += v;
+    }
+    sc.incl = incl;
+    const int t = __shfl(incl, 63);
+    sc.GX = static_cast<int>(gridDim.x) / kXcds;
+    const int b = static_cast<int>(blockIdx.x), x = b % kXcds;
+    sc.l = b / kXcds;
+    const int per = (t + kXcds - 1) / kXcds;
+    sc.first = x * per;
+    const int last = sc.first + per < t ? sc.first + per : t;
+    const int n = last > sc.first ? last - sc.first : 0;
+    sc.R = n / sc.GX;
+    sc.r = n - sc.R * sc.GX;
+    sc.s = 4 * sc.r <= sc.GX ? 4 : (2 * sc.r <= sc.GX ? 2 : 1);
+}
+
+// Base piece t of the list (t < total).
+__device__ inline Piece up_base(const UpSched& sc, int t) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t m = __ballot(lane < sc.E && sc.incl > t);
+    const int e = __ffsll(static_cast<unsigned long long>(m)) - 1;
+    const int before = __shfl(sc.incl, e > 0 ? e - 1 : 0);
+    const int i = t - (e > 0 ? before : 0);          // piece index within expert e
+    const int e_r128 = __shfl(sc.r128, e);
+    const int gsz = 2 * sc.pairs + sc.odd;           // pieces of a full 256-row group
+    const int g = i / gsz, r = i - g * gsz;
+    const int nw = e_r128 - 2 * g < 2 ? e_r128 - 2 * g : 2;  // 128-row tiles in group g
+    Piece u;
+    u.expert = e;
+    u.end = __shfl(sc.hi, e);
+    u.half = 0;
+    const uint32_t e_lo = __shfl(sc.lo, e);
+    if (r < sc.pairs * nw) {
+        u.kind = kPieceW;
+        u.m0 = e_lo + static_cast<uint32_t>(2 * g + r / sc.pairs) * 128u;
+        u.cb0 = 2 * (r % sc.pairs);
+    } else {
+        u.kind = nw == 2 ? kPieceT : kPieceS;
+        u.m0 = e_lo + static_cast<uint32_t>(g) * 256u;
+        u.cb0 = sc.nblk - 1;
+    }
+    return u;
+}
+
+// Tail piece p of this XCD (p < r * s): sub-piece p % s of the slice's base
+// piece R * GX + p / s.
+__device__ inline bool up_tail(const UpSched& sc, int p, Piece& u) {
+    const int sub = p % sc.s;
+    u = up_base(sc, sc.first + sc.R * sc.GX + p / sc.s);
+    if (sc.s == 1) return true;
+    if (u.kind == kPieceW) {
+        if (sc.s == 2) {
+            u.kind = kPieceS;
+            u.cb0 += sub;
+        } else {
+            u.kind = kPieceQ;
+            u.cb0 += sub >> 1;
+            u.half = sub & 1;
+        }
+    } else if (u.kind == kPieceT) {
+        if (sc.s == 2) {
+            u.kind = kPieceS;
+            u.m0 += 128u * sub;
+        } else {
+            u.kind = kPieceQ;
+            u.m0 += 128u * (sub >> 1);
+            u.half = sub & 1;
+        }
+    } else {  // S: its two halves
+        if (sub >= 2) return false;
+        u.kind = kPieceQ;
+        u.half = sub;
+    }
+    return u.m0 < u.end;
+}
+
+template <class Fmt>
+__device__ inline void run_up_piece(Ring3& ring, const uint8_t* x, int64_t x_row_bytes, const uint32_t* arows,
+                                    const uint8_t* w13, bf16_t* act, int H, int F, const float* sx,
+                                    const float* s1, const float* s3, const Piece& u) {
+    switch (u.kind) {
+        case kPieceW: up_piece<PShape<kPieceW>, Fmt>(ring, x, x_row_bytes, arows, w13, act, H, F, sx, s1, s3, u); break;
+        case kPieceT: up_piece<PShape<kPieceT>, Fmt>(ring, x, x_row_bytes, arows, w13, act, H, F, sx, s1, s3, u); break;
+        case kPieceS: up_piece<PShape<kPieceS>, Fmt>(ring, x, x_row_bytes, arows, w13, act, H, F, sx, s1, s3, u); break;
+        default: up_piece<PShape<kPieceQ>, Fmt>(ring, x, x_row_bytes, arows, w13, act, H, F, sx, s1, s3, u); break;
     }
 }
 
@@ -656,10 +880,22 @@ k_ffn_up(const uint8_t* __restrict__ x, int64_t x_row_bytes, const uint32_t* __r
          int H, int F, int E, const float* __restrict__ sx, const float* __restrict__ s1,
          const float* __restrict__ s3) {
     __shared__ __align__(16) Ring3 ring;
-    Tile u;
-    if (!locate_block<false>(offsets, E, F / 64, u)) return;
-    if (u.tall) ffn_up_block<true, Fmt>(ring, x, x_row_bytes, assignment_rows, w13, act, H, F, sx, s1, s3, u);
-    else ffn_up_block<false, Fmt>(ring, x, x_row_bytes, assignment_rows, w13, act, H, F, sx, s1, s3, u);
+    UpSched sc;
+    up_sched(offsets, E, F / 64, sc);
+    // one call site, so that each piece shape is instantiated once
+    for (int i = 0; i <= sc.R; ++i) {
+        Piece u;
+        if (i < sc.R) u = up_base(sc, sc.first + i * sc.GX + sc.l);
+        else if (!(sc.l < sc.r * sc.s && up_tail(sc, sc.l, u))) break;
+        u.kind = __builtin_amdgcn_readfirstlane(u.kind);
+        u.expert = __builtin_amdgcn_readfirstlane(u.expert);
+        u.cb0 = __builtin_amdgcn_readfirstlane(u.cb0);
+        u.half = __builtin_amdgcn_readfirstlane(u.half);
+        u.m0 = __builtin_amdgcn_readfirstlane(u.m0);
+        u.end = __builtin_amdgcn_readfirstlane(u.end);
+        if (i > 0) raw_barrier();  // the previous piece has read its staged tile out of the ring
+        run_up_piece<Fmt>(ring, x, x_row_bytes, assignment_rows, w13, act, H, F, sx, s1, s3, u);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1110,6 +1346,13 @@ int64_t max_blocks(int64_t rows, int nblk, int experts, bool all_tall) {
 
 dim3 grid_of(int64_t blocks) { return dim3(static_cast<unsigned>(ceil_div(blocks, kXcds) * kXcds)); }
 
+// Persistent grid of the w1||w3 GEMM: one block per CU (a multiple of the
+// XCD count); the kernel deals its pieces to them.
+dim3 grid_up() {
+    const int g = num_cus() / kXcds * kXcds;
+    return dim3(static_cast<unsigned>(g > 0 ? g : kXcds));
+}
+
 }  // namespace
 
 // Compute units of the current device (cached per device).
@@ -1131,7 +1374,7 @@ hipError_t launch_ffn_up_bf16(const bf16_t* x, const uint32_t* offsets,
                               hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (hidden % 64 != 0 || ffn % 64 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_ffn_up<Bf16Fmt>, grid_of(max_blocks(rows, ffn / 64, experts, false)), dim3(256), 0, s,
+    hipLaunchKernelGGL(k_ffn_up<Bf16Fmt>, grid_up(), dim3(256), 0, s,
                        reinterpret_cast<const uint8_t*>(x), static_cast<int64_t>(hidden) * 2, offsets,
                        assignment_rows, reinterpret_cast<const uint8_t*>(w13), act, hidden, ffn, experts,
                        nullptr, nullptr, nullptr);
@@ -1162,7 +1405,7 @@ hipError_t launch_ffn_up_fp8(const uint8_t* xq, const float* x_scale, const uint
                              int experts, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (hidden % 128 != 0 || ffn % 64 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_ffn_up<Fp8Fmt>, grid_of(max_blocks(rows, ffn / 64, experts, false)), dim3(256), 0, s,
+    hipLaunchKernelGGL(k_ffn_up<Fp8Fmt>, grid_up(), dim3(256), 0, s,
                        xq, static_cast<int64_t>(hidden), offsets, assignment_rows, w13, act, hidden, ffn, experts,
                        x_scale, w1_scale, w3_scale);
     return hipGetLastError();
