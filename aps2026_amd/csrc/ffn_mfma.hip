@@ -163,6 +163,10 @@ struct Bf16Fmt {
     __device__ static void mma_pinned(f32x16_t& c, const frag_t& b, const frag_t& a) {
         asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(b), "a"(a));
     }
+    // the first k step of a tile: c = b x a + 0 (no zeroed accumulators)
+    __device__ static void mma_pinned_first(f32x16_t& c, const frag_t& b, const frag_t& a) {
+        asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(b), "a"(a));
+    }
 };
 
 struct Fp8Fmt {
@@ -190,8 +194,17 @@ struct Fp8Fmt {
     __device__ static f32x16_t mma(const frag_t& a, const frag_t& b, f32x16_t c) {
         return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
     }
-    static constexpr bool kPinned = false;   // 128 act registers: the allocator copes
-    __device__ static void mma_pinned(f32x16_t& c, const frag_t& b, const frag_t& a) { c = mma(b, a, c); }
+    // The register-resident w2 kernel pins its operands as for bf16:
+    // accumulators in VGPRs, the resident act fragments in AGPRs, so that
+    // the epilogue reads the accumulators without v_accvgpr_read (128 VALU
+    // moves per column block, which add to the MFMA time on a SIMD).
+    static constexpr bool kPinned = true;
+    __device__ static void mma_pinned(f32x16_t& c, const frag_t& b, const frag_t& a) {
+        asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+v"(c) : "v"(b), "a"(a));
+    }
+    __device__ static void mma_pinned_first(f32x16_t& c, const frag_t& b, const frag_t& a) {
+        asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=&v"(c) : "v"(b), "a"(a));
+    }
 };
 
 // ---------------------------------------------------------------------------
@@ -1232,9 +1245,7 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
     for (int ui = 0; ui < nunits; ++ui) {
         const int nb = u.nb0 + ui;
         const int g0 = ui * KT;
-        f32x16_t acc[2][4];
-        zero_acc(acc);
-        if constexpr (Fmt::kPinned) asm volatile("s_nop 4");  // VALU write -> MFMA srcC (hidden in asm)
+        f32x16_t acc[2][4];   // written from zero by the column block's first MFMAs
         const __amdgpu_buffer_rsrc_t prev = ui > 0 ? ys : ynull;  // unit 0 stores nothing, same count
         load_b(bf[0], g0, 0);
         load_b(bf[1], g0, 1);
@@ -1261,7 +1272,10 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) Fmt::mma_pinned(acc[i][j], bf[q % 3][j], areg[kt][i][s]);
+                        for (int j = 0; j < 4; ++j) {
+                            if (q == 0) Fmt::mma_pinned_first(acc[i][j], bf[q % 3][j], areg[kt][i][s]);
+                            else Fmt::mma_pinned(acc[i][j], bf[q % 3][j], areg[kt][i][s]);
+                        }
                     APS_PIN();
                     if (st) {
                         // the previous column block's y chunks 4kt .. 4kt+3
