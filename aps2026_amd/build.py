@@ -2,7 +2,9 @@
   libaps_moe.so     all HIP sources under csrc/ (gfx950): the C ABI;
   libaps_layers.so  the C++ host API (cpp/*.cpp: Tensor, tensor_ops,
                     PhiMLP, PhiMoE) over libaps_moe.so;
-  tests/cpp/layer_check  the GPU check program of the C++ API.
+  tests/cpp/layer_check  the GPU check program of the C++ API;
+  tests/cpp/libmodel_drive.so  a C ABI over PhiTinyMoEModel for the tests
+                    and bench.py --host cpp.
 
     python -m aps2026_amd.build
 
@@ -49,6 +51,9 @@ LAYERS_LIB = os.path.join(HERE, "libaps_layers.so")
 REPO = os.path.dirname(HERE)
 CHECK_SRC = os.path.join(REPO, "tests", "cpp", "layer_check.cpp")
 CHECK_BIN = os.path.join(REPO, "tests", "cpp", "layer_check")
+# C ABI driver of the C++ model for the tests and bench.py --host cpp
+DRIVE_SRC = os.path.join(REPO, "tests", "cpp", "model_drive.cpp")
+DRIVE_LIB = os.path.join(REPO, "tests", "cpp", "libmodel_drive.so")
 
 # host-only C++ (HIP runtime API, no device code): the system C++ compiler
 CXX = os.environ.get("CXX", "g++")
@@ -106,6 +111,11 @@ def build(verbose: bool = False) -> str:
         _run([CXX, *HOST_FLAGS, "-o", tmp, CHECK_SRC, "-L" + HERE, "-laps_layers", "-laps_moe",
               "-Wl,-rpath,$ORIGIN/../../aps2026_amd", *HIP_LINK], verbose)
         os.replace(tmp, CHECK_BIN)
+    if os.path.exists(DRIVE_SRC):
+        tmp = DRIVE_LIB + ".tmp"
+        _run([CXX, *HOST_FLAGS, "-shared", "-o", tmp, DRIVE_SRC, "-L" + HERE, "-laps_layers", "-laps_moe",
+              "-Wl,-rpath,$ORIGIN/../../aps2026_amd", *HIP_LINK], verbose)
+        os.replace(tmp, DRIVE_LIB)
     return LIB
 
 

@@ -80,6 +80,9 @@ def parse():
                          "or the reference's optional split-bf16 tensor-core Linear: tc = three products (USE_TC; "
                          "at c4 the LM head and layer 31 as the reference selects), tc_all = four products on every "
                          "layer (USE_TC_ALL)")
+    ap.add_argument("--host", default="py", choices=["py", "cpp"],
+                    help="c4: drive the prefill through the Python mirror (aps2026_amd/decoder.py) or the C++ "
+                         "drop-in PhiTinyMoEModel::generate (include/model.h, through tests/cpp/libmodel_drive.so)")
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "skip"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline: repeat full-batch runs until this much time is spent (at least 2 runs)")
@@ -168,6 +171,101 @@ def load_bench(args):
     }), flush=True)
 
 
+def cpp_c4_bench(args):
+    """--config c4 --host cpp: the same prefill through the C++ drop-in
+    (PhiTinyMoEModel::generate, as the reference harness calls it,
+    src/main.cpp:585-594): a 32-layer model built from parts (random-init
+    weights of the same distributions, fp32 tensors copied into the C++
+    Tensors, bf16 experts registered by PhiMoE), each step one generate() on
+    C4's 16 prompts (host trie and upload included)."""
+    import torch
+    from aps2026_amd import capi, synth
+
+    if args.proj != "fp32":
+        raise SystemExit("--host cpp runs the default build's fp32 projections")
+    dev = torch.device("cuda:0")
+    H, F, E, V, nl = 4096, 448, 16, 32064, 32
+    drive_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "cpp", "libmodel_drive.so")
+    if not os.path.exists(drive_path):
+        raise SystemExit(f"{drive_path} is not built (python -m aps2026_amd.build)")
+    D = ctypes.CDLL(drive_path)
+    D.md_model_create.restype = ctypes.c_void_p
+    D.md_model_create.argtypes = [ctypes.c_int] * 8 + [ctypes.POINTER(ctypes.c_char_p),
+                                                       ctypes.POINTER(ctypes.c_void_p), ctypes.c_int]
+    D.md_generate.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                              ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_double)]
+    D.md_model_free.argtypes = [ctypes.c_void_p]
+    D.md_last_error.restype = ctypes.c_char_p
+    g = torch.Generator(device=dev).manual_seed(11)
+    rn = lambda *shape, s=0.02: (s * torch.randn(shape, generator=g, device=dev)).contiguous()
+    W = {"model.embed_tokens.weight": rn(V, H, s=1.0), "model.norm.weight": torch.ones(H, device=dev),
+         "model.norm.bias": torch.zeros(H, device=dev), "lm_head.weight": rn(V, H), "lm_head.bias": rn(V)}
+    model = None
+    for i in range(nl):
+        p = f"model.layers.{i}."
+        for nm in ("input_layernorm", "post_attention_layernorm"):
+            W[p + nm + ".weight"] = torch.ones(H, device=dev)
+            W[p + nm + ".bias"] = torch.zeros(H, device=dev)
+        for nm, (o, k) in (("q_proj", (2048, H)), ("k_proj", (512, H)), ("v_proj", (512, H)), ("o_proj", (H, 2048))):
+            W[p + f"self_attn.{nm}.weight"] = rn(o, k)
+            W[p + f"self_attn.{nm}.bias"] = rn(o)
+        m = p + "block_sparse_moe."
+        W[m + "gate.weight"] = rn(E, H)
+        for e in range(E):
+            for nm, shp in (("w1", (F, H)), ("w3", (F, H)), ("w2", (H, F))):
+                W[m + f"experts.{e}.{nm}.weight"] = rn(*shp)
+    names = list(W.keys())
+    torch.cuda.synchronize()
+    model = D.md_model_create(nl, H, V, E, F, 2048, 512, len(names),
+                              (ctypes.c_char_p * len(names))(*[n.encode() for n in names]),
+                              (ctypes.c_void_p * len(names))(*[W[n].data_ptr() for n in names]), capi.DTYPE_BF16)
+    if not model:
+        raise RuntimeError(D.md_last_error().decode())
+    del W  # the C++ model holds its own copies
+    torch.cuda.empty_cache()
+    prompts = synth.c4_prompts()
+    tokens = sum(len(q) for q in prompts)
+    ids = (ctypes.c_int * tokens)(*[t for q in prompts for t in q])
+    lens = (ctypes.c_int * len(prompts))(*[len(q) for q in prompts])
+    logits = torch.empty((len(prompts), V), dtype=torch.float32, device=dev)
+    secs = ctypes.c_double(0.0)
+
+    def step(i):
+        if D.md_generate(model, ids, lens, len(prompts), ctypes.c_void_p(logits.data_ptr()), ctypes.byref(secs)):
+            raise RuntimeError(D.md_last_error().decode())
+    t_settle = time.perf_counter()
+    n_settle = 0
+    while time.perf_counter() - t_settle < args.settle:
+        step(n_settle)
+        n_settle += 1
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    per = []
+    for i in range(args.steps):
+        step(i)
+        per.append(secs.value)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    line = {
+        "metric": "whole-model prefill tokens/s", "value": tokens * args.steps / elapsed, "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "settle_steps": n_settle,
+        "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 attention, bf16 experts",
+        "data": "synthetic (seeded torch normals, random-init weights)",
+        "config": {"workload": ("c4 through the C++ drop-in: PhiTinyMoEModel::generate (host trie, embedding "
+                                "gather, 32 x PhiDecoderLayer::forward_carry, final LayerNorm, last rows, LM head) "
+                                f"on 16 prompts x 1024 ids, hidden {H}, {E} bf16 experts of {F}, vocab {V}; "
+                                f"value counts the {tokens} prompt tokens"),
+                   "host": "cpp", "tokens": tokens, "hidden": H, "experts": E, "ffn": F, "layers": nl},
+        "roofline": None, "cpu_baseline": None,
+        "stages": {"generate_ms_median": statistics.median(per) * 1e3, "generate_ms_min": min(per) * 1e3},
+    }
+    print(json.dumps(line), flush=True)
+    D.md_model_free(model)
+
+
 def decoder_bench(args):
     """--config c3: one whole decoder layer (input LayerNorm, fp32 q/k/v
     projections with bias, RoPE, GQA-4 tree attention, o projection, residual
@@ -190,6 +288,8 @@ def decoder_bench(args):
     stream = torch.cuda.current_stream(dev)
     sptr = ctypes.c_void_p(stream.cuda_stream)
     L = capi.lib()
+    if c4 and args.host == "cpp":
+        return cpp_c4_bench(args)
     if c4:
         prompts = synth.c4_prompts()
         nl = 32

@@ -26,6 +26,7 @@ import torch
 import oracle
 from aps2026_amd import decoder, synth
 from tests import model_chain
+from tests.device_weights import random_model_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -185,32 +186,6 @@ def test_decoder_layer_split_bf16_projections(gpu_device):
     lw.release()
 
 
-def _c4_model_weights(device, H=4096, F=448, E=16, V=32064, layers=32, seed=5):
-    """Random-init model weights drawn on the device (name -> tensor): linear
-    and expert weights, projection and LM-head biases ~N(0, 0.02), LayerNorm
-    weight 1 and bias 0, embeddings ~N(0, 1)."""
-    g = torch.Generator(device=device).manual_seed(seed)
-    rn = lambda *shape, s=0.02: (s * torch.randn(shape, generator=g, device=device)).contiguous()
-    W = {"model.embed_tokens.weight": rn(V, H, s=1.0), "model.norm.weight": torch.ones(H, device=device),
-         "model.norm.bias": torch.zeros(H, device=device), "lm_head.weight": rn(V, H), "lm_head.bias": rn(V)}
-    for i in range(layers):
-        p = f"model.layers.{i}."
-        for nm in ("input_layernorm", "post_attention_layernorm"):
-            W[p + nm + ".weight"] = torch.ones(H, device=device)
-            W[p + nm + ".bias"] = torch.zeros(H, device=device)
-        for nm, (o, k) in (("q_proj", (2048, H)), ("k_proj", (512, H)), ("v_proj", (512, H)),
-                           ("o_proj", (H, 2048))):
-            W[p + f"self_attn.{nm}.weight"] = rn(o, k)
-            W[p + f"self_attn.{nm}.bias"] = rn(o)
-        m = p + "block_sparse_moe."
-        W[m + "gate.weight"] = rn(E, H)
-        for e in range(E):
-            W[m + f"experts.{e}.w1.weight"] = rn(F, H)
-            W[m + f"experts.{e}.w3.weight"] = rn(F, H)
-            W[m + f"experts.{e}.w2.weight"] = rn(H, F)
-    return W
-
-
 def _model(W, layers, moe_dtype):
     lws = [decoder.layer_from_tensors(W, i, moe_dtype=moe_dtype) for i in range(layers)]
     return decoder.Model(W["model.embed_tokens.weight"], W["model.norm.weight"], W["model.norm.bias"],
@@ -224,7 +199,7 @@ def test_c4_whole_model_dedup_and_routing_agreement(gpu_device):
     layers = 32
     prompts = synth.c4_prompts()
     note(f"C4 whole model: {layers} layers, 16 prompts x 1024 (4 groups sharing 512)")
-    W = _c4_model_weights(gpu_device, layers=layers)
+    W = random_model_weights(gpu_device, layers=layers)
     model16, lw16 = _model(W, layers, torch.bfloat16)
     trie = decoder.RowPlan.from_prompts(prompts, gpu_device)
     full = decoder.RowPlan.packed(prompts, gpu_device)
@@ -265,7 +240,7 @@ def test_model_split_bf16_projections_and_lm_head(gpu_device):
     layers, V = 2, 1000
     prompts = [list(range(1, 40)), list(range(1, 25)) + [7, 8, 9], [500, 3, 2]]
     note("model with split-bf16 projections and LM head (four products): 2 layers, vocab 1000")
-    W = _c4_model_weights(gpu_device, V=V, layers=layers, seed=8)
+    W = random_model_weights(gpu_device, V=V, layers=layers, seed=8)
     lws = [decoder.layer_from_tensors(W, i, moe_dtype=torch.bfloat16) for i in range(layers)]
     args = (W["model.embed_tokens.weight"], W["model.norm.weight"], W["model.norm.bias"], W["lm_head.weight"],
             W["lm_head.bias"], lws)
