@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <deque>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -549,23 +550,42 @@ namespace {
 // Per-row segment start and position of a packed batch, on the device,
 // cached per seq_lens (the reference's packed_meta keeps the last one; this
 // keeps a few, since a prefill alternates between the same two or three).
+// Entries are shared: a caller holds its entry until its launches are
+// queued, so evicting it from the cache (another thread, a ninth seq_lens)
+// never frees arrays a launch is about to use; the last holder frees them
+// after the device has finished its queued work.
 struct PackedSegments {
     std::vector<std::size_t> lens;
     std::size_t rows = 0, max_seq = 0;
     int dev = 0;
     std::uint32_t* offset = nullptr;  // [rows]
     std::uint32_t* pos = nullptr;     // [rows]
+    PackedSegments() = default;
+    PackedSegments(const PackedSegments&) = delete;
+    PackedSegments& operator=(const PackedSegments&) = delete;
+    ~PackedSegments() {
+        if (!offset && !pos) return;
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        if (cur != dev) (void)hipSetDevice(dev);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(offset);
+        (void)hipFree(pos);
+        if (cur != dev) (void)hipSetDevice(cur);
+    }
 };
 std::mutex g_seg_mu;
-std::deque<PackedSegments> g_segs;  // push_back keeps references to the others valid
+// never destroyed: its entries call into HIP, which may be gone at exit
+std::deque<std::shared_ptr<const PackedSegments>>& g_segs = *new std::deque<std::shared_ptr<const PackedSegments>>();
 
-const PackedSegments& packed_segments(const std::vector<std::size_t>& seq_lens) {
+std::shared_ptr<const PackedSegments> packed_segments(const std::vector<std::size_t>& seq_lens) {
     int dev = 0;
     hip_check(hipGetDevice(&dev), "hipGetDevice");
     std::lock_guard<std::mutex> lock(g_seg_mu);
-    for (const PackedSegments& s : g_segs)
-        if (s.dev == dev && s.lens == seq_lens) return s;
-    PackedSegments s;
+    for (const auto& e : g_segs)
+        if (e->dev == dev && e->lens == seq_lens) return e;
+    auto entry = std::make_shared<PackedSegments>();
+    PackedSegments& s = *entry;
     s.lens = seq_lens;
     s.dev = dev;
     std::vector<std::uint32_t> off, pos;
@@ -586,14 +606,9 @@ const PackedSegments& packed_segments(const std::vector<std::size_t>& seq_lens) 
         hip_check(hipMemcpy(s.pos, pos.data(), s.rows * sizeof(std::uint32_t), hipMemcpyHostToDevice),
                   "copy segment positions");
     }
-    if (g_segs.size() == 8) {  // keep the cache small; the legacy stream orders the frees after queued use
-        hip_check(hipDeviceSynchronize(), "segment cache");
-        (void)hipFree(g_segs.front().offset);
-        (void)hipFree(g_segs.front().pos);
-        g_segs.pop_front();
-    }
-    g_segs.push_back(std::move(s));
-    return g_segs.back();
+    if (g_segs.size() == 8) g_segs.pop_front();  // keep the cache small; holders keep their entry alive
+    g_segs.push_back(entry);
+    return entry;
 }
 
 }  // namespace
@@ -605,11 +620,11 @@ void apply_rope_gpu(Tensor& q, Tensor& k, const std::vector<std::size_t>& seq_le
     const std::size_t rows = head_dim && q_heads ? q.size() / (q_heads * head_dim) : 0;
     if (q.size() != rows * q_heads * head_dim || k.size() != rows * kv_heads * head_dim || head_dim % 2 != 0)
         throw std::invalid_argument("apply_rope_gpu shape");
-    const PackedSegments& seg = packed_segments(seq_lens);
-    if (seg.rows != rows) throw std::invalid_argument("packed sequence lengths");
+    const auto seg = packed_segments(seq_lens);
+    if (seg->rows != rows) throw std::invalid_argument("packed sequence lengths");
     if (rows == 0) return;
     // positions restart per sequence, so the longest sequence bounds the table
-    apply_rope_tree_gpu(q, k, seg.pos, rows, seg.max_seq, q_heads, kv_heads, head_dim, theta);
+    apply_rope_tree_gpu(q, k, seg->pos, rows, seg->max_seq, q_heads, kv_heads, head_dim, theta);
 }
 
 void attention_gpu(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out,
@@ -620,11 +635,11 @@ void attention_gpu(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& ou
     if (q.size() != rows * q_heads * head_dim || k.size() != rows * kv_heads * head_dim || v.size() != k.size() ||
         out.size() != q.size())
         throw std::invalid_argument("attention_gpu shape");
-    const PackedSegments& seg = packed_segments(seq_lens);
-    if (seg.rows != rows) throw std::invalid_argument("packed sequence lengths");
+    const auto seg = packed_segments(seq_lens);
+    if (seg->rows != rows) throw std::invalid_argument("packed sequence lengths");
     if (rows == 0) return;
     const int rc = aps_attention_packed(q.cuda_data(), k.cuda_data(), v.cuda_data(), out.cuda_data_write(),
-                                        seg.offset, seg.pos, static_cast<int64_t>(seg.max_seq),
+                                        seg->offset, seg->pos, static_cast<int64_t>(seg->max_seq),
                                         static_cast<int64_t>(rows), static_cast<int32_t>(q_heads),
                                         static_cast<int32_t>(kv_heads), static_cast<int32_t>(head_dim),
                                         static_cast<int32_t>(apss26::SLIDING_WINDOW), nullptr);

@@ -904,7 +904,7 @@ int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float
 // share the array and race.
 namespace {
 
-constexpr size_t kStaticScratchBytes = size_t(64) << 20;  // 64 MiB per device
+constexpr size_t kStaticScratchBytes = size_t(96) << 20;  // 96 MiB per device
 static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 
 constexpr int kMaxDevices = 64;

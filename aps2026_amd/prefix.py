@@ -75,16 +75,19 @@ def node_parents_and_runs(plan: PrefixPlan):
     return parent, run_start
 
 
-def ancestors_gpu(plan: PrefixPlan, device, stream=None):
+def ancestors_gpu(plan: PrefixPlan, device):
     """The ancestor table [nodes][max_len] (int32 view of uint32) built on
-    the device from the plan's parents and runs, equal to the host table."""
+    the device from the plan's parents and runs, equal to the host table.
+    It runs on torch's current stream of `device`, the stream the input
+    uploads are ordered on and the one whose caching allocator takes them
+    back on return."""
     parent, run_start = node_parents_and_runs(plan)
     n, stride = plan.nodes, max(plan.max_len, 1)
     to_dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(device)
     p_d, d_d, r_d = to_dev(parent), to_dev(plan.node_depth), to_dev(run_start)
     anc = torch.empty((n, stride), dtype=torch.int32, device=device)
     _call(capi.lib().aps_prefix_ancestors(_ptr(p_d), _ptr(d_d), _ptr(r_d), n, stride, _ptr(anc),
-                                          _stream(anc.device) if stream is None else stream))
+                                          _stream(anc.device)))
     return anc
 
 

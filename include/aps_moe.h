@@ -242,12 +242,12 @@ APS_API int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, con
 
 /* aps_moe_forward without a workspace argument: the intermediate arrays
  * live in a static device array of aps_moe_noalloc_scratch_bytes() bytes
- * (64 MiB, one copy per device, held until the process ends), so the call
+ * (96 MiB, one copy per device, held until the process ends), so the call
  * allocates nothing -- for callers that cannot allocate: code under HIP
  * graph capture, serving loops, harnesses that forbid it.  No counterpart
  * in the reference.  Rows whose aps_moe_workspace_layout total exceeds the
- * scratch are refused with APS_ERR_WORKSPACE (about 3,500 tokens at hidden
- * 4096, ffn 448, bf16).  Calls that overlap on one device share the scratch
+ * scratch are refused with APS_ERR_WORKSPACE (up to about 5,500 tokens fit
+ * at hidden 4096, ffn 448, bf16: 18.3 KB per token, y and act).  Calls that overlap on one device share the scratch
  * and race: serialise them (one stream, or events). */
 APS_API int aps_moe_forward_noalloc(uint64_t handle, const void* x, int32_t x_dtype, const float* gate,
                                     int64_t rows, void* out, int32_t out_dtype, void* stream);
@@ -414,7 +414,11 @@ APS_API int aps_rope_tree(float* q, float* k, const uint32_t* row_pos, int64_t r
  * [rows][kv_heads][128], out [rows][q_heads][128], fp32; q_heads = 4 kv_heads
  * ("attention_tree_gpu expects GQA-4"); head_dim 128; k 16-byte aligned.
  * Ancestor entries must be < rows and positions < anc_stride (the kernel
- * clamps them, for memory safety only). */
+ * clamps them, for memory safety only).  v must be finite: four rows on one
+ * ancestor chain are computed together over the union of their windows,
+ * and a key outside one row's window enters that row's value products with
+ * weight 0, which leaves the result unchanged for a finite value (0 * inf
+ * would not); the reference model's activations are finite. */
 APS_API int aps_attention_tree(const float* q, const float* k, const float* v, float* out, const uint32_t* row_pos,
                                const uint32_t* anc, int64_t anc_stride, int64_t rows, int32_t q_heads,
                                int32_t kv_heads, int32_t head_dim, int32_t window, void* stream);
@@ -422,7 +426,8 @@ APS_API int aps_attention_tree(const float* q, const float* k, const float* v, f
 /* Replaces tensor_ops::attention_gpu's GQA-4 path (reference include/tensor.h:
  * 95-98, src/tensor.cu:3318-3340, kernel k_attention_grouped_gqa4
  * :2267-2405): the same attention and arithmetic as aps_attention_tree, over
- * packed token sequences instead of trie nodes -- row r of a segment that
+ * packed token sequences instead of trie nodes (and with its precondition
+ * on v: finite values) -- row r of a segment that
  * starts at row seg_offset[r] sits at position seg_pos[r] in it, and its
  * keys are rows seg_offset[r] + begin .. seg_offset[r] + seg_pos[r] (begin =
  * max(0, pos + 1 - window)).  max_seq bounds every segment length (the

@@ -174,6 +174,44 @@ def test_attention_packed_long_sequences_bit_exact(gpu_device, window):
     np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("window", [2047, 5])
+def test_attention_excluded_keys_take_no_part(gpu_device, window):
+    """Precondition of the path-group kernel: value rows are finite.  A key
+    inside a four-row group's span but outside one row's window (a later row
+    of the group, causally, or a key past the sliding window) enters that
+    row's value MFMAs with p = 0, which leaves its chains unchanged for every
+    finite value; the reference's row kernel never reads such keys.  Value
+    rows of +-1e30 at every other position (excluded for the earlier rows of
+    each group, and for the later ones at window 5) must leave every output
+    bit for bit equal to the oracle's, which reads only in-window keys."""
+    from aps2026_amd import capi
+    from aps2026_amd.moe import _ptr, _stream
+    note(f"attention: large finite values in excluded keys, window={window}")
+    lens = [300, 77, 8]
+    rows, stride = sum(lens), max(lens)
+    off = np.repeat(np.cumsum([0] + lens[:-1]), lens).astype(np.uint32)
+    pos = np.concatenate([np.arange(n) for n in lens]).astype(np.uint32)
+    anc = np.zeros((rows, stride), np.uint32)
+    for r in range(rows):
+        anc[r, :pos[r] + 1] = off[r] + np.arange(pos[r] + 1)
+    rng = np.random.default_rng(100 + window)
+    q = rng.standard_normal((rows, 16 * 128)).astype(np.float32)
+    k = rng.standard_normal((rows, 4 * 128)).astype(np.float32)
+    v = rng.standard_normal((rows, 4 * 128)).astype(np.float32)
+    v[1::2] = np.where(rng.random((v[1::2].shape)) < 0.5, -1e30, 1e30).astype(np.float32)
+    qd, kd, vd = dev(q, gpu_device), dev(k, gpu_device), dev(v, gpu_device)
+    out = torch.empty((rows, 16 * 128), dtype=torch.float32, device=gpu_device)
+    od, pd = dev(off.view(np.int32), gpu_device), dev(pos.view(np.int32), gpu_device)
+    rc = capi.lib().aps_attention_packed(_ptr(qd), _ptr(kd), _ptr(vd), _ptr(out), _ptr(od), _ptr(pd), stride, rows,
+                                         16, 4, 128, window, _stream(qd.device))
+    assert rc == 0, capi.last_error()
+    torch.cuda.synchronize()
+    want = oracle.attention_tree(q, k, v, pos, anc, stride, 16, 4, 128, window)
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all() and np.isfinite(want).all()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_attention_nodes_equal_token_rows(gpu_device):
     note("attention tree nodes vs token rows")
     batch = shared_batch(4, groups=2, per=4, pre=60, suf=20)

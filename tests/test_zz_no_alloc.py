@@ -38,7 +38,7 @@ def _x(inp, dev):
     return torch.from_numpy(inp.x).to(dev)
 
 
-@pytest.mark.parametrize("dtype,sizes", [("bf16", (2048, 300)), ("f32", (512, 77))])
+@pytest.mark.parametrize("dtype,sizes", [("bf16", (4096, 300)), ("f32", (512, 77))])
 def test_forward_noalloc_equals_workspace_forward(gpu_device, dtype, sizes):
     L = capi.lib()
     T0 = sizes[0]
