@@ -4,7 +4,9 @@
                     PhiMLP, PhiMoE) over libaps_moe.so;
   tests/cpp/layer_check  the GPU check program of the C++ API;
   tests/cpp/libmodel_drive.so  a C ABI over PhiTinyMoEModel for the tests
-                    and bench.py --host cpp.
+                    and bench.py --host cpp;
+  probe/libaps_probe.so  bench.py's measurement of the fp32 FMA chain cost
+                    (probe/fma_chain.hip), not part of the library.
 
     python -m aps2026_amd.build
 
@@ -55,6 +57,10 @@ CHECK_BIN = os.path.join(REPO, "tests", "cpp", "layer_check")
 DRIVE_SRC = os.path.join(REPO, "tests", "cpp", "model_drive.cpp")
 DRIVE_LIB = os.path.join(REPO, "tests", "cpp", "libmodel_drive.so")
 
+# bench.py's FMA-chain probe (a separate library: not part of the C ABI)
+PROBE_SRC = os.path.join(HERE, "probe", "fma_chain.hip")
+PROBE_LIB = os.path.join(HERE, "probe", "libaps_probe.so")
+
 # host-only C++ (HIP runtime API, no device code): the system C++ compiler
 CXX = os.environ.get("CXX", "g++")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
@@ -100,6 +106,9 @@ def build_hip(out: str = LIB, defines=(), verbose: bool = False, jobs: int = 0) 
 
 def build(verbose: bool = False) -> str:
     build_hip(LIB, verbose=verbose)
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC, *FLAGS, "-o", tmp, PROBE_SRC], verbose)
+    os.replace(tmp, PROBE_LIB)
     # C++ host API over the C ABI
     tmp = LAYERS_LIB + ".tmp"
     cpp = sorted(glob.glob(os.path.join(HERE, "cpp", "*.cpp")))

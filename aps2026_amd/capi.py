@@ -51,7 +51,8 @@ class WeightsDesc(ctypes.Structure):
 class WsLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in (
         "total_bytes", "logits", "routes", "tile_counts", "counts", "offsets",
-        "assignment_rows", "route_positions", "act", "act_scale", "y", "xq", "xq_scale", "actq")]
+        "assignment_rows", "route_positions", "act", "act_scale", "y", "xq", "xq_scale", "actq",
+        "tile_counts0", "slot1", "slot_rows", "slot_tokens")]
 
 
 class ApsError(RuntimeError):

@@ -114,6 +114,12 @@ void make_layout(const WeightSet& w, int64_t rows, aps_moe_ws_layout* L) {
     L->actq = 0;
     L->xq = 0;
     L->xq_scale = 0;
+    // the fused forward's folded combine: the slot-0 histogram and the
+    // dispatch's slot-ordered lists
+    L->tile_counts0 = take(static_cast<size_t>(aps::ceil_div(rows, aps::kTileTokens)) * E * 4);
+    L->slot1 = take(E * 4);
+    L->slot_rows = take(2 * T * 4);
+    L->slot_tokens = take(2 * T * 4);
     if (w.compute == APS_DTYPE_BF16) {
         // bf16 copy of x for the fused entry points when x arrives as fp32:
         // written by the router, last read by the w1||w3 GEMM, so it shares
@@ -188,9 +194,15 @@ int check_x_dtype(const WeightSet& w, int32_t x_dtype) {
 
 // Routing (from `logits`; nullptr when the router kernel already wrote the
 // routes and tile histogram into the workspace), dispatch, FFN and combine.
+// The fp8 path with bf16 output folds the combine into the w2 GEMM when the
+// router wrote the slot-0 histogram (aps_moe_forward): no y round trip.
+bool fold_combine(const WeightSet& w, int64_t rows, int32_t out_dtype) {
+    return w.compute == APS_DTYPE_E4M3 && out_dtype == APS_DTYPE_BF16 && aps::ffn_down_fold_fits(rows, w.H, w.F);
+}
+
 int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const float* logits, int64_t rows,
                         void* out, int32_t out_dtype, char* ws, const aps_moe_ws_layout& L,
-                        hipStream_t s) {
+                        hipStream_t s, bool fold = false) {
     auto* routes = reinterpret_cast<uint8_t*>(ws + L.routes);
     auto* tiles = reinterpret_cast<uint32_t*>(ws + L.tile_counts);
     auto* counts = reinterpret_cast<uint32_t*>(ws + L.counts);
@@ -203,8 +215,17 @@ int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const 
         x = xb;
     }
     if (logits) APS_HIP(aps::launch_route_top2(logits, rows, w.E, routes, tiles, s), "route_top2 launch");
-    APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, w.E, counts, offsets, arows, rpos, nullptr, s),
-            "dispatch launch");
+    auto* tiles0 = reinterpret_cast<uint32_t*>(ws + L.tile_counts0);
+    auto* slot1 = reinterpret_cast<uint32_t*>(ws + L.slot1);
+    auto* srows = reinterpret_cast<uint32_t*>(ws + L.slot_rows);
+    auto* stoks = reinterpret_cast<uint32_t*>(ws + L.slot_tokens);
+    if (fold)
+        APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, w.E, counts, offsets, arows, rpos, nullptr, s,
+                                             tiles0, slot1, srows, stoks),
+                "dispatch launch");
+    else
+        APS_HIP(aps::launch_dispatch_scatter(routes, tiles, rows, w.E, counts, offsets, arows, rpos, nullptr, s),
+                "dispatch launch");
     if (w.compute == APS_DTYPE_E4M3) {
         auto* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
         auto* xs = reinterpret_cast<float*>(ws + L.xq_scale);
@@ -217,6 +238,15 @@ int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const 
         APS_HIP(aps::launch_ffn_up_fp8(xq, xs, offsets, arows, w.q13, w.s1, w.s3, act, rows, w.H, w.F, w.E, s),
                 "ffn_up_fp8 launch");
         APS_HIP(aps::launch_quant_rows_e4m3(act, w.F, w.F, actq, kp, as, 2 * rows, s), "quantise act launch");
+        if (fold) {
+            // slot-0 rows to y's bytes as [rows][H] by token, then slot-1 rows
+            // combined with them straight into out
+            APS_HIP(aps::launch_ffn_down_fold_fp8(actq, as, offsets, slot1, srows, stoks, w.q2, w.s2,
+                                                  reinterpret_cast<aps::bf16_t*>(ws + L.y),
+                                                  static_cast<aps::bf16_t*>(out), rows, w.H, w.F, w.E, s),
+                    "ffn_down_fold_fp8 launch");
+            return APS_OK;
+        }
         APS_HIP(aps::launch_ffn_down_fp8(actq, as, offsets, w.q2, w.s2, reinterpret_cast<aps::bf16_t*>(ws + L.y),
                                          rows, w.H, w.F, w.E, s),
                 "ffn_down_fp8 launch");
@@ -357,7 +387,7 @@ int aps_router_logits(const void* x, int32_t x_dtype, const float* gate, int64_t
         return fail(APS_ERR_DTYPE, "router x dtype %d not supported", x_dtype);
     if (rows > 0 && (!x || !gate || !logits)) return fail(APS_ERR_ARG, "router: NULL pointer");
     APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, hidden, num_experts, logits, nullptr,
-                               nullptr, nullptr, static_cast<hipStream_t>(stream)),
+                               nullptr, nullptr, nullptr, static_cast<hipStream_t>(stream)),
             "router_logits launch");
     return APS_OK;
 }
@@ -886,10 +916,13 @@ int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float
     auto* tiles = reinterpret_cast<uint32_t*>(ws + L.tile_counts);
     const bool copy = x_dtype == APS_DTYPE_F32 && w->compute == APS_DTYPE_BF16;
     auto* xb = copy ? reinterpret_cast<aps::bf16_t*>(ws + L.xq) : nullptr;
-    APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, w->H, w->E, logits, routes, tiles, xb, s),
+    const bool fold = fold_combine(*w, rows, out_dtype);
+    auto* tiles0 = fold ? reinterpret_cast<uint32_t*>(ws + L.tile_counts0) : nullptr;
+    APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, w->H, w->E, logits, routes, tiles, tiles0,
+                               xb, s),
             "router launch");
-    if (copy) return grouped_from_logits(*w, xb, false, nullptr, rows, out, out_dtype, ws, L, s);
-    return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, nullptr, rows, out, out_dtype, ws, L, s);
+    if (copy) return grouped_from_logits(*w, xb, false, nullptr, rows, out, out_dtype, ws, L, s, fold);
+    return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, nullptr, rows, out, out_dtype, ws, L, s, fold);
 }
 
 // ---- allocation-free forward --------------------------------------------

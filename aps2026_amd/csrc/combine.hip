@@ -2,11 +2,12 @@
 // registration.
 //
 // Reference: k_moe_combine (src/tensor.cu:1968-1988) computes
-// out[t][d] = 0 + 0.5*y[p_lo][d] + 0.5*y[p_hi][d].  0.5*v is exact in binary
-// floating point, so the sum rounds once and its order cannot change a bit:
-// RN(0.5a + 0.5b) is what every order gives.  Here one thread moves 8
-// consecutive elements of one token (16-byte bf16 or 2x16-byte f32 loads),
-// so every wave reads and writes whole 128-byte lines.
+// out[t][d] = (0 + 0.5*y[p_lo][d]) + 0.5*y[p_hi][d].  0.5*v is exact in
+// binary floating point, so the sum rounds once and the order of the two
+// terms cannot change a bit; the leading 0 matters only for signed zeros
+// (0 + -0 = +0, so two -0 terms give +0) and is kept (moe_combine2).  Here one
+// thread moves 8 consecutive elements of one token (16-byte bf16 or
+// 2x16-byte f32 loads), so every wave reads and writes whole 128-byte lines.
 #include "common.hpp"
 
 namespace aps {
@@ -60,7 +61,7 @@ k_combine(const void* __restrict__ y, const uint32_t* __restrict__ route_positio
     load8<YBF16>(y, static_cast<int64_t>(p0) * H + c, a);
     load8<YBF16>(y, static_cast<int64_t>(p1) * H + c, b);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) o[k] = __fadd_rn(__fmul_rn(0.5f, a[k]), __fmul_rn(0.5f, b[k]));
+    for (int k = 0; k < 8; ++k) o[k] = moe_combine2(a[k], b[k]);
     if (OBF16) {
         uint4 q;
         q.x = pack2_bf16(o[0], o[1]);

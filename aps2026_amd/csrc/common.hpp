@@ -67,6 +67,14 @@ __device__ inline uint32_t tile_quarter_counts(int first, int second, int e) {
 }
 __host__ __device__ inline uint32_t tile_word_total(uint32_t w) { return (w * 0x01010101u) >> 24; }
 
+// The reference's combine of a token's two expert outputs (k_moe_combine,
+// src/tensor.cu:1968-1988): value = 0, then value += 0.5 a, value += 0.5 b,
+// each step rounded.  0.5 v is exact, so the order of a and b changes no
+// bit; the leading 0 turns a -0 first term into +0 (two -0 terms give +0).
+__device__ inline float moe_combine2(float a, float b) {
+    return __fadd_rn(__fadd_rn(0.0f, __fmul_rn(0.5f, a)), __fmul_rn(0.5f, b));
+}
+
 // Caller-supplied routes (aps_moe_dispatch) are made memory-safe before they
 // are counted or ranked: an expert id >= E is clamped to E - 1 (and reported
 // by the caller-visible counter), a token whose two slots name the same
@@ -129,12 +137,13 @@ __device__ inline RowTile wave_find_tile(int tile, int bm, uint32_t lo, uint32_t
 // ---- launchers (defined in the .hip files) --------------------------------
 
 // Router GEMM; with routes != nullptr also the top-2 routes and the tile
-// histogram (tile_counts), in the same kernel; with x_copy != nullptr (fp32
+// histogram (tile_counts), in the same kernel, and with tile_counts0 !=
+// nullptr the histogram of slot-0 routes alone; with x_copy != nullptr (fp32
 // x only) also the bf16 copy of x [rows][hidden].
 int num_cus();  // compute units of the current device
 hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t rows, int hidden,
                          int experts, float* logits, uint8_t* routes, uint32_t* tile_counts,
-                         bf16_t* x_copy, hipStream_t s);
+                         uint32_t* tile_counts0, bf16_t* x_copy, hipStream_t s);
 hipError_t launch_route_top2(const float* logits, int64_t rows, int experts, uint8_t* routes,
                              uint32_t* tile_counts, hipStream_t s);
 // status (may be null): one u32 that counts the route ids >= experts the
@@ -206,10 +215,15 @@ hipError_t launch_linear_f32(const float* x, const float* w, const float* bias, 
 
 hipError_t launch_layer_norm(float* x, const float* residual, const float* weight, const float* bias, float* y,
                              int64_t rows, int hidden, float eps, hipStream_t s);
+// With tile_counts0 (the slot-0 histogram) also the slot-ordered lists:
+// slot1[e] = offsets[e] + (slot-0 routes of e); slot_rows / slot_tokens
+// [2 rows] = position / token of list entry i (see dispatch.hip).
 hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_counts,
                                    int64_t rows, int experts, uint32_t* counts,
                                    uint32_t* offsets, uint32_t* assignment_rows,
-                                   uint32_t* route_positions, uint32_t* status, hipStream_t s);
+                                   uint32_t* route_positions, uint32_t* status, hipStream_t s,
+                                   const uint32_t* tile_counts0 = nullptr, uint32_t* slot1 = nullptr,
+                                   uint32_t* slot_rows = nullptr, uint32_t* slot_tokens = nullptr);
 
 // bf16 MFMA path.  w13 / w2 are packed tile images (see launch_pack_*):
 // w13 [E][F/64][H/64][128][64], w2 [E][H/128][F/64][128][64]; act/y bf16.
@@ -233,6 +247,15 @@ hipError_t launch_ffn_up_fp8(const uint8_t* xq, const float* x_scale, const uint
 hipError_t launch_ffn_down_fp8(const uint8_t* actq, const float* act_scale, const uint32_t* offsets,
                                const uint8_t* w2, const float* w2_scale, bf16_t* y, int64_t rows, int hidden,
                                int ffn, int experts, hipStream_t s);
+// The fp8 w2 GEMM with the combine folded in (two launches over the
+// dispatch's slot-ordered lists): slot-0 rows to ya [rows][hidden] bf16 by
+// token, then slot-1 rows combined with them into out [rows][hidden] bf16.
+// ffn_down_fold_fits: the shapes it serves.
+bool ffn_down_fold_fits(int64_t rows, int hidden, int ffn);
+hipError_t launch_ffn_down_fold_fp8(const uint8_t* actq, const float* act_scale, const uint32_t* offsets,
+                                    const uint32_t* slot1, const uint32_t* slot_rows, const uint32_t* slot_tokens,
+                                    const uint8_t* w2, const float* w2_scale, bf16_t* ya, bf16_t* out,
+                                    int64_t rows, int hidden, int ffn, int experts, hipStream_t s);
 // Per-row e4m3 quantisation of bf16 rows (n values, row strides in
 // elements / bytes; codes zero-padded to dst_stride).
 hipError_t launch_quant_rows_e4m3(const bf16_t* src, int64_t src_stride, int n, uint8_t* dst, int64_t dst_stride,

@@ -16,6 +16,13 @@
 //      lane its stable rank inside the tile.
 // Every (token, slot) is written exactly once, by the wave that owns the
 // token, so the scatter is O(T) work instead of the reference's O(E*T).
+//
+// SLOTS (the fused forward's folded combine): a second histogram counts the
+// slot-0 routes alone, and the scatter also writes each expert's positions
+// reordered by slot: list entries [offsets[e], slot1[e]) are the positions
+// of the tokens whose first route is e, [slot1[e], offsets[e+1]) those whose
+// second route is e, each in ascending token order (slot_rows = position,
+// slot_tokens = token).  The positions themselves are the reference's.
 #include "common.hpp"
 
 namespace aps {
@@ -52,11 +59,14 @@ k_tile_hist(const uint8_t* __restrict__ routes, int64_t rows, int E,
     if (tile < ntiles && lane < E) tile_counts[tile * E + lane] = mine;
 }
 
+template <bool SLOTS>
 __global__ void __launch_bounds__(256)
 k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restrict__ tile_counts,
                    int64_t rows, int E, uint32_t* __restrict__ counts,
                    uint32_t* __restrict__ offsets, uint32_t* __restrict__ assignment_rows,
-                   uint32_t* __restrict__ route_positions, uint32_t* __restrict__ status) {
+                   uint32_t* __restrict__ route_positions, uint32_t* __restrict__ status,
+                   const uint32_t* __restrict__ tile_counts0, uint32_t* __restrict__ slot1,
+                   uint32_t* __restrict__ slot_rows, uint32_t* __restrict__ slot_tokens) {
     const int lane = threadIdx.x & 63;
     const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     const int64_t ntiles = (rows + kWave - 1) / kWave;
@@ -77,54 +87,73 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
     //    (Each wave reading the whole histogram, one narrow load per tile,
     //    was the kernel's main cost.)
     __shared__ uint32_t part[4][5][kMaxExperts];
+    __shared__ uint32_t part0[SLOTS ? 4 : 1][5][kMaxExperts];   // slot-0 totals and prefixes
     const int wave = threadIdx.x >> 6;
     const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * 4;  // the workgroup's first tile
     const int tpl = 64 % E == 0 ? 64 / E : 1;
     const int ex = lane % E;  // this lane's expert in the histogram loads
     const bool active = lane < tpl * E;
-    uint32_t tot = 0, bef0 = 0, bef1 = 0, bef2 = 0, bef3 = 0;
+    // [0]: all routes, [1]: slot-0 routes (SLOTS)
+    uint32_t tot[2] = {0, 0}, bef0[2] = {0, 0}, bef1[2] = {0, 0}, bef2[2] = {0, 0}, bef3[2] = {0, 0};
     // eight loads in flight per batch: unconditional (index clamped), used
     // only where the tile exists
     for (int64_t j0 = static_cast<int64_t>(wave) * tpl; j0 < ntiles; j0 += 32 * tpl) {
-        uint32_t c[8];
+        uint32_t c[2][8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int64_t j = j0 + 4 * tpl * i + lane / E;
-            c[i] = tile_counts[(j < ntiles ? j : ntiles - 1) * E + ex];
+            const int64_t at = (j < ntiles ? j : ntiles - 1) * E + ex;
+            c[0][i] = tile_counts[at];
+            if constexpr (SLOTS) c[1][i] = tile_counts0[at];
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int64_t j = j0 + 4 * tpl * i + lane / E;
-            const uint32_t n = active && j < ntiles ? tile_word_total(c[i]) : 0u;
-            tot += n;
-            bef0 += j < tile0 ? n : 0u;
-            bef1 += j < tile0 + 1 ? n : 0u;
-            bef2 += j < tile0 + 2 ? n : 0u;
-            bef3 += j < tile0 + 3 ? n : 0u;
+        for (int h = 0; h < (SLOTS ? 2 : 1); ++h)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int64_t j = j0 + 4 * tpl * i + lane / E;
+                const uint32_t n = active && j < ntiles ? tile_word_total(c[h][i]) : 0u;
+                tot[h] += n;
+                bef0[h] += j < tile0 ? n : 0u;
+                bef1[h] += j < tile0 + 1 ? n : 0u;
+                bef2[h] += j < tile0 + 2 ? n : 0u;
+                bef3[h] += j < tile0 + 3 ? n : 0u;
+            }
+    }
+#pragma unroll
+    for (int h = 0; h < (SLOTS ? 2 : 1); ++h)
+        for (int d = E; d < 64 && tpl > 1; d <<= 1) {  // lanes e, e + E, e + 2E, ...
+            tot[h] += __shfl_xor(tot[h], d);
+            bef0[h] += __shfl_xor(bef0[h], d);
+            bef1[h] += __shfl_xor(bef1[h], d);
+            bef2[h] += __shfl_xor(bef2[h], d);
+            bef3[h] += __shfl_xor(bef3[h], d);
         }
-    }
-    for (int d = E; d < 64 && tpl > 1; d <<= 1) {  // lanes e, e + E, e + 2E, ...
-        tot += __shfl_xor(tot, d);
-        bef0 += __shfl_xor(bef0, d);
-        bef1 += __shfl_xor(bef1, d);
-        bef2 += __shfl_xor(bef2, d);
-        bef3 += __shfl_xor(bef3, d);
-    }
     if (lane < E) {
-        part[wave][0][lane] = tot;
-        part[wave][1][lane] = bef0;
-        part[wave][2][lane] = bef1;
-        part[wave][3][lane] = bef2;
-        part[wave][4][lane] = bef3;
+        part[wave][0][lane] = tot[0];
+        part[wave][1][lane] = bef0[0];
+        part[wave][2][lane] = bef1[0];
+        part[wave][3][lane] = bef2[0];
+        part[wave][4][lane] = bef3[0];
+        if constexpr (SLOTS) {
+            part0[wave][0][lane] = tot[1];
+            part0[wave][1][lane] = bef0[1];
+            part0[wave][2][lane] = bef1[1];
+            part0[wave][3][lane] = bef2[1];
+            part0[wave][4][lane] = bef3[1];
+        }
     }
     __syncthreads();
     if (tile >= ntiles) return;  // wave-uniform, after the workgroup's barrier
-    uint32_t total = 0, before = 0;
+    uint32_t total = 0, before = 0, total0 = 0, before0 = 0;
     if (lane < E) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             total += part[w][0][lane];
             before += part[w][1 + wave][lane];
+            if constexpr (SLOTS) {
+                total0 += part0[w][0][lane];
+                before0 += part0[w][1 + wave][lane];
+            }
         }
     }
     // 2. exclusive scan of totals over lanes 0..E-1
@@ -140,7 +169,12 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
         counts[lane] = total;
         offsets[lane] = excl;
         if (lane == E - 1) offsets[E] = incl;
+        if constexpr (SLOTS) slot1[lane] = excl + total0;
     }
+    // SLOTS: list index of this tile's first slot-0 / slot-1 route of each
+    // expert (lane e)
+    const uint32_t lbase0 = excl + before0;
+    const uint32_t lbase1 = excl + total0 + (before - before0);
 
     // 3. stable rank of each lane's (token, slot) pairs inside this tile, per
     //    expert: the pairs of lower lanes come first, slot 0 before slot 1
@@ -152,7 +186,7 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
         if (status && bad) atomicAdd(status, static_cast<uint32_t>(bad));
     }
     const uint64_t below = (1ull << lane) - 1ull;
-    uint32_t p0 = 0, p1 = 0;
+    uint32_t p0 = 0, p1 = 0, i0 = 0, i1 = 0;
     for (int e = 0; e < E; ++e) {
         const uint64_t m0 = __ballot(first == e), m1 = __ballot(second == e);
         if ((m0 | m1) == 0) continue;  // wave-uniform
@@ -160,12 +194,29 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
         const uint32_t r = static_cast<uint32_t>(__popcll(m0 & below) + __popcll(m1 & below));
         if (first == e) p0 = b + r;
         if (second == e) p1 = b + r + (first == e ? 1u : 0u);
+        if constexpr (SLOTS) {
+            const uint32_t l0 = __shfl(lbase0, e), l1 = __shfl(lbase1, e);
+            if (first == e) i0 = l0 + static_cast<uint32_t>(__popcll(m0 & below));
+            if (second == e) i1 = l1 + static_cast<uint32_t>(__popcll(m1 & below));
+        }
     }
     if (t < rows) {
         assignment_rows[p0] = static_cast<uint32_t>(t);
         assignment_rows[p1] = static_cast<uint32_t>(t);
         route_positions[2 * t] = p0;
         route_positions[2 * t + 1] = p1;
+        if constexpr (SLOTS) {
+            // in range whenever the slot-0 histogram matches the routes
+            const uint32_t A = static_cast<uint32_t>(2 * rows);
+            if (i0 < A) {
+                slot_rows[i0] = p0;
+                slot_tokens[i0] = static_cast<uint32_t>(t);
+            }
+            if (i1 < A) {
+                slot_rows[i1] = p1;
+                slot_tokens[i1] = static_cast<uint32_t>(t);
+            }
+        }
     }
 }
 
@@ -203,18 +254,29 @@ hipError_t launch_tile_hist(const uint8_t* routes, int64_t rows, int experts,
 hipError_t launch_dispatch_scatter(const uint8_t* routes, const uint32_t* tile_counts,
                                    int64_t rows, int experts, uint32_t* counts,
                                    uint32_t* offsets, uint32_t* assignment_rows,
-                                   uint32_t* route_positions, uint32_t* status, hipStream_t s) {
+                                   uint32_t* route_positions, uint32_t* status, hipStream_t s,
+                                   const uint32_t* tile_counts0, uint32_t* slot1, uint32_t* slot_rows,
+                                   uint32_t* slot_tokens) {
     if (experts <= 0 || experts > kMaxExperts) return hipErrorInvalidValue;
+    const bool slots = tile_counts0 != nullptr;
+    if (slots && (!slot1 || !slot_rows || !slot_tokens)) return hipErrorInvalidValue;
     if (rows <= 0) {
         // empty batch: counts and offsets are all zero
         hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(128), 0, s, counts, experts);
         hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(128), 0, s, offsets, experts + 1);
+        if (slots) hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(128), 0, s, slot1, experts);
         return hipGetLastError();
     }
     const int64_t ntiles = ceil_div(rows, kWave);
-    hipLaunchKernelGGL(k_dispatch_scatter, dim3(static_cast<unsigned>(ceil_div(ntiles, 4))),
-                       dim3(256), 0, s, routes, tile_counts, rows, experts, counts, offsets,
-                       assignment_rows, route_positions, status);
+    const dim3 grid(static_cast<unsigned>(ceil_div(ntiles, 4)));
+    if (slots)
+        hipLaunchKernelGGL(k_dispatch_scatter<true>, grid, dim3(256), 0, s, routes, tile_counts, rows, experts,
+                           counts, offsets, assignment_rows, route_positions, status, tile_counts0, slot1,
+                           slot_rows, slot_tokens);
+    else
+        hipLaunchKernelGGL(k_dispatch_scatter<false>, grid, dim3(256), 0, s, routes, tile_counts, rows, experts,
+                           counts, offsets, assignment_rows, route_positions, status, nullptr, nullptr,
+                           nullptr, nullptr);
     return hipGetLastError();
 }
 

@@ -160,12 +160,19 @@ struct Bf16Fmt {
     // plus 128 accumulators overflow the VGPR file and every step shuffles
     // operands between the two files.
     static constexpr bool kPinned = true;
+    // NOP: three wait states in the same statement first, for a VALU write
+    // of an operand register that the compiler may place right before it
+    // (the hazard recognizer does not look into inline asm; 2 are needed)
+    template <bool NOP = false>
     __device__ static void mma_pinned(f32x16_t& c, const frag_t& b, const frag_t& a) {
-        asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(b), "a"(a));
+        if constexpr (NOP) asm("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(b), "a"(a));
+        else asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(b), "a"(a));
     }
     // the first k step of a tile: c = b x a + 0 (no zeroed accumulators)
+    template <bool NOP = false>
     __device__ static void mma_pinned_first(f32x16_t& c, const frag_t& b, const frag_t& a) {
-        asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(b), "a"(a));
+        if constexpr (NOP) asm("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(b), "a"(a));
+        else asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(b), "a"(a));
     }
 };
 
@@ -199,11 +206,15 @@ struct Fp8Fmt {
     // the epilogue reads the accumulators without v_accvgpr_read (128 VALU
     // moves per column block, which add to the MFMA time on a SIMD).
     static constexpr bool kPinned = true;
+    template <bool NOP = false>
     __device__ static void mma_pinned(f32x16_t& c, const frag_t& b, const frag_t& a) {
-        asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+v"(c) : "v"(b), "a"(a));
+        if constexpr (NOP) asm("s_nop 2\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+v"(c) : "v"(b), "a"(a));
+        else asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+v"(c) : "v"(b), "a"(a));
     }
+    template <bool NOP = false>
     __device__ static void mma_pinned_first(f32x16_t& c, const frag_t& b, const frag_t& a) {
-        asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=&v"(c) : "v"(b), "a"(a));
+        if constexpr (NOP) asm("s_nop 2\n\tv_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=&v"(c) : "v"(b), "a"(a));
+        else asm("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=&v"(c) : "v"(b), "a"(a));
     }
 };
 
@@ -1041,11 +1052,18 @@ struct ArWork {
     uint32_t m0, end;
 };
 
-__device__ inline bool locate_ar(const uint32_t* __restrict__ offsets, int E, int NB, ArWork& u) {
+// Rows [lo, hi) of expert e in the list the kernel walks: positions of the
+// routing plan (FOLD 0), or the dispatch's slot-ordered list, slot-0 rows
+// (FOLD 1) or slot-1 rows (FOLD 2).
+template <int FOLD>
+__device__ inline bool locate_ar(const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ slot1, int E,
+                                 int NB, ArWork& u) {
     const int lane = threadIdx.x & 63;
-    const uint32_t lo = lane < E ? offsets[lane] : 0u;
-    uint32_t hi = __shfl_down(lo, 1);
-    if (lane == E - 1) hi = offsets[E];
+    uint32_t lo = 0u, hi = 0u;
+    if (lane < E) {
+        lo = FOLD == 2 ? slot1[lane] : offsets[lane];
+        hi = FOLD == 1 ? slot1[lane] : offsets[lane + 1];
+    }
     const uint32_t cnt = lane < E ? hi - lo : 0u;
     const int r256 = static_cast<int>((cnt + kArRows - 1) / kArRows);
     int tiles = r256;
@@ -1090,6 +1108,13 @@ __device__ inline __amdgpu_buffer_rsrc_t y_rsrc(bf16_t* y, uint32_t m0, uint32_t
     return __builtin_amdgcn_make_buffer_rsrc(y + static_cast<int64_t>(m0) * H, 0,
                                              static_cast<int>(rows * static_cast<uint32_t>(H) * 2u), 0x00020000);
 }
+// A buffer over `bytes` bytes of p (0: every access is dropped or reads 0).
+__device__ inline __amdgpu_buffer_rsrc_t flat_rsrc(void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(p, 0, static_cast<int>(bytes), 0x00020000);
+}
+// Marks a row past the segment's end in the folded kernels' row tables
+// (not an offset: every offset a buffer access takes stays below 2^31).
+constexpr uint32_t kNoRow = 0xFFFFFFFFu;
 
 // 16-byte chunks c0 .. c0 + N - 1 of this thread's share of the staged y
 // tile: chunk c is tile row (tid + 256 c) / 16, column chunk (tid + 256 c) % 16.
@@ -1110,6 +1135,53 @@ __device__ inline void write_y_chunks(__amdgpu_buffer_rsrc_t rs, int H, int nb, 
     }
 }
 
+// The folded combine's rows.  rowoff[c] is the byte offset of this thread's
+// chunk row c (tile row tid / 16 + 16 c) in a [T][H] bf16 array, token x
+// 2H, or the array's size past the segment's end; tok_off adds the chunk's
+// column (below 2^20), so a row past the end lands past the array, out of
+// range of its buffer, and every offset stays below 2^31 (T H 2 + 2^20 <
+// 2^31): the buffer range check drops such accesses, while offsets with bit
+// 31 set must not be relied on to be dropped.
+__device__ inline uint32_t tok_off(uint32_t rowoff, int nb, int tid) {
+    return rowoff + static_cast<uint32_t>((nb * 128 + (tid & 15) * 8) * 2);
+}
+// The staged y tile's bytes (row pitch kArPitch bf16) as 17 direct-to-LDS
+// copies per thread: copy i of thread tid fills stage bytes P = 4096 i +
+// 16 tid, i.e. row P / 272 at byte P % 272.  kYaCopies covers 256 rows.
+constexpr int kYaCopies = (kArRows * kArPitch * 2 + 4095) / 4096;
+static_assert(kArPitch * 2 % 16 == 0, "16-byte copies tile a staged row");
+// 4 bf16 of a and of b (u32x2 each): (0 + 0.5 a) + 0.5 b element-wise,
+// rounded to bf16, as two FMAs: t = fma(b, 0.5, 0) is 0.5 b with -0 made +0
+// (exact), then fma(a, 0.5, t) rounds 0.5 a + t once.  0.5 v is exact for a
+// bf16 v, so this equals the reference's two rounded adds for every input
+// pair, signed zeros included (the reference never yields -0: its first add
+// turns -0 into +0; here t does, and a -0 first term meets +0 or a nonzero).
+__device__ inline float combine_fma(float a, float b) { return __fmaf_rn(a, 0.5f, __fmaf_rn(b, 0.5f, 0.0f)); }
+__device__ inline u32x2_t combine4_bf16(u32x2_t a, u32x2_t b) {
+    float o[4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        o[2 * k] = combine_fma(__uint_as_float(a[k] << 16), __uint_as_float(b[k] << 16));
+        o[2 * k + 1] = combine_fma(__uint_as_float(a[k] & 0xFFFF0000u), __uint_as_float(b[k] & 0xFFFF0000u));
+    }
+    return u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) for any n in 0 .. 47 known at run time.
+template <int N>
+__device__ inline void wait_vm_lgkm0_table(int n) {
+    if constexpr (N < 0) {
+        wait_vm_lgkm0<0>();
+    } else {
+        if (n == N) wait_vm_lgkm0<N>();
+        else wait_vm_lgkm0_table<N - 1>(n);
+    }
+}
+__device__ inline void wait_vm_lgkm0_n(int n) {
+    if (n >= 47) wait_vm_lgkm0<47>();
+    else wait_vm_lgkm0_table<46>(n);
+}
+
 // KT (k stages of 128 bytes) is a template argument so that the resident act
 // fragments take exactly KT x 2 x kSub registers.  With KT >= 4 (the
 // production shapes: F = 448 bf16, 512 fp8) the y tile of column block u-1
@@ -1122,20 +1194,35 @@ __device__ inline void write_y_chunks(__amdgpu_buffer_rsrc_t rs, int H, int nb, 
 // stage g-1 with stage g+3... (g+1)+2.  Per step: wait for this step's
 // fragments, [barrier], [read this step's share of the staged y tile],
 // read the fragments of step + 2, MFMAs, [store the y share].
-template <class Fmt, int KT>
+//
+// FOLD (the fused forward's combine, KT >= 4, bf16 output): the kernel walks
+// one slot of the dispatch's slot-ordered lists (act rows gathered through
+// slot_rows, outputs scattered to token rows).  FOLD 1 stores each slot-0
+// row's bf16 output row to ya[token] (y is ya).  FOLD 2 (fp8) combines each
+// slot-1 row with it into out[token] = (0 + 0.5 ya) + 0.5 y, the reference's
+// combine: it stores the previous tile in k stages 0 and 1 (8 chunks each),
+// which frees the stage; at k stage 2 it copies its own tile's ya rows into
+// the stage (direct to LDS, in the stage's layout), and the epilogue
+// combines each value in place.
+template <class Fmt, int KT, int FOLD = 0>
 __global__ void __launch_bounds__(256, 1)
 k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint32_t* __restrict__ offsets,
               const uint8_t* __restrict__ w2, bf16_t* __restrict__ y, int H, int E,
-              const float* __restrict__ sa, const float* __restrict__ s2) {
+              const float* __restrict__ sa, const float* __restrict__ s2, const uint32_t* __restrict__ slot1,
+              const uint32_t* __restrict__ slot_rows, const uint32_t* __restrict__ slot_tokens,
+              bf16_t* __restrict__ out, int64_t tokens) {
     constexpr bool kFp8 = Fmt::kElt == 1;
     constexpr bool kOverlap = KT >= 4;
+    static_assert(FOLD == 0 || kOverlap, "the folded combine needs the overlapped stores");
+    static_assert(FOLD != 2 || (kFp8 && KT == 4), "the folded combine's schedule is fp8's, four k stages");
     constexpr int KTM = KT;
     constexpr int kSub = Fmt::kSub;
     constexpr int kLoads = kFp8 ? 8 : 4;       // ds_read_b128 per fragment set
+    constexpr int kChunks = FOLD == 2 ? 8 : 4;  // staged chunks stored per storing k stage
     static_assert(kSub >= 2, "two steps per stage");
     __shared__ __align__(16) ArLds<kFp8> lds;
     ArWork u;
-    if (!locate_ar(offsets, E, H / 128, u)) return;
+    if (!locate_ar<FOLD>(offsets, slot1, E, H / 128, u)) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int aR = wave * 64;
@@ -1143,8 +1230,40 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
     const int nunits = u.nb1 - u.nb0;
     const int nstages = nunits * KT;
     bf16_t* stage = reinterpret_cast<bf16_t*>(lds.stage);
-    const __amdgpu_buffer_rsrc_t ys = y_rsrc(y, u.m0, u.end, H, true);
-    const __amdgpu_buffer_rsrc_t ynull = y_rsrc(y, u.m0, u.end, H, false);
+    // FOLD 0: y tile rows m0 .. m0 + 255 (contiguous); FOLD 1 / 2: [T][H]
+    // bf16 arrays (ya, out) addressed per row through rowoff[]
+    const uint32_t tbytes = static_cast<uint32_t>(tokens) * static_cast<uint32_t>(H) * 2u;
+    const __amdgpu_buffer_rsrc_t ys = FOLD == 0 ? y_rsrc(y, u.m0, u.end, H, true)
+                                               : flat_rsrc(FOLD == 1 ? y : out, tbytes);
+    const __amdgpu_buffer_rsrc_t ynull = FOLD == 0 ? y_rsrc(y, u.m0, u.end, H, false) : flat_rsrc(y, 0u);
+    uint32_t rowoff[16];
+    uint32_t yaoff[FOLD == 2 ? kYaCopies : 1];   // FOLD 2: ya source of each stage copy (kNoRow: none)
+    if constexpr (FOLD != 0) {
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const uint32_t q = u.m0 + static_cast<uint32_t>((tid >> 4) + 16 * c);
+            const uint32_t tk = q < u.end ? slot_tokens[q] : kNoRow;
+            rowoff[c] = tk < static_cast<uint32_t>(tokens) ? tk * static_cast<uint32_t>(2 * H) : tbytes;
+        }
+    }
+    if constexpr (FOLD == 2) {
+#pragma unroll
+        for (int i = 0; i < kYaCopies; ++i) {
+            const uint32_t P = 4096u * i + 16u * tid;
+            const uint32_t row = P / (kArPitch * 2), b = P % (kArPitch * 2);
+            const uint32_t q = u.m0 + row;
+            uint32_t tk = row < kArRows && b < 256u && q < u.end ? slot_tokens[q] : kNoRow;
+            yaoff[i] = tk < static_cast<uint32_t>(tokens) ? tk * static_cast<uint32_t>(2 * H) + b : kNoRow;
+        }
+    }
+    // act row (plan position) of list entry q
+    auto act_pos = [&](uint32_t q) -> uint32_t {
+        q = q < u.end ? q : u.end - 1;
+        if constexpr (FOLD == 0) return q;
+        const uint32_t p = slot_rows[q];
+        const uint32_t amax = 2u * static_cast<uint32_t>(tokens) - 1u;
+        return p < amax ? p : amax;
+    };
 
     // w2 ring: stage g = (unit g / KT, k stage g % KT); wave w copies bytes
     // [4 KB w, 4 KB w + 4 KB) of the 16 KB image, verbatim (pre-swizzled).
@@ -1155,17 +1274,35 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
 #pragma unroll
         for (int c = 0; c < 4; ++c) dma16(src + c * 1024, dst + c * 1024);
     };
-    // y chunks issued by the overlap schedule at k stage k of a column block
-    auto stores_at = [](int k) { return kOverlap && (k + KTM) % KTM < 4 ? 4 : 0; };
+    // FOLD 2: column block nb's ya rows into the stage (rows past the
+    // segment read ya row 0 into rows whose results are dropped)
+    auto issue_ya = [&](int nb) {
+#pragma unroll
+        for (int i = 0; i < kYaCopies; ++i) {
+            const uint32_t off = yaoff[i] == kNoRow ? 0u : yaoff[i] + static_cast<uint32_t>(nb * 256);
+            dma16(reinterpret_cast<const uint8_t*>(y) + off, lds.stage + 4096 * i + 1024 * wave);
+        }
+    };
+    // VMEM operations issued at stage x (global index, x = unit x / KT, k
+    // stage x % KT): staged-chunk stores (k stages 0..3, FOLD 2: 0..1) and
+    // FOLD 2's stage copies (k stage 2).  Unit 0 has no previous tile: FOLD 0
+    // issues its stores to a null buffer (same count at every unit), the
+    // folded kernels issue none (the counts below follow).
+    auto has_st = [](int k) { return kOverlap && (k + KTM) % KTM < (FOLD == 2 ? 2 : 4); };
+    auto vm_at = [&](int x) {
+        const bool st = has_st(x % KTM) && (FOLD == 0 || x >= KTM);
+        return (st ? kChunks : 0) + (FOLD == 2 && x % KTM == 2 ? kYaCopies : 0);
+    };
     // Stage g (k stage kt) landed for every wave.  Issued after stage g's
-    // copies (at stage_ready(g-2)): stage g+1's copies, if any, and the y
-    // chunks of k stages kt-2, kt-1 (bf16: the stores of a stage precede its
-    // stage_ready) or kt-3, kt-2 (fp8: they follow it).  Stages 0..2 wait for
-    // everything.  Then stage g-2's slot takes stage g+2.
+    // copies (at stage_ready(g-2)): stage g+1's copies, if any, and the
+    // operations of k stages kt-2, kt-1 (bf16: the stores of a stage precede
+    // its stage_ready) or kt-3, kt-2 (fp8: they follow it).  Stages 0..2
+    // wait for everything.  Then stage g-2's slot takes stage g+2.
     auto stage_ready = [&](int g, int kt) {
         const int later = g + 1 < nstages ? 1 : 0;
-        const int kS = kFp8 ? stores_at(kt - 2) + stores_at(kt - 3) : stores_at(kt - 1) + stores_at(kt - 2);
-        wait_vm_lgkm0_upto20(g < 3 ? 0 : 4 * later + kS);
+        const int kS = g < 3 ? 0 : (kFp8 ? vm_at(g - 2) + vm_at(g - 3) : vm_at(g - 1) + vm_at(g - 2));
+        if constexpr (FOLD == 2) wait_vm_lgkm0_n(g < 3 ? 0 : 4 * later + kS);
+        else wait_vm_lgkm0_upto20(g < 3 ? 0 : 4 * later + kS);
         raw_barrier();
         if (g + 2 < nstages) issue_b(g + 2);
     };
@@ -1176,11 +1313,7 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
         for (int t = tid; t < nunits * 32; t += 256)
             *reinterpret_cast<float4*>(lds.scl + 4 * t) = *reinterpret_cast<const float4*>(src + 4 * t);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            uint32_t p = u.m0 + aR + 32 * i + (lane & 31);
-            p = p < u.end ? p : u.end - 1;
-            rs[i] = sa[p];
-        }
+        for (int i = 0; i < 2; ++i) rs[i] = sa[act_pos(u.m0 + aR + 32 * i + (lane & 31))];
     }
 
     // ---- the row tile of act into registers, one 32 KB stage at a time ----
@@ -1195,9 +1328,7 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const int row = slot_row(s, wave, lane);
-            uint32_t p = u.m0 + row;
-            p = p < u.end ? p : u.end - 1;
-            asrc[s] = act + static_cast<int64_t>(p) * act_row_bytes + slot_chunk(row, lane) * 16;
+            asrc[s] = act + static_cast<int64_t>(act_pos(u.m0 + row)) * act_row_bytes + slot_chunk(row, lane) * 16;
         }
         auto aslot = [&](int kt) -> uint8_t* {
             const int j = kt & 3;
@@ -1261,9 +1392,9 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
                     if (next1) wait_lgkm_n<kLoads>();
                     else wait_lgkm0();
                     if (s == kSub - 2 && g + 1 < nstages) stage_ready(g + 1, (kt + 1) % KTM);
-                    const bool st = kOverlap && s == 0 && kt < 4;
-                    u32x4_t yv[4];
-                    if (st) read_y_chunks<4>(stage, 4 * kt, tid, yv);
+                    const bool st = s == 0 && has_st(kt);
+                    u32x4_t yv[kChunks];
+                    if (st) read_y_chunks<kChunks>(stage, kChunks * kt, tid, yv);
                     if (next2) {
                         const int s2_ = (s + 2) % kSub;
                         load_b(bf[(q + 2) % 3], s + 2 < kSub ? g : g + 1, s2_);
@@ -1273,14 +1404,31 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
                     for (int i = 0; i < 2; ++i)
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
-                            if (q == 0) Fmt::mma_pinned_first(acc[i][j], bf[q % 3][j], areg[kt][i][s]);
-                            else Fmt::mma_pinned(acc[i][j], bf[q % 3][j], areg[kt][i][s]);
+                            // the folded kernels' register pressure puts B
+                            // fragments in AGPRs, copied back right before use
+                            if (q == 0) Fmt::template mma_pinned_first<FOLD != 0>(acc[i][j], bf[q % 3][j], areg[kt][i][s]);
+                            else Fmt::template mma_pinned<FOLD != 0>(acc[i][j], bf[q % 3][j], areg[kt][i][s]);
                         }
                     APS_PIN();
-                    if (st) {
-                        // the previous column block's y chunks 4kt .. 4kt+3
-                        write_y_chunks<4>(prev, H, nb - 1, 4 * kt, tid, yv);
+                    if (st && (FOLD == 0 || ui > 0)) {
+                        // the previous column block's chunks kChunks kt ..
+                        if constexpr (FOLD == 0) {
+                            write_y_chunks<4>(prev, H, nb - 1, 4 * kt, tid, yv);
+                        } else {
+#pragma unroll
+                            for (int c = 0; c < kChunks; ++c)
+                                __builtin_amdgcn_raw_buffer_store_b128(yv[c], ys,
+                                                                       tok_off(rowoff[kChunks * kt + c], nb - 1, tid), 0, 0);
+                        }
                         APS_PIN();
+                    }
+                    if constexpr (FOLD == 2) {
+                        if (s == 0 && kt == 2) {
+                            // every wave has read the stage out (the barrier of
+                            // this step's stage_ready): this tile's ya rows go in
+                            issue_ya(nb);
+                            APS_PIN();
+                        }
                     }
                 }
             }
@@ -1288,6 +1436,13 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
 
         // epilogue: scales (fp8), bf16, staged in LDS
         if constexpr (Fmt::kPinned) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");  // MFMA write -> VALU read
+        if constexpr (FOLD == 2) {
+            // this wave's ya copies have landed (issued at k stage 2; since:
+            // the ring copies of k stage 3's stage_ready, if it ran one); the
+            // barrier below makes every wave's visible
+            const int g3 = g0 + 3;
+            wait_vm_lgkm0_n(g3 + 1 < nstages && g3 + 3 < nstages ? 4 : 0);
+        }
         if (kOverlap) raw_barrier();  // every thread has read the previous tile out of the stage
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -1305,21 +1460,38 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
                         o[0] = o[0] * rs[i] * a.x; o[1] = o[1] * rs[i] * a.y;
                         o[2] = o[2] * rs[i] * a.z; o[3] = o[3] * rs[i] * a.w;
                     }
+                    u32x2_t* at = reinterpret_cast<u32x2_t*>(stage + row * kArPitch + col);
                     const u32x2_t v = {pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
-                    *reinterpret_cast<u32x2_t*>(stage + row * kArPitch + col) = v;
+                    // FOLD 2: this row's slot-1 output (bf16, as y would hold
+                    // it) combined with the token's slot-0 row in the stage
+                    if constexpr (FOLD == 2) *at = combine4_bf16(*at, v);
+                    else *at = v;
                 }
         }
         wait_lgkm0();
         raw_barrier();
-        if (!kOverlap || ui + 1 == nunits) {
-            // no later column block to hide under: store the tile now
+        if constexpr (FOLD == 0) {
+            if (!kOverlap || ui + 1 == nunits) {
+                // no later column block to hide under: store the tile now
+                u32x4_t yv[16];
+                read_y_chunks<16>(stage, 0, tid, yv);
+                write_y_chunks<16>(ys, H, nb, 0, tid, yv);
+                if (!kOverlap) {
+                    wait_lgkm0();
+                    raw_barrier();  // the stage is read out before the next epilogue
+                }
+            }
+        }
+    }
+    if constexpr (FOLD != 0) {
+        // the last column block's tile, after the loop
+        if (nunits > 0) {
+            const int nb = u.nb1 - 1;
             u32x4_t yv[16];
             read_y_chunks<16>(stage, 0, tid, yv);
-            write_y_chunks<16>(ys, H, nb, 0, tid, yv);
-            if (!kOverlap) {
-                wait_lgkm0();
-                raw_barrier();  // the stage is read out before the next epilogue
-            }
+#pragma unroll
+            for (int c = 0; c < 16; ++c)
+                __builtin_amdgcn_raw_buffer_store_b128(yv[c], ys, tok_off(rowoff[c], nb, tid), 0, 0);
         }
     }
 }
@@ -1328,7 +1500,8 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
 // The register-resident w2 kernel for KT k stages, or null when KT is past
 // the register budget (the streamed kernel serves those shapes).
 typedef void (*down_ar_fn)(const uint8_t*, int64_t, const uint32_t*, const uint8_t*, bf16_t*, int, int,
-                           const float*, const float*);
+                           const float*, const float*, const uint32_t*, const uint32_t*, const uint32_t*, bf16_t*,
+                           int64_t);
 template <class Fmt>
 down_ar_fn down_ar_kernel(int KT) {
     switch (KT) {
@@ -1341,6 +1514,13 @@ down_ar_fn down_ar_kernel(int KT) {
         case 7: return DownAr<Fmt>::kKtMax >= 7 ? k_ffn_down_ar<Fmt, (DownAr<Fmt>::kKtMax >= 7 ? 7 : 1)> : nullptr;
         default: return nullptr;
     }
+}
+
+// The folded combine's two passes for fp8's production k-stage count (KT =
+// 4), or null.
+down_ar_fn down_fold_kernel_fp8(int KT, int fold) {
+    if (KT != 4) return nullptr;
+    return fold == 1 ? k_ffn_down_ar<Fp8Fmt, 4, 1> : k_ffn_down_ar<Fp8Fmt, 4, 2>;
 }
 
 // Grid of the register-resident w2 kernel: about one block per CU, at least
@@ -1403,7 +1583,8 @@ hipError_t launch_ffn_down_bf16(const bf16_t* act, const uint32_t* offsets, cons
     if (auto kern = down_ar_kernel<Bf16Fmt>(ffn / 64)) {
         hipLaunchKernelGGL(kern, grid_ar(rows, experts), dim3(256), 0, s,
                            reinterpret_cast<const uint8_t*>(act), static_cast<int64_t>(ffn) * 2, offsets,
-                           reinterpret_cast<const uint8_t*>(w2), y, hidden, experts, nullptr, nullptr);
+                           reinterpret_cast<const uint8_t*>(w2), y, hidden, experts, nullptr, nullptr, nullptr,
+                           nullptr, nullptr, nullptr, rows);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_ffn_down<Bf16Fmt>, grid_of(max_blocks(rows, hidden / 128, experts, APS_DOWN_TALL)),
@@ -1433,13 +1614,39 @@ hipError_t launch_ffn_down_fp8(const uint8_t* actq, const float* act_scale, cons
     const int kpad = static_cast<int>(ceil_div(ffn, 128) * 128);
     if (auto kern = down_ar_kernel<Fp8Fmt>(kpad / 128)) {
         hipLaunchKernelGGL(kern, grid_ar(rows, experts), dim3(256), 0, s, actq,
-                           static_cast<int64_t>(kpad), offsets, w2, y, hidden, experts, act_scale, w2_scale);
+                           static_cast<int64_t>(kpad), offsets, w2, y, hidden, experts, act_scale, w2_scale,
+                           nullptr, nullptr, nullptr, nullptr, rows);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_ffn_down<Fp8Fmt>, grid_of(max_blocks(rows, hidden / 128, experts, APS_DOWN_TALL)),
                        dim3(256), 0, s, actq, static_cast<int64_t>(kpad), offsets, w2, y, hidden, kpad / 128,
                        experts, act_scale, w2_scale);
     return hipGetLastError();
+}
+
+bool ffn_down_fold_fits(int64_t rows, int hidden, int ffn) {
+    // byte offsets into the [rows][hidden] bf16 arrays stay below 2^31
+    const int64_t bytes = rows * static_cast<int64_t>(hidden) * 2;
+    return rows > 0 && hidden % 128 == 0 && ffn % 64 == 0 && ceil_div(ffn, 128) == 4 &&
+           bytes + (int64_t(1) << 20) < (int64_t(1) << 31);
+}
+
+hipError_t launch_ffn_down_fold_fp8(const uint8_t* actq, const float* act_scale, const uint32_t* offsets,
+                                    const uint32_t* slot1, const uint32_t* slot_rows, const uint32_t* slot_tokens,
+                                    const uint8_t* w2, const float* w2_scale, bf16_t* ya, bf16_t* out,
+                                    int64_t rows, int hidden, int ffn, int experts, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (!ffn_down_fold_fits(rows, hidden, ffn)) return hipErrorInvalidValue;
+    const int kpad = static_cast<int>(ceil_div(ffn, 128) * 128);
+    for (int fold = 1; fold <= 2; ++fold) {
+        down_ar_fn kern = down_fold_kernel_fp8(kpad / 128, fold);
+        if (!kern) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(kern, grid_ar(rows, experts), dim3(256), 0, s, actq, static_cast<int64_t>(kpad), offsets,
+                           w2, ya, hidden, experts, act_scale, w2_scale, slot1, slot_rows, slot_tokens, out, rows);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace aps

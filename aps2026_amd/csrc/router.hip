@@ -33,9 +33,11 @@
 //    A lane-per-token layout (x per lane from LDS and converted every step,
 //    gate broadcast) ran at 12.4.
 // After the chain a row holds its token's E logits.  Every lane gathers them
-// (ds_bpermute), quantises and runs the reference's greedy scan; the
+// (DPP row broadcasts), quantises and runs the reference's greedy scan; the
 // workgroup's per-expert counts (one 16-token quarter of a 64-token tile)
-// become one byte of the tile histogram words that the dispatch reads.
+// become one byte of the tile histogram words that the dispatch reads, and,
+// when asked, the counts of slot-0 routes alone one byte of a second
+// histogram (the dispatch's slot-ordered lists for the folded combine).
 #include "common.hpp"
 
 #include <utility>
@@ -207,7 +209,7 @@ template <bool XBF16, int R, int GW, bool XCOPY = false, int NWV = 4>
 __global__ void __launch_bounds__(64 * NWV * R)
 k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, int E,
          float* __restrict__ logits, uint8_t* __restrict__ routes, uint8_t* __restrict__ tile_bytes,
-         bf16_t* __restrict__ xcopy) {
+         uint8_t* __restrict__ tile_bytes0, bf16_t* __restrict__ xcopy) {
     static_assert(!(XCOPY && XBF16), "the bf16 copy is made from fp32 x");
     constexpr int kGW = GW;                    // windows per ring stage
     constexpr int kWinBytes = 8 * 1024 * R;    // 32 (k/4) x 16 R experts x 16 B
@@ -223,7 +225,9 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
     constexpr int kTok = 4 * NWV;              // tokens per workgroup
     constexpr int kQ = kTok / kRTokens;        // routing-tile quarters per workgroup
     static_assert(R == 1 || NWV == 4, "eight-wave workgroups for E <= 16");
-    __shared__ uint32_t cnt[kQ][16 * R];
+    // [0]: the quarters' route counts per expert, [1]: slot-0 routes only
+    // (tile_bytes0)
+    __shared__ uint32_t cnt[2][kQ][16 * R];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -233,7 +237,8 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kTok + gr / R;
     const int NW = H / kRWin;
     const int NG = NW / kGW;
-    if (tid < kQ * 16 * R) cnt[tid / (16 * R)][tid % (16 * R)] = 0u;
+    static_assert(2 * kQ * 16 * R <= 64 * NWV * R, "one counter per thread to clear");
+    if (tid < 2 * kQ * 16 * R) (&cnt[0][0][0])[tid] = 0u;
 
     // x: lane i of a row reads elements 8i .. 8i+7 of every window of its
     // token (rows past the end re-read the last row; their results are
@@ -363,7 +368,8 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
         routes[2 * t] = static_cast<uint8_t>(first);
         routes[2 * t + 1] = static_cast<uint8_t>(second);
     }
-    if (valid && e < E && (e == first || e == second)) atomicAdd(&cnt[(gr / R) / kRTokens][e], 1u);
+    if (valid && e < E && (e == first || e == second)) atomicAdd(&cnt[0][(gr / R) / kRTokens][e], 1u);
+    if (tile_bytes0 && valid && e < E && e == first) atomicAdd(&cnt[1][(gr / R) / kRTokens][e], 1u);
     __syncthreads();
     if (tid < kQ * E) {
         // byte (quarter % 4) of word [tile][expert]; the last workgroup also
@@ -372,9 +378,15 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
         const int64_t quarter = static_cast<int64_t>(blockIdx.x) * kQ + qi;
         const int sub = static_cast<int>(quarter % 4);
         uint8_t* word = tile_bytes + ((quarter / 4) * E + ex) * 4;
-        word[sub] = static_cast<uint8_t>(cnt[qi][ex]);
+        word[sub] = static_cast<uint8_t>(cnt[0][qi][ex]);
         if (blockIdx.x == gridDim.x - 1 && qi == kQ - 1)
             for (int s2 = sub + 1; s2 < 4; ++s2) word[s2] = 0;
+        if (tile_bytes0) {
+            uint8_t* word0 = tile_bytes0 + ((quarter / 4) * E + ex) * 4;
+            word0[sub] = static_cast<uint8_t>(cnt[1][qi][ex]);
+            if (blockIdx.x == gridDim.x - 1 && qi == kQ - 1)
+                for (int s2 = sub + 1; s2 < 4; ++s2) word0[s2] = 0;
+        }
     }
 }
 
@@ -415,13 +427,15 @@ k_route_top2(const float* __restrict__ logits, int64_t rows, int E, uint8_t* __r
 
 hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t rows, int hidden,
                          int experts, float* logits, uint8_t* routes, uint32_t* tile_counts,
-                         bf16_t* x_copy, hipStream_t s) {
+                         uint32_t* tile_counts0, bf16_t* x_copy, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (hidden <= 0 || hidden % (2 * kRWin) != 0 || experts <= 0 || experts > kMaxExperts)
         return hipErrorInvalidValue;
     if (routes && (experts < 2 || !tile_counts)) return hipErrorInvalidValue;
+    if (tile_counts0 && !routes) return hipErrorInvalidValue;
     if (x_copy && x_bf16) return hipErrorInvalidValue;
     auto* tb = reinterpret_cast<uint8_t*>(tile_counts);
+    auto* tb0 = reinterpret_cast<uint8_t*>(tile_counts0);
     // windows per stage: 512 steps of 16 R experts (32 KB) when H allows
     const int R = experts <= 16 ? 1 : experts <= 32 ? 2 : 4;
     const bool wide = hidden % (4 * kRWin) == 0;
@@ -436,10 +450,10 @@ hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t 
     do {                                                                                                      \
         if (!(XB) && x_copy)                                                                                 \
             hipLaunchKernelGGL((k_router<false, R, GW, true, NWV>), grid, dim3(64 * NWV * R), 0, s, x, gate, \
-                               rows, hidden, experts, logits, routes, tb, x_copy);                           \
+                               rows, hidden, experts, logits, routes, tb, tb0, x_copy);                      \
         else                                                                                                 \
             hipLaunchKernelGGL((k_router<XB, R, GW, false, NWV>), grid, dim3(64 * NWV * R), 0, s, x, gate,   \
-                               rows, hidden, experts, logits, routes, tb, nullptr);                          \
+                               rows, hidden, experts, logits, routes, tb, tb0, nullptr);                     \
     } while (0)
     if (x_bf16) {
         if (eight) APS_ROUTER_LAUNCH(true, 1, 4, 8);

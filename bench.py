@@ -450,6 +450,35 @@ def decoder_bench(args):
         lw.release()
 
 
+PROBE_LIB = os.path.join(ROOT, "aps2026_amd", "probe", "libaps_probe.so")
+
+
+def fma_chain_costs():
+    """fp32 FMA chain costs on this device, from aps_probe_fma_chain
+    (aps2026_amd/probe/fma_chain.hip; one workgroup per CU, 8192 steps):
+    dependent v_fmac_f32 at one wave per SIMD (the chain latency),
+    dependent v_fmac_f32_dpp (the router's instruction), and independent
+    FMAs at four waves per SIMD (the SIMD's issue interval per wave
+    instruction: cycles per wave / 4); shader clock in MHz."""
+    if not os.path.exists(PROBE_LIB):
+        raise RuntimeError(f"{PROBE_LIB} is not built (python -m aps2026_amd.build)")
+    L = ctypes.CDLL(PROBE_LIB)
+    L.aps_probe_fma_chain.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_double)] * 2
+
+    def run(waves_per_simd, dpp, chains):
+        cyc, mhz = ctypes.c_double(0.0), ctypes.c_double(0.0)
+        rc = L.aps_probe_fma_chain(waves_per_simd, dpp, chains, 8192, ctypes.byref(cyc), ctypes.byref(mhz))
+        if rc != 0:
+            raise RuntimeError(f"aps_probe_fma_chain: HIP error {rc}")
+        return cyc.value, mhz.value
+
+    dep, mhz = run(1, 0, 1)
+    dep_dpp, _ = run(1, 1, 1)
+    ind4, _ = run(4, 0, 2)
+    return {"dependent_cycles": dep, "dependent_dpp_cycles": dep_dpp, "simd_issue_cycles": ind4 / 4.0,
+            "clock_mhz": mhz}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -608,18 +637,23 @@ def main():
     bytes_router = T * H * esz + E * H * 4 + T * E * 4
     bytes_combine = A * H * esz + T * H * esz + A * 4
     # The router's bound is its FMA chains, not HBM: every logit is one fp32
-    # FMA chain over H steps in the reference's order, so the floor is the
-    # longer of one chain at one VALU issue (4 cycles for a 64-wide wave on a
-    # 16-lane SIMD) per step, and all T*E chains through every SIMD's 16
-    # lanes, at the 2.4 GHz peak clock.
+    # FMA chain over H steps in the reference's order, one chain per lane.
+    # Floor per step: the dependent-FMA latency of one wave, or, when the
+    # T*E chains need several waves per SIMD, that many wave instructions at
+    # the SIMD's issue interval; both measured on this device at its
+    # sustained clock (aps2026_amd/probe/fma_chain.hip).
     n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
-    chain_cycles = max(4.0 * H, T * E * H / (n_cu * 64.0))
-    chain_floor_s = chain_cycles / 2.4e9
+    fma = fma_chain_costs()
+    waves_per_simd = -(-T * E // (n_cu * 4 * 64))
+    floor_cycles = max(fma["dependent_cycles"], waves_per_simd * fma["simd_issue_cycles"])
+    chain_floor_s = H * floor_cycles / (fma["clock_mhz"] * 1e6)
     stage_report = {
         "router_logits": {"us": mean_t["router_logits"] * 1e6,
                           "GB_s": bytes_router / mean_t["router_logits"] / 1e9,
                           "chain_floor_us": chain_floor_s * 1e6,
-                          "frac_of_chain_floor": chain_floor_s / mean_t["router_logits"]},
+                          "frac_of_chain_floor": chain_floor_s / mean_t["router_logits"],
+                          "cycles_per_step": mean_t["router_logits"] * fma["clock_mhz"] * 1e6 / H,
+                          "fma_chain_probe": {**fma, "waves_per_simd": waves_per_simd}},
         "route_top2": {"us": mean_t["route_top2"] * 1e6},
         "dispatch": {"us": mean_t["dispatch"] * 1e6},
         "ffn_up": {"us": mean_t["ffn_up"] * 1e6, "TFLOP_s": flops_up / mean_t["ffn_up"] / 1e12},

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define APS_MOE_ABI_VERSION 1
+#define APS_MOE_ABI_VERSION 2  /* 2: aps_moe_ws_layout grew the slot-ordered lists */
 
 #if defined(__GNUC__) || defined(__clang__)
 #define APS_API __attribute__((visibility("default")))
@@ -106,6 +106,14 @@ typedef struct aps_moe_ws_layout {
     size_t xq_scale;        /* fp8 path: f32 [rows] per-token scale */
     size_t actq;            /* fp8 path: e4m3 act [2*rows][ffn rounded
                                up to 128], zero padded              */
+    size_t tile_counts0;    /* u32 [ceil(rows/64)][E]: as tile_counts,
+                               slot-0 routes only (aps_moe_forward) */
+    size_t slot1;           /* u32 [E]: offsets[e] + slot-0 routes of e */
+    size_t slot_rows;       /* u32 [2*rows] slot-ordered list: entries
+                               [offsets[e], slot1[e]) the positions of
+                               e's slot-0 routes, [slot1[e], offsets[e+1])
+                               of its slot-1 routes, tokens ascending  */
+    size_t slot_tokens;     /* u32 [2*rows] the token of each entry  */
 } aps_moe_ws_layout;
 
 /* ---- weights ----------------------------------------------------------- */

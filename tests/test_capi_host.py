@@ -15,7 +15,7 @@ def test_library_exports_every_declared_symbol():
     assert len(names) == 42
     for n in names:
         assert hasattr(L, n), n
-    assert L.aps_moe_abi_version() == 1
+    assert L.aps_moe_abi_version() == 2
 
 
 def _desc(E=16, H=4096, F=448, src=capi.DTYPE_BF16, compute=capi.DTYPE_BF16, null_table=False):

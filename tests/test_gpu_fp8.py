@@ -53,12 +53,20 @@ def rowwise_err(got, ref):
 
 
 def run_block(inp, dev):
+    """The fused forward (router, and for F in (384, 512] the w2 GEMM with
+    the combine folded in), then the grouped forward from the router's
+    logits (w2 to y, then k_combine), which leaves every intermediate in the
+    workspace: the two outputs must agree bit for bit."""
     w = fp8_weights(inp, dev)
     x = to_dev_bf16(inp.packed["x_bf16"], dev)
     gate = torch.from_numpy(inp.gate).to(dev)
     out = moe.moe_forward_gpu(x, gate, w, out_dtype=torch.bfloat16)
+    logits = w.plan_views(inp.T)["logits"].clone()
+    out_g = moe.moe_forward_grouped_gpu(x, logits, w, out_dtype=torch.bfloat16)
     plan = w.plan_views(inp.T)
     torch.cuda.synchronize()
+    diff = int((out.view(torch.int16) != out_g.view(torch.int16)).sum())
+    assert diff == 0, f"fused forward and w2 + combine differ in {diff} elements"
     return w, out, plan
 
 
