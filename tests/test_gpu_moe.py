@@ -172,6 +172,48 @@ def test_large_batch_65536_tokens(gpu_device):
     w.release()
 
 
+@pytest.mark.parametrize("y_dtype,out_dtype", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                               (torch.float32, torch.float32), (torch.float32, torch.bfloat16)])
+def test_combine_signed_zeros_and_special_values(gpu_device, y_dtype, out_dtype):
+    """aps_moe_combine against the oracle's literal (0 + 0.5 a) + 0.5 b
+    (k_moe_combine): token pairs of -0/-0 (the reference gives +0), -0/+0,
+    -0/x, subnormals, the largest finite values (0.5 a + 0.5 b stays finite),
+    infinities and NaN, beside random values; bit for bit, NaN as NaN."""
+    rng = np.random.default_rng(21)
+    T, H = 300, 256
+    y = rng.standard_normal((2 * T, H)).astype(np.float32)
+    special = np.array([-0.0, 0.0, -0.0, 1.5, 1e-40, -1e-40, 3.3e38, 3.3e38, np.inf, -np.inf, np.nan, 2.0],
+                       np.float32)
+    pos = rng.permutation(2 * T).astype(np.uint32)
+    for k in range(len(special)):
+        for j in range(len(special)):
+            t = (k * len(special) + j) % T
+            y[pos[2 * t], k * 16 + j] = special[k]
+            y[pos[2 * t + 1], k * 16 + j] = special[j]
+    if y_dtype == torch.bfloat16:
+        y = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(y))   # the values a bf16 y holds
+        y_dev = torch.from_numpy(synth.f32_to_bf16_bits(y).view(np.int16)).to(gpu_device).view(torch.bfloat16)
+    else:
+        y_dev = torch.from_numpy(y).to(gpu_device)
+    routes = np.zeros((T, 2), np.int32)
+    routes[:, 1] = 1
+    want = oracle.combine(y, routes, pos)
+    got = moe.combine(y_dev, torch.from_numpy(pos.view(np.int32)).to(gpu_device), T, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    if out_dtype == torch.bfloat16:
+        got = synth.bf16_bits_to_f32(got.view(torch.int16).cpu().numpy().view(np.uint16))
+        want = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(want))
+    else:
+        got = got.cpu().numpy()
+    nan = np.isnan(want)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got.view(np.uint32)[~nan], want.view(np.uint32)[~nan])
+    # the -0/-0 pairs (special values 0 and 2) gave +0
+    for k, j in ((0, 0), (0, 2), (2, 0), (2, 2)):
+        t = (k * len(special) + j) % T
+        assert got.view(np.uint32)[t, k * 16 + j] == 0, (k, j)
+
+
 def test_c2_deterministic_and_entry_points_agree(gpu_device):
     note("C2 determinism + fused vs grouped vs staged entry points (T=1024)")
     inp = synth.make_config("c2", T=1024)
