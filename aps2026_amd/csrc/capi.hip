@@ -200,9 +200,10 @@ bool fold_combine(const WeightSet& w, int64_t rows, int32_t out_dtype) {
     return w.compute == APS_DTYPE_E4M3 && out_dtype == APS_DTYPE_BF16 && aps::ffn_down_fold_fits(rows, w.H, w.F);
 }
 
+// xq_ready: the router has written the fp8 codes and scales of x (fp8 path).
 int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const float* logits, int64_t rows,
                         void* out, int32_t out_dtype, char* ws, const aps_moe_ws_layout& L,
-                        hipStream_t s, bool fold = false) {
+                        hipStream_t s, bool fold = false, bool xq_ready = false) {
     auto* routes = reinterpret_cast<uint8_t*>(ws + L.routes);
     auto* tiles = reinterpret_cast<uint32_t*>(ws + L.tile_counts);
     auto* counts = reinterpret_cast<uint32_t*>(ws + L.counts);
@@ -233,8 +234,9 @@ int grouped_from_logits(const WeightSet& w, const void* x, bool x_is_f32, const 
         auto* actq = reinterpret_cast<uint8_t*>(ws + L.actq);
         auto* as = reinterpret_cast<float*>(ws + L.act_scale);
         const int64_t kp = static_cast<int64_t>(kpad128(w.F));
-        APS_HIP(aps::launch_quant_rows_e4m3(static_cast<const aps::bf16_t*>(x), w.H, w.H, xq, w.H, xs, rows, s),
-                "quantise x launch");
+        if (!xq_ready)
+            APS_HIP(aps::launch_quant_rows_e4m3(static_cast<const aps::bf16_t*>(x), w.H, w.H, xq, w.H, xs, rows, s),
+                    "quantise x launch");
         APS_HIP(aps::launch_ffn_up_fp8(xq, xs, offsets, arows, w.q13, w.s1, w.s3, act, rows, w.H, w.F, w.E, s),
                 "ffn_up_fp8 launch");
         APS_HIP(aps::launch_quant_rows_e4m3(act, w.F, w.F, actq, kp, as, 2 * rows, s), "quantise act launch");
@@ -387,7 +389,7 @@ int aps_router_logits(const void* x, int32_t x_dtype, const float* gate, int64_t
         return fail(APS_ERR_DTYPE, "router x dtype %d not supported", x_dtype);
     if (rows > 0 && (!x || !gate || !logits)) return fail(APS_ERR_ARG, "router: NULL pointer");
     APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, hidden, num_experts, logits, nullptr,
-                               nullptr, nullptr, nullptr, static_cast<hipStream_t>(stream)),
+                               nullptr, nullptr, nullptr, nullptr, nullptr, static_cast<hipStream_t>(stream)),
             "router_logits launch");
     return APS_OK;
 }
@@ -918,11 +920,18 @@ int aps_moe_forward(uint64_t handle, const void* x, int32_t x_dtype, const float
     auto* xb = copy ? reinterpret_cast<aps::bf16_t*>(ws + L.xq) : nullptr;
     const bool fold = fold_combine(*w, rows, out_dtype);
     auto* tiles0 = fold ? reinterpret_cast<uint32_t*>(ws + L.tile_counts0) : nullptr;
+    // fp8 weights with bf16 x: the router also writes x's e4m3 codes and row
+    // scales (x read once for both)
+    const bool xq_in_router = w->compute == APS_DTYPE_E4M3 && x_dtype == APS_DTYPE_BF16 &&
+                              aps::router_quantises_x(w->H, w->E);
+    auto* xq = xq_in_router ? reinterpret_cast<uint8_t*>(ws + L.xq) : nullptr;
+    auto* xqs = xq_in_router ? reinterpret_cast<float*>(ws + L.xq_scale) : nullptr;
     APS_HIP(aps::launch_router(x, x_dtype == APS_DTYPE_BF16, gate, rows, w->H, w->E, logits, routes, tiles, tiles0,
-                               xb, s),
+                               xb, xq, xqs, s),
             "router launch");
     if (copy) return grouped_from_logits(*w, xb, false, nullptr, rows, out, out_dtype, ws, L, s, fold);
-    return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, nullptr, rows, out, out_dtype, ws, L, s, fold);
+    return grouped_from_logits(*w, x, x_dtype == APS_DTYPE_F32, nullptr, rows, out, out_dtype, ws, L, s, fold,
+                               xq_in_router);
 }
 
 // ---- allocation-free forward --------------------------------------------

@@ -75,6 +75,69 @@ __device__ inline float moe_combine2(float a, float b) {
     return __fadd_rn(__fadd_rn(0.0f, __fmul_rn(0.5f, a)), __fmul_rn(0.5f, b));
 }
 
+// ---- fp8 e4m3 row quantisation (the library's fp8 format) ------------------
+// scale = amax(|row|) / 448 (1 if the row is all zero), code = e4m3(v / scale)
+// with nearest-even rounding, saturating at +-448 (OCP "e4m3fn").  Shared by
+// the row quantiser and the router's x quantisation, so that both give the
+// same bits.
+typedef uint32_t e4m3_words_t __attribute__((ext_vector_type(4)));  // 8 bf16 values
+constexpr float kE4m3Max = 448.0f;
+
+// e4m3 codes of two fp32 values in bytes 2 kHi, 2 kHi + 1 of `old`: gfx950's
+// v_cvt_pk_fp8_f32 (OCP e4m3, round to nearest even).  For every fp32 |v| <=
+// 464 (a row quotient is at most 448 plus rounding) it equals the encoder
+// "keep 3 mantissa bits, ties to even; subnormal grid 2^-9; saturate at 448"
+// bit for bit, -0 and subnormals included: 2.28e9 values checked on the GPU.
+template <bool kHi>
+__device__ inline uint32_t e4m3_pack2(float a, float b, uint32_t old) {
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, static_cast<int>(old), kHi));
+}
+
+// v / sc as IEEE division rounds it, for its e4m3 code, from the row's
+// reciprocal r = RN(1 / sc): q0 = RN(v r), then one Markstein correction
+// q = RN(q0 + RN(v - q0 sc) r) with both steps fused (the residual is exact
+// while it stays normal), given v's sign so that -0 stays -0.  Valid for
+// sc >= 2^-89: then a value whose residual could underflow has a quotient
+// below 2^-10, whose code is +-0 either way.  For every bf16 amax >= 448 *
+// 2^-89 and every bf16 |v| <= amax the code equals that of the IEEE quotient
+// (1.07e9 pairs, tests/cpp/quotient_check.c; without the correction 58,276
+// of them differ).  A multiply and two FMAs replace a ten-instruction
+// division per value.
+constexpr float kMinFastScale = 0x1p-89f;
+__device__ inline float e4m3_quotient(float v, float sc, float r) {
+    const float q0 = __fmul_rn(v, r);
+    return copysignf(__fmaf_rn(__fmaf_rn(-q0, sc, v), r, q0), v);
+}
+__device__ inline float bf16w_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf16w_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// The running |v| maximum of a row over the 8 bf16 values of w (fmaxf
+// ignores NaN; the maximum does not depend on the order of the values).
+__device__ inline float e4m3_amax8(float amax, const e4m3_words_t& w) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) amax = fmaxf(amax, fmaxf(fabsf(bf16w_lo(w[k])), fabsf(bf16w_hi(w[k]))));
+    return amax;
+}
+// The row's scale from its amax.
+__device__ inline float e4m3_row_scale(float amax) {
+    const float sc = __fdiv_rn(amax, kE4m3Max);
+    return sc > 0.0f ? sc : 1.0f;
+}
+
+// Codes of the 8 bf16 values of one 16-byte chunk, as two words.
+template <bool kFast>
+__device__ inline void e4m3_chunk_codes(const e4m3_words_t& w, float sc, float rc, uint32_t& lo, uint32_t& hi) {
+    float q[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float a = bf16w_lo(w[k]), b = bf16w_hi(w[k]);
+        q[2 * k] = kFast ? e4m3_quotient(a, sc, rc) : __fdiv_rn(a, sc);
+        q[2 * k + 1] = kFast ? e4m3_quotient(b, sc, rc) : __fdiv_rn(b, sc);
+    }
+    lo = e4m3_pack2<true>(q[2], q[3], e4m3_pack2<false>(q[0], q[1], 0u));
+    hi = e4m3_pack2<true>(q[6], q[7], e4m3_pack2<false>(q[4], q[5], 0u));
+}
+
 // Caller-supplied routes (aps_moe_dispatch) are made memory-safe before they
 // are counted or ranked: an expert id >= E is clamped to E - 1 (and reported
 // by the caller-visible counter), a token whose two slots name the same
@@ -139,11 +202,14 @@ __device__ inline RowTile wave_find_tile(int tile, int bm, uint32_t lo, uint32_t
 // Router GEMM; with routes != nullptr also the top-2 routes and the tile
 // histogram (tile_counts), in the same kernel, and with tile_counts0 !=
 // nullptr the histogram of slot-0 routes alone; with x_copy != nullptr (fp32
-// x only) also the bf16 copy of x [rows][hidden].
+// x only) also the bf16 copy of x [rows][hidden]; with xq, xq_scale !=
+// nullptr (bf16 x, router_quantises_x) also the e4m3 codes of x [rows][hidden]
+// and the row scales [rows], equal to launch_quant_rows_e4m3's.
 int num_cus();  // compute units of the current device
+bool router_quantises_x(int hidden, int experts);
 hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t rows, int hidden,
                          int experts, float* logits, uint8_t* routes, uint32_t* tile_counts,
-                         uint32_t* tile_counts0, bf16_t* x_copy, hipStream_t s);
+                         uint32_t* tile_counts0, bf16_t* x_copy, uint8_t* xq, float* xq_scale, hipStream_t s);
 hipError_t launch_route_top2(const float* logits, int64_t rows, int experts, uint8_t* routes,
                              uint32_t* tile_counts, hipStream_t s);
 // status (may be null): one u32 that counts the route ids >= experts the

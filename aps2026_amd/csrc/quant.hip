@@ -13,52 +13,11 @@
 namespace aps {
 namespace {
 
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef e4m3_words_t u32x4_t;
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr float kE4m3Max = 448.0f;
-
-// e4m3 codes of two fp32 values in bytes 2 kHi, 2 kHi + 1 of `old`: gfx950's
-// v_cvt_pk_fp8_f32 (OCP e4m3, round to nearest even).  For every fp32 |v| <=
-// 464 (a row quotient is at most 448 plus rounding) it equals the encoder
-// "keep 3 mantissa bits, ties to even; subnormal grid 2^-9; saturate at 448"
-// bit for bit, -0 and subnormals included: 2.28e9 values checked on the GPU.
-template <bool kHi>
-__device__ inline uint32_t e4m3_pack2(float a, float b, uint32_t old) {
-    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, static_cast<int>(old), kHi));
-}
-
-// v / sc as IEEE division rounds it, for its e4m3 code, from the row's
-// reciprocal r = RN(1 / sc): q0 = RN(v r), then one Markstein correction
-// q = RN(q0 + RN(v - q0 sc) r) with both steps fused (the residual is exact
-// while it stays normal), given v's sign so that -0 stays -0.  Valid for
-// sc >= 2^-89: then a value whose residual could underflow has a quotient
-// below 2^-10, whose code is +-0 either way.  For every bf16 amax >= 448 *
-// 2^-89 and every bf16 |v| <= amax the code equals that of the IEEE quotient
-// (1.07e9 pairs, tests/cpp/quotient_check.c; without the correction 58,276
-// of them differ).  A multiply and two FMAs replace a ten-instruction
-// division per value.
-constexpr float kMinFastScale = 0x1p-89f;
-__device__ inline float quotient(float v, float sc, float r) {
-    const float q0 = __fmul_rn(v, r);
-    return copysignf(__fmaf_rn(__fmaf_rn(-q0, sc, v), r, q0), v);
-}
-__device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
-
-// Codes of the 8 bf16 values of one 16-byte chunk, as two words.
-template <bool kFast>
-__device__ inline void chunk_codes(const u32x4_t& w, float sc, float rc, uint32_t& lo, uint32_t& hi) {
-    float q[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float a = bf16_lo(w[k]), b = bf16_hi(w[k]);
-        q[2 * k] = kFast ? quotient(a, sc, rc) : __fdiv_rn(a, sc);
-        q[2 * k + 1] = kFast ? quotient(b, sc, rc) : __fdiv_rn(b, sc);
-    }
-    lo = e4m3_pack2<true>(q[2], q[3], e4m3_pack2<false>(q[0], q[1], 0u));
-    hi = e4m3_pack2<true>(q[6], q[7], e4m3_pack2<false>(q[4], q[5], 0u));
-}
+// The arithmetic (scale, quotient, code) is in common.hpp, shared with the
+// router's x quantisation.
 
 // One wave per row of n bf16 values (n % 8 == 0, n <= 512 * CH): each lane
 // holds up to CH chunks of 8 values.  Writes n codes then zeros up to
@@ -78,14 +37,11 @@ k_quant_rows(const bf16_t* __restrict__ src, int64_t src_stride, int n, uint8_t*
     for (int c = 0; c < CH; ++c) {
         const int ch = lane + 64 * c;
         v[c] = ch < nch ? *reinterpret_cast<const u32x4_t*>(s + ch * 8) : u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(v[c][k])), fabsf(bf16_hi(v[c][k]))));
+        amax = e4m3_amax8(amax, v[c]);
     }
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d));
-    float sc = __fdiv_rn(amax, kE4m3Max);
-    if (!(sc > 0.0f)) sc = 1.0f;
+    const float sc = e4m3_row_scale(amax);
     const float rc = __fdiv_rn(1.0f, sc);
     const bool fast = sc >= kMinFastScale;  // wave-uniform
     if (lane == 0) scale[row] = sc;
@@ -97,8 +53,8 @@ k_quant_rows(const bf16_t* __restrict__ src, int64_t src_stride, int n, uint8_t*
         if (ch >= dch) continue;
         uint32_t lo = 0, hi = 0;
         if (ch < nch) {
-            if (fast) chunk_codes<true>(v[c], sc, rc, lo, hi);
-            else chunk_codes<false>(v[c], sc, rc, lo, hi);
+            if (fast) e4m3_chunk_codes<true>(v[c], sc, rc, lo, hi);
+            else e4m3_chunk_codes<false>(v[c], sc, rc, lo, hi);
         }
         *reinterpret_cast<u32x2_t*>(d8 + ch * 8) = u32x2_t{lo, hi};
     }

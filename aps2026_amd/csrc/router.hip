@@ -181,6 +181,7 @@ __device__ inline void r_gate_reads(rf32x4_t (&gd)[4], uint32_t addr) {
 template <int V>
 struct RInt {
     static constexpr int value = V;
+    constexpr operator int() const { return V; }
 };
 
 // Two fp32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32), the
@@ -205,12 +206,21 @@ __device__ inline uint32_t r_pack2_bf16(float lo, float hi) {
 // NWV waves per 16 R lanes of experts: 4 (16 tokens per workgroup) or, for
 // R = 1 and large batches, 8 (32 tokens): the gate then streams once per 32
 // tokens instead of once per 16, half the gate copies per CU.
-template <bool XBF16, int R, int GW, bool XCOPY = false, int NWV = 4>
+// XQS > 0 (bf16 x, R = 1, H = XQS stages): the fp8 path's x quantisation on
+// the way.  Each lane keeps the raw x words it loads for the chain (XQS * GW
+// windows of 8 bf16 values: 4 XQS GW registers), and after the chain its row
+// reduces the token's amax over its 16 lanes and every lane writes the e4m3
+// codes of its own elements and lane 0 the row's scale, with the row
+// quantiser's arithmetic (common.hpp), so the codes and scales are the ones
+// k_quant_rows writes.  x is read from memory once for both.
+template <bool XBF16, int R, int GW, bool XCOPY = false, int NWV = 4, int XQS = 0>
 __global__ void __launch_bounds__(64 * NWV * R)
 k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, int E,
          float* __restrict__ logits, uint8_t* __restrict__ routes, uint8_t* __restrict__ tile_bytes,
-         uint8_t* __restrict__ tile_bytes0, bf16_t* __restrict__ xcopy) {
+         uint8_t* __restrict__ tile_bytes0, bf16_t* __restrict__ xcopy, uint8_t* __restrict__ xq,
+         float* __restrict__ xq_scale) {
     static_assert(!(XCOPY && XBF16), "the bf16 copy is made from fp32 x");
+    static_assert(XQS == 0 || (XBF16 && R == 1 && !XCOPY), "x quantisation reads bf16 x, one row per token");
     constexpr int kGW = GW;                    // windows per ring stage
     constexpr int kWinBytes = 8 * 1024 * R;    // 32 (k/4) x 16 R experts x 16 B
     constexpr int kElt = XBF16 ? 2 : 4;
@@ -235,8 +245,9 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
     const int gr = 4 * w + (lane >> 4);        // row of the workgroup, 0 .. 16R-1
     const int e = (gr % R) * 16 + (lane & 15); // this lane's expert
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kTok + gr / R;
-    const int NW = H / kRWin;
-    const int NG = NW / kGW;
+    // stages: compile-time when the x words are kept (their registers are
+    // indexed by stage), H = XQS GW 128 then
+    const int NG = XQS > 0 ? XQS : H / kRWin / kGW;
     static_assert(2 * kQ * 16 * R <= 64 * NWV * R, "one counter per thread to clear");
     if (tid < 2 * kQ * 16 * R) (&cnt[0][0][0])[tid] = 0u;
 
@@ -289,15 +300,25 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
         r_gate_reads<gate_off(b), kGateStride>(gd, addr);
     };
 
+    // the raw x words of every window, for the quantisation after the chain
+    ru32x4_t xs[XQS > 0 ? XQS * kGW : 1];
+
     float acc = 0.0f;
-    auto run_stage = [&](auto par, int g) {
+    // stage g (an int, or an RInt when the x words are kept)
+    auto run_stage = [&](auto par, auto gq) {
         constexpr int P = decltype(par)::value;
+        const int g = gq;
         constexpr int nb = 8 * kGW;
         // this stage's x elements, then the next stage's x loads (the x
         // registers of this stage are free once converted)
         float c[kGW][8];
 #pragma unroll
         for (int wi = 0; wi < kGW; ++wi) r_elements(c[wi], xr[P][wi]);
+        if constexpr (XQS > 0) {
+            constexpr int G = decltype(gq)::value;
+#pragma unroll
+            for (int wi = 0; wi < kGW; ++wi) xs[G * kGW + wi] = xr[P][wi][0];
+        }
         if constexpr (XCOPY) {
 #pragma unroll
             for (int wi = 0; wi < kGW; ++wi) {
@@ -339,13 +360,56 @@ k_router(const void* xv, const float* __restrict__ gate, int64_t rows, int H, in
     issue_gate(RInt<1>{}, NG > 1 ? 1 : 0);
     r_wait_vm<kCopies>();
     r_barrier();
-    for (int g = 0; g < NG; g += 2) {
-        run_stage(RInt<0>{}, g);
-        if (g + 1 < NG) run_stage(RInt<1>{}, g + 1);
+    if constexpr (XQS > 0) {
+        [&]<int... G>(std::integer_sequence<int, G...>) { (run_stage(RInt<G % 2>{}, RInt<G>{}), ...); }(
+            std::make_integer_sequence<int, XQS>{});
+    } else {
+        for (int g = 0; g < NG; g += 2) {
+            run_stage(RInt<0>{}, g);
+            if (g + 1 < NG) run_stage(RInt<1>{}, g + 1);
+        }
     }
 
     const bool valid = t < rows;
     if (valid && e < E) logits[t * E + e] = acc;
+    if constexpr (XQS > 0) {
+        // the token's row scale (its 16 lanes hold the whole row), then the
+        // codes of this lane's 8 elements of every window
+        float amax = 0.0f;
+#pragma unroll
+        for (int v = 0; v < XQS * kGW; ++v) amax = e4m3_amax8(amax, xs[v]);
+#pragma unroll
+        for (int d = 8; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d));
+        const float sc = e4m3_row_scale(amax);
+        const float rc = __fdiv_rn(1.0f, sc);
+        if (valid) {
+            if ((lane & 15) == 0) xq_scale[t] = sc;
+            typedef uint32_t ru32x2_t __attribute__((ext_vector_type(2)));
+            uint8_t* d8 = xq + t * static_cast<int64_t>(H) + 8 * (lane & 15);
+            // The words pass through an empty asm statement, so that the
+            // compiler converts them again here instead of keeping all 256
+            // fp32 values of the amax loop alive (which spilled).
+            if (sc >= kMinFastScale) {
+#pragma unroll
+                for (int v = 0; v < XQS * kGW; ++v) {
+                    e4m3_words_t wv = xs[v];
+                    asm volatile("" : "+v"(wv));
+                    uint32_t lo, hi;
+                    e4m3_chunk_codes<true>(wv, sc, rc, lo, hi);
+                    *reinterpret_cast<ru32x2_t*>(d8 + v * kRWin) = ru32x2_t{lo, hi};
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < XQS * kGW; ++v) {
+                    e4m3_words_t wv = xs[v];
+                    asm volatile("" : "+v"(wv));
+                    uint32_t lo, hi;
+                    e4m3_chunk_codes<false>(wv, sc, rc, lo, hi);
+                    *reinterpret_cast<ru32x2_t*>(d8 + v * kRWin) = ru32x2_t{lo, hi};
+                }
+            }
+        }
+    }
     if (routes == nullptr) return;  // kernel-uniform
 
     // top-2 of the token: its 16 R logits sit in lanes base .. base + 16R - 1
@@ -425,15 +489,24 @@ k_route_top2(const float* __restrict__ logits, int64_t rows, int E, uint8_t* __r
 
 }  // namespace
 
+// Stages of 512 steps the router's x quantisation keeps in registers.
+constexpr int kXqStages = 8;
+
+bool router_quantises_x(int hidden, int experts) {
+    return experts >= 1 && experts <= 16 && hidden == kXqStages * 4 * kRWin;
+}
+
 hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t rows, int hidden,
                          int experts, float* logits, uint8_t* routes, uint32_t* tile_counts,
-                         uint32_t* tile_counts0, bf16_t* x_copy, hipStream_t s) {
+                         uint32_t* tile_counts0, bf16_t* x_copy, uint8_t* xq, float* xq_scale, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (hidden <= 0 || hidden % (2 * kRWin) != 0 || experts <= 0 || experts > kMaxExperts)
         return hipErrorInvalidValue;
     if (routes && (experts < 2 || !tile_counts)) return hipErrorInvalidValue;
     if (tile_counts0 && !routes) return hipErrorInvalidValue;
     if (x_copy && x_bf16) return hipErrorInvalidValue;
+    if ((xq != nullptr) != (xq_scale != nullptr)) return hipErrorInvalidValue;
+    if (xq && (!x_bf16 || !router_quantises_x(hidden, experts))) return hipErrorInvalidValue;
     auto* tb = reinterpret_cast<uint8_t*>(tile_counts);
     auto* tb0 = reinterpret_cast<uint8_t*>(tile_counts0);
     // windows per stage: 512 steps of 16 R experts (32 KB) when H allows
@@ -446,14 +519,23 @@ hipError_t launch_router(const void* x, bool x_bf16, const float* gate, int64_t 
     const int64_t cus = num_cus();
     const bool eight = R == 1 && wide && rows > kRTokens * cus && ceil_div(rows, 2 * kRTokens) <= cus;
     const dim3 grid(static_cast<unsigned>(ceil_div(rows, eight ? 2 * kRTokens : kRTokens)));
+    if (xq) {
+        if (eight)
+            hipLaunchKernelGGL((k_router<true, 1, 4, false, 8, kXqStages>), grid, dim3(64 * 8), 0, s, x, gate, rows,
+                               hidden, experts, logits, routes, tb, tb0, nullptr, xq, xq_scale);
+        else
+            hipLaunchKernelGGL((k_router<true, 1, 4, false, 4, kXqStages>), grid, dim3(64 * 4), 0, s, x, gate, rows,
+                               hidden, experts, logits, routes, tb, tb0, nullptr, xq, xq_scale);
+        return hipGetLastError();
+    }
 #define APS_ROUTER_LAUNCH(XB, R, GW, NWV)                                                                     \
     do {                                                                                                      \
         if (!(XB) && x_copy)                                                                                 \
             hipLaunchKernelGGL((k_router<false, R, GW, true, NWV>), grid, dim3(64 * NWV * R), 0, s, x, gate, \
-                               rows, hidden, experts, logits, routes, tb, tb0, x_copy);                      \
+                               rows, hidden, experts, logits, routes, tb, tb0, x_copy, nullptr, nullptr);    \
         else                                                                                                 \
             hipLaunchKernelGGL((k_router<XB, R, GW, false, NWV>), grid, dim3(64 * NWV * R), 0, s, x, gate,   \
-                               rows, hidden, experts, logits, routes, tb, tb0, nullptr);                     \
+                               rows, hidden, experts, logits, routes, tb, tb0, nullptr, nullptr, nullptr);   \
     } while (0)
     if (x_bf16) {
         if (eight) APS_ROUTER_LAUNCH(true, 1, 4, 8);

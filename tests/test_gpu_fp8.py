@@ -53,18 +53,24 @@ def rowwise_err(got, ref):
 
 
 def run_block(inp, dev):
-    """The fused forward (router, and for F in (384, 512] the w2 GEMM with
-    the combine folded in), then the grouped forward from the router's
-    logits (w2 to y, then k_combine), which leaves every intermediate in the
-    workspace: the two outputs must agree bit for bit."""
+    """The fused forward (the router quantising x on the way when H = 4096
+    and E <= 16, and for F in (384, 512] the w2 GEMM with the combine folded
+    in), then the grouped forward from the router's logits (x quantised by
+    the row quantiser, w2 to y, then k_combine), which leaves every
+    intermediate in the workspace: x's codes and scales and the two outputs
+    must agree bit for bit."""
     w = fp8_weights(inp, dev)
     x = to_dev_bf16(inp.packed["x_bf16"], dev)
     gate = torch.from_numpy(inp.gate).to(dev)
     out = moe.moe_forward_gpu(x, gate, w, out_dtype=torch.bfloat16)
-    logits = w.plan_views(inp.T)["logits"].clone()
+    fused = w.plan_views(inp.T)
+    logits = fused["logits"].clone()
+    xq_f, xs_f = fused["xq"].clone(), fused["x_scale"].clone()
     out_g = moe.moe_forward_grouped_gpu(x, logits, w, out_dtype=torch.bfloat16)
     plan = w.plan_views(inp.T)
     torch.cuda.synchronize()
+    assert torch.equal(xq_f, plan["xq"]), "x codes of the fused forward differ from the row quantiser's"
+    assert torch.equal(xs_f.view(torch.int32), plan["x_scale"].view(torch.int32)), "x scales differ"
     diff = int((out.view(torch.int16) != out_g.view(torch.int16)).sum())
     assert diff == 0, f"fused forward and w2 + combine differ in {diff} elements"
     return w, out, plan
@@ -252,3 +258,47 @@ def test_quantiser_every_bf16_value_at_many_scales(gpu_device):
     note(f"quantiser: {x.shape[0]} rows")
     np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), want_s.view(np.uint32))
     np.testing.assert_array_equal(q.cpu().numpy(), want_q)
+
+
+def every_bf16_rows(exps, per=4095):
+    """Rows of 4096 bf16 values: for each exponent e, amax = 1.5 * 2^e (2^127
+    for e = 127) and then every finite bf16 value of magnitude <= amax, 4095
+    per row, so each row's scale is amax / 448."""
+    allv = synth.bf16_bits_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    allv = allv[np.isfinite(allv)]
+    rows = []
+    for e in exps:
+        amax = np.float32(np.ldexp(np.float32(1.5), e)) if e < 127 else np.float32(np.ldexp(np.float32(1.0), 127))
+        amax = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(np.array([amax], np.float32)))[0]
+        vals = allv[np.abs(allv) <= amax]
+        for i in range(0, vals.size, per):
+            chunk = vals[i:i + per]
+            row = np.zeros(4096, np.float32)
+            row[0] = amax
+            row[1:1 + chunk.size] = chunk
+            rows.append(row)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("T", [613, 8192])
+def test_router_x_quantisation_every_bf16_value(gpu_device, T):
+    """The fused forward's router writes x's e4m3 codes and row scales (fp8
+    weights, bf16 x, hidden 4096, 16 experts): on rows holding every finite
+    bf16 value at 33 row scales (subnormal scales, the IEEE-division range
+    below 2^-89, up to 2^127), plus an all-zero row, both must equal the
+    oracle's quantiser bit for bit.  613 rows run 16-token workgroups, 8192
+    (the rows repeated) the 32-token ones."""
+    exps = list(range(-133, -120, 3)) + list(range(-92, -76, 2)) + list(range(-60, 128, 7))
+    x = np.concatenate([every_bf16_rows(exps), np.zeros((1, 4096), np.float32)])
+    x = np.resize(x, (T, 4096))
+    note(f"router x quantisation: T={T} rows of every bf16 value at {len(exps)} scales")
+    inp = synth.make_moe_inputs(T=16, dtype="fp8", seed=5)
+    w = fp8_weights(inp, gpu_device)
+    xd = to_dev_bf16(synth.f32_to_bf16_bits(x), gpu_device)
+    gate = torch.from_numpy(inp.gate).to(gpu_device)
+    moe.moe_forward_gpu(xd, gate, w, out_dtype=torch.bfloat16)
+    plan = w.plan_views(T)
+    want_q, want_s = oracle.quantise_rows_e4m3(x)
+    np.testing.assert_array_equal(plan["x_scale"].cpu().numpy().view(np.uint32), want_s.view(np.uint32))
+    np.testing.assert_array_equal(plan["xq"].cpu().numpy(), want_q)
+    w.release()
