@@ -100,8 +100,6 @@ void matmul_transposed_gpu(const Tensor& a, const Tensor& b, Tensor& c) {
         if (rc) throw_status(rc, "matmul_transposed_gpu");
         return;
     }
-    if (k % 16 != 0 || n % 4 != 0)
-        throw std::invalid_argument("matmul_transposed_gpu: this build needs k % 16 == 0 and n % 4 == 0");
     const int rc = aps_linear(da, db, nullptr, static_cast<int64_t>(m), static_cast<int32_t>(k),
                               static_cast<int32_t>(n), c.cuda_data_write(), nullptr);
     if (rc) throw_status(rc, "matmul_transposed_gpu");
@@ -117,8 +115,6 @@ void matmul_transposed_bias_gpu(const Tensor& a, const Tensor& b, const Tensor& 
         linear_tc(a.cuda_data(), b, bias.cuda_data(), m, k, n, c.cuda_data_write(), "matmul_transposed_bias_gpu");
         return;
     }
-    if (k % 16 != 0 || n % 4 != 0)
-        throw std::invalid_argument("matmul_transposed_bias_gpu: this build needs k % 16 == 0 and n % 4 == 0");
     const int rc = aps_linear(a.cuda_data(), b.cuda_data(), bias.cuda_data(), static_cast<int64_t>(m),
                               static_cast<int32_t>(k), static_cast<int32_t>(n), c.cuda_data_write(), nullptr);
     if (rc) throw_status(rc, "matmul_transposed_bias_gpu");
@@ -529,8 +525,13 @@ void matmul_pair_bias_gpu(const Tensor& a, const Tensor& first_weight, const Ten
         matmul_transposed_bias_gpu(a, second_weight, second_bias, second_out);
         return;
     }
-    if (k % 16 != 0 || n % 4 != 0)
-        throw std::invalid_argument("matmul_pair_bias_gpu: this build needs k % 16 == 0 and n % 4 == 0");
+    if (k % 16 != 0 || n % 4 != 0) {
+        // shapes the one-grid kernel does not take: each output on its own
+        // (aps_linear's general kernel, the same chains)
+        matmul_transposed_bias_gpu(a, first_weight, first_bias, first_out);
+        matmul_transposed_bias_gpu(a, second_weight, second_bias, second_out);
+        return;
+    }
     // both outputs in one grid (their column blocks share it)
     const float* ws[2] = {first_weight.cuda_data(), second_weight.cuda_data()};
     const float* bs[2] = {first_bias.cuda_data(), second_bias.cuda_data()};
@@ -630,7 +631,9 @@ void apply_rope_gpu(Tensor& q, Tensor& k, const std::vector<std::size_t>& seq_le
 void attention_gpu(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out,
                    const std::vector<std::size_t>& seq_lens, std::size_t q_heads, std::size_t kv_heads,
                    std::size_t head_dim) {
-    if (q_heads != 4 * kv_heads) throw std::invalid_argument("attention_gpu expects GQA-4");
+    // GQA-4 takes the grouped kernel, other layouts the generic one (as the
+    // reference's attention_gpu, src/tensor.cu:3316-3340)
+    if (kv_heads == 0 || q_heads % kv_heads != 0) throw std::invalid_argument("attention_gpu shape");
     const std::size_t rows = head_dim && q_heads ? q.size() / (q_heads * head_dim) : 0;
     if (q.size() != rows * q_heads * head_dim || k.size() != rows * kv_heads * head_dim || v.size() != k.size() ||
         out.size() != q.size())

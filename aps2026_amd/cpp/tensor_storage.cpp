@@ -161,6 +161,15 @@ void Tensor::prepare_cuda_bf16_weight(bool with_low_residual) const {
         device_call(hipMemsetAsync(static_cast<char*>(p) + bytes / 2, 0, bytes / 2, nullptr), "hipMemsetAsync BF16 lo");
     bf16_ = p;
     bf16_bytes_ = bytes;
+    // As the reference (src/tensor.cu:168-175), the fp32 device copy goes once
+    // packed: the matmuls read the bf16 images, and a later cuda_data() uploads
+    // the host copy again.  The free is queued after the packing on the same
+    // stream.  A weight whose only current copy is on the device keeps it.
+    if ((fresh_ & kOnHost) && dev_) {
+        device_call(hipFreeAsync(dev_, nullptr), "hipFreeAsync packed FP32 weight");
+        dev_ = nullptr;
+        fresh_ &= ~kOnDevice;
+    }
 }
 
 float* Tensor::data() { return host_for_write(); }

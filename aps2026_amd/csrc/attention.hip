@@ -514,6 +514,82 @@ k_attention_tree(const float* __restrict__ q, const float* __restrict__ k, const
     orow[kHeadDim] = o1;
 }
 
+// Packed-sequence attention for head layouts other than GQA-4 (reference
+// k_attention, src/tensor.cu:2209-2274, launched by attention_gpu,
+// :3316-3340, when q_heads != 4 kv_heads).  One 128-thread workgroup per
+// (row, query head); the arithmetic is the reference kernel's:
+//   s_w = (fma chain over d ascending of q[d] k_w[d], from +0) * scale
+//   m = max_w s_w;  e_w = (float)exp((double)(s_w - m));
+//   den = fp32 sum of e_w, w ascending (one lane);  p_w = e_w / den
+//   out[d] = fma chain over w ascending of p_w v_w[d]
+// The scores and exps of different keys are independent, so threads take
+// keys w = tid, tid + 128, ...; only the denominator is a serial sum.  Keys
+// are the rows seg_offset[row] + begin .. seg_offset[row] + pos of the row's
+// own sequence, begin = max(0, pos + 1 - window).  Dynamic LDS: wmax scores.
+constexpr int kAnyThreads = 128;
+
+__global__ void __launch_bounds__(kAnyThreads)
+k_attention_any(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+                float* __restrict__ out, const uint32_t* __restrict__ seg_offset, const uint32_t* __restrict__ seg_pos,
+                int64_t rows, int q_heads, int kv_heads, int head_dim, int64_t max_seq, int wmax, float scale) {
+    extern __shared__ float sc[];
+    __shared__ float qs[kAnyThreads];
+    __shared__ float red[kAnyThreads / kWave];
+    __shared__ float den_s;
+    const int tid = threadIdx.x;
+    const int64_t task = blockIdx.x;
+    const int64_t row = task / q_heads;
+    const int qh = static_cast<int>(task % q_heads);
+    const int kh = qh / (q_heads / kv_heads);
+    // positions and segment starts clamped for memory safety only (the C++
+    // layer builds them from the sequence lengths)
+    int64_t pos = seg_pos[row];
+    pos = pos < max_seq ? pos : max_seq - 1;
+    const int64_t begin = pos + 1 > wmax ? pos + 1 - wmax : 0;
+    const int window = static_cast<int>(pos - begin + 1);
+    const int64_t first = static_cast<int64_t>(seg_offset[row]) + begin;
+    auto key_row = [&](int w) {
+        const int64_t r = first + w;
+        return r < rows ? r : rows - 1;
+    };
+    const float* qrow = q + (row * q_heads + qh) * static_cast<int64_t>(head_dim);
+    if (tid < head_dim) qs[tid] = qrow[tid];
+    __syncthreads();
+    float m = -3.402823466e+38F;
+    for (int w = tid; w < window; w += kAnyThreads) {
+        const float* kr = k + (key_row(w) * kv_heads + kh) * static_cast<int64_t>(head_dim);
+        float a = 0.0f;
+        for (int d = 0; d < head_dim; ++d) a = __fmaf_rn(qs[d], kr[d], a);
+        const float sw = __fmul_rn(a, scale);
+        sc[w] = sw;
+        m = fmaxf(m, sw);
+    }
+    // the window's maximum (order-independent)
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(red[0], red[1]);
+    for (int w = tid; w < window; w += kAnyThreads)
+        sc[w] = static_cast<float>(exp(static_cast<double>(__fsub_rn(sc[w], m))));
+    __syncthreads();
+    if (tid == 0) {
+        float den = 0.0f;
+        for (int w = 0; w < window; ++w) den = __fadd_rn(den, sc[w]);
+        den_s = den;
+    }
+    __syncthreads();
+    const float den = den_s;
+    for (int w = tid; w < window; w += kAnyThreads) sc[w] = __fdiv_rn(sc[w], den);
+    __syncthreads();
+    if (tid < head_dim) {
+        float o = 0.0f;
+        for (int w = 0; w < window; ++w)
+            o = __fmaf_rn(sc[w], v[(key_row(w) * kv_heads + kh) * static_cast<int64_t>(head_dim) + tid], o);
+        out[(row * q_heads + qh) * static_cast<int64_t>(head_dim) + tid] = o;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_rope_tree(float* x, const uint32_t* row_pos, int64_t rows, int heads, int head_dim,
@@ -575,6 +651,29 @@ hipError_t launch_attention_tree(const float* q, const float* k, const float* v,
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(rows * kv_heads)), dim3(kAttnThreads), lds, s, q, k, v, out,
                        row_pos, anc, anc_stride, rows, q_heads, kv_heads, wmax, scale,
                        group ? static_cast<int>(span) : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_any(const float* q, const float* k, const float* v, float* out, const uint32_t* seg_offset,
+                                const uint32_t* seg_pos, int64_t max_seq, int64_t rows, int q_heads, int kv_heads,
+                                int head_dim, int window_max, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0 || head_dim <= 0 || head_dim > kAnyThreads ||
+        max_seq <= 0 || window_max <= 0 || rows * q_heads > 0x7FFFFFFFll)
+        return hipErrorInvalidValue;
+    const int64_t keys = max_seq < window_max ? max_seq : window_max;
+    if (keys > kAttnMaxWindow) return hipErrorInvalidValue;
+    const int wmax = static_cast<int>(keys);
+    const size_t lds = static_cast<size_t>(wmax) * sizeof(float);
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention_any),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return e;
+    }
+    const float root = sqrtf(static_cast<float>(head_dim));
+    const float scale = 1.0f / root;
+    hipLaunchKernelGGL(k_attention_any, dim3(static_cast<unsigned>(rows * q_heads)), dim3(kAnyThreads), lds, s, q, k,
+                       v, out, seg_offset, seg_pos, rows, q_heads, kv_heads, head_dim, max_seq, wmax, scale);
     return hipGetLastError();
 }
 

@@ -611,20 +611,23 @@ int aps_prefix_ancestors(const uint32_t* node_parent, const uint32_t* node_depth
 
 int aps_linear(const float* x, const float* weight, const float* bias, int64_t rows, int32_t in_features,
                int32_t out_features, float* y, void* stream) {
-    if (rows < 0 || in_features <= 0 || out_features <= 0 || in_features % 16 != 0 || out_features % 4 != 0 ||
-        (rows + 63) / 64 > 65535)
-        return fail(APS_ERR_SHAPE,
-                    "linear shape: rows %lld in %d (multiple of 16) out %d (multiple of 4)", (long long)rows,
-                    in_features, out_features);
+    if (rows < 0 || in_features <= 0 || out_features <= 0)
+        return fail(APS_ERR_SHAPE, "linear shape: rows %lld in %d out %d", (long long)rows, in_features,
+                    out_features);
     if (rows == 0) return APS_OK;
     if (!x || !weight || !y) return fail(APS_ERR_ARG, "linear: NULL pointer");
-    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
-          reinterpret_cast<uintptr_t>(y)) & 15u) != 0)
-        return fail(APS_ERR_ARG, "linear: arrays must be 16-byte aligned");
+    const uintptr_t addr_bits = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+                                reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(y);
+    if ((addr_bits & 3u) != 0) return fail(APS_ERR_ARG, "linear: arrays must be 4-byte aligned");
     if (y == x) return fail(APS_ERR_ARG, "linear: y must not alias x");
-    APS_HIP(aps::launch_linear_f32(x, weight, bias, y, rows, in_features, out_features,
-                                   static_cast<hipStream_t>(stream)),
-            "linear launch");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    // in % 16, out % 4 and 16-byte alignment take the vector / matrix-core
+    // kernels; any other shape the SIMT kernel (same chains, same bits)
+    if (in_features % 16 == 0 && out_features % 4 == 0 && (addr_bits & 15u) == 0 && (rows + 63) / 64 <= 65535)
+        APS_HIP(aps::launch_linear_f32(x, weight, bias, y, rows, in_features, out_features, s), "linear launch");
+    else
+        APS_HIP(aps::launch_linear_any_f32(x, weight, bias, y, rows, in_features, out_features, s),
+                "linear launch");
     return APS_OK;
 }
 
@@ -812,7 +815,25 @@ int aps_attention_tree(const float* q, const float* k, const float* v, float* ou
 int aps_attention_packed(const float* q, const float* k, const float* v, float* out, const uint32_t* seg_offset,
                          const uint32_t* seg_pos, int64_t max_seq, int64_t rows, int32_t q_heads, int32_t kv_heads,
                          int32_t head_dim, int32_t window, void* stream) {
-    if (kv_heads <= 0 || q_heads != 4 * kv_heads) return fail(APS_ERR_SHAPE, "attention_gpu expects GQA-4");
+    if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0)
+        return fail(APS_ERR_SHAPE, "attention heads: %d query heads over %d KV heads", q_heads, kv_heads);
+    if (q_heads != 4 * kv_heads) {
+        // other head layouts: the reference's generic kernel (k_attention)
+        if (rows < 0 || head_dim <= 0 || head_dim > 128 || max_seq <= 0 || window <= 0)
+            return fail(APS_ERR_SHAPE, "attention shape: rows %lld head_dim %d (1..128) max_seq %lld window %d",
+                        (long long)rows, head_dim, (long long)max_seq, window);
+        if ((max_seq < window ? max_seq : window) > aps::kAttnMaxWindow)
+            return fail(APS_ERR_SHAPE, "attention: a window of %lld keys exceeds the %d that fit in LDS",
+                        (long long)(max_seq < window ? max_seq : window), aps::kAttnMaxWindow);
+        if (rows * q_heads > 0x7FFFFFFFll)
+            return fail(APS_ERR_SHAPE, "attention: %lld rows x %d heads", (long long)rows, q_heads);
+        if (rows == 0) return APS_OK;
+        if (!q || !k || !v || !out || !seg_offset || !seg_pos) return fail(APS_ERR_ARG, "attention: NULL pointer");
+        APS_HIP(aps::launch_attention_any(q, k, v, out, seg_offset, seg_pos, max_seq, rows, q_heads, kv_heads,
+                                          head_dim, window, static_cast<hipStream_t>(stream)),
+                "attention launch");
+        return APS_OK;
+    }
     if (rows < 0 || head_dim != 128 || max_seq <= 0 || window <= 0)
         return fail(APS_ERR_SHAPE, "attention shape: rows %lld head_dim %d (128 only) max_seq %lld window %d",
                     (long long)rows, head_dim, (long long)max_seq, window);

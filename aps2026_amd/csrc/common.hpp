@@ -246,6 +246,11 @@ constexpr int kAttnMaxWindow = 7936;
 hipError_t launch_attention_tree(const float* q, const float* k, const float* v, float* out, const uint32_t* row_pos,
                                  const uint32_t* anc, int64_t anc_stride, int64_t rows, int q_heads, int kv_heads,
                                  int head_dim, int window_max, bool packed, hipStream_t s);
+// Packed-sequence attention for any head layout (q_heads % kv_heads == 0,
+// head_dim <= 128): the reference's generic kernel's arithmetic.
+hipError_t launch_attention_any(const float* q, const float* k, const float* v, float* out, const uint32_t* seg_offset,
+                                const uint32_t* seg_pos, int64_t max_seq, int64_t rows, int q_heads, int kv_heads,
+                                int head_dim, int window_max, hipStream_t s);
 
 // Elementwise fp32 ops (reference k_add, k_add_bias, k_silu_mul, zero_gpu).
 hipError_t launch_add_inplace(float* a, const float* b, int64_t n, hipStream_t s);
@@ -278,6 +283,9 @@ hipError_t launch_linear_mfma_multi(const float* x, int64_t rows, int in_f, int 
                                     const float* const* bias, float* const* y, const int* out_f, hipStream_t s);
 hipError_t launch_linear_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows, int in_f,
                              int out_f, hipStream_t s);
+// the same chains for any in_f, out_f and 4-byte alignment (SIMT, scalar loads)
+hipError_t launch_linear_any_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows, int in_f,
+                                 int out_f, hipStream_t s);
 
 hipError_t launch_layer_norm(float* x, const float* residual, const float* weight, const float* bias, float* y,
                              int64_t rows, int hidden, float eps, hipStream_t s);

@@ -220,6 +220,75 @@ k_linear_f32(const float* __restrict__ x, const float* __restrict__ w, const flo
     }
 }
 
+// The same product for any K, N and alignment (the reference's fallback for
+// shapes its fast kernels do not take, k_matmul_transposed_tiled,
+// src/tensor.cu:433-461): scalar loads, k past K read as zero.  A padded step
+// adds the exact product 0 * 0 to an accumulator that is never -0 (it starts
+// at +0, and a sum that cancels exactly rounds to +0), so it changes no bit:
+// every output is the chain over k = 0 .. K-1.  Row tiles are walked
+// grid-stride over gridDim.y.
+__global__ void __launch_bounds__(256)
+k_linear_any(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
+             float* __restrict__ y, int64_t M, int K, int N) {
+    __shared__ float As[kBK][kF32BM + 1];
+    __shared__ float Bs[kBK][kF32BN + 1];
+    const int n0 = blockIdx.x * kF32BN;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int sr = tid >> 2, sk = (tid & 3) * 4;
+    const bool b_ok = n0 + sr < N;
+    const float* b_src = w + static_cast<int64_t>(b_ok ? n0 + sr : 0) * K;
+    for (int64_t m0 = static_cast<int64_t>(blockIdx.y) * kF32BM; m0 < M;
+         m0 += static_cast<int64_t>(gridDim.y) * kF32BM) {
+        const bool a_ok = m0 + sr < M;
+        const float* a_src = x + (a_ok ? m0 + sr : 0) * static_cast<int64_t>(K);
+        float acc[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[r][c] = 0.0f;
+        for (int k0 = 0; k0 < K; k0 += kBK) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int k = k0 + sk + i;
+                av[i] = a_ok && k < K ? a_src[k] : 0.0f;
+                bv[i] = b_ok && k < K ? b_src[k] : 0.0f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                As[sk + i][sr] = av[i];
+                Bs[sk + i][sr] = bv[i];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int kk = 0; kk < kBK; ++kk) {
+                float ar[4], br[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    ar[i] = As[kk][ty * 4 + i];
+                    br[i] = Bs[kk][tx * 4 + i];
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[r][c] = __builtin_fmaf(ar[r], br[c], acc[r][c]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + ty * 4 + r;
+            if (row >= M) continue;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int col = n0 + tx * 4 + c;
+                if (col >= N) continue;
+                y[row * N + col] = bias ? __fadd_rn(acc[r][c], bias[col]) : acc[r][c];
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_linear_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows, int in_f,
@@ -233,6 +302,16 @@ hipError_t launch_linear_f32(const float* x, const float* w, const float* bias, 
     if (ty > 65535) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>(ceil_div(out_f, kF32BN)), static_cast<unsigned>(ty));
     hipLaunchKernelGGL(k_linear_f32, grid, dim3(256), 0, s, x, w, bias, y, rows, in_f, out_f);
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_any_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows, int in_f,
+                                 int out_f, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (in_f <= 0 || out_f <= 0) return hipErrorInvalidValue;
+    const int64_t ty = ceil_div(rows, kF32BM);
+    const dim3 grid(static_cast<unsigned>(ceil_div(out_f, kF32BN)), static_cast<unsigned>(ty < 65535 ? ty : 65535));
+    hipLaunchKernelGGL(k_linear_any, grid, dim3(256), 0, s, x, w, bias, y, rows, in_f, out_f);
     return hipGetLastError();
 }
 

@@ -346,8 +346,11 @@ APS_API int aps_prefix_ancestors(const uint32_t* node_parent, const uint32_t* no
  * 3034-3143, kernel k_matmul_transposed_8x8 :715-800): y [rows][out] =
  * x [rows][in] . weight [out][in]^T, each output one fp32 FMA chain over k
  * ascending, then + bias[out] when bias is not NULL (the decoder's q/k/v/o
- * projections).  in % 16 == 0, out % 4 == 0, arrays 16-byte aligned, y not
- * aliasing x. */
+ * projections).  Any in and out (the reference's k_matmul_transposed_tiled
+ * fallback, :433-461, serves the shapes its fast kernels do not): in % 16 ==
+ * 0, out % 4 == 0 with 16-byte aligned arrays run the vector / matrix-core
+ * kernels, other shapes a SIMT kernel with the same chains.  Arrays 4-byte
+ * aligned, y not aliasing x. */
 APS_API int aps_linear(const float* x, const float* weight, const float* bias, int64_t rows, int32_t in_features,
                        int32_t out_features, float* y, void* stream);
 /* Replaces tensor_ops::matmul_pair_bias_gpu (reference include/tensor.h:
@@ -431,7 +434,7 @@ APS_API int aps_attention_tree(const float* q, const float* k, const float* v, f
                                const uint32_t* anc, int64_t anc_stride, int64_t rows, int32_t q_heads,
                                int32_t kv_heads, int32_t head_dim, int32_t window, void* stream);
 
-/* Replaces tensor_ops::attention_gpu's GQA-4 path (reference include/tensor.h:
+/* Replaces tensor_ops::attention_gpu (reference include/tensor.h:
  * 95-98, src/tensor.cu:3318-3340, kernel k_attention_grouped_gqa4
  * :2267-2405): the same attention and arithmetic as aps_attention_tree, over
  * packed token sequences instead of trie nodes (and with its precondition
@@ -439,10 +442,12 @@ APS_API int aps_attention_tree(const float* q, const float* k, const float* v, f
  * starts at row seg_offset[r] sits at position seg_pos[r] in it, and its
  * keys are rows seg_offset[r] + begin .. seg_offset[r] + seg_pos[r] (begin =
  * max(0, pos + 1 - window)).  max_seq bounds every segment length (the
- * reference's PackedMeta::max_seq).  q_heads = 4 kv_heads ("attention_gpu
- * expects GQA-4": the reference's fallback kernel for other ratios,
- * k_attention, is not provided); head_dim 128; k 16-byte aligned.  RoPE of
- * packed rows is aps_rope_tree with row_pos = seg_pos. */
+ * reference's PackedMeta::max_seq).  q_heads = 4 kv_heads takes the grouped
+ * kernel (head_dim 128, k 16-byte aligned); any other layout with q_heads a
+ * multiple of kv_heads and head_dim <= 128 the reference's generic kernel's
+ * arithmetic (k_attention, :2209-2274: each score one fma chain over d, the
+ * same softmax and value chains; any v, no finiteness precondition).  RoPE
+ * of packed rows is aps_rope_tree with row_pos = seg_pos. */
 APS_API int aps_attention_packed(const float* q, const float* k, const float* v, float* out,
                                  const uint32_t* seg_offset, const uint32_t* seg_pos, int64_t max_seq, int64_t rows,
                                  int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t window, void* stream);

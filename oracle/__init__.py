@@ -63,6 +63,8 @@ def lib():
         L.oracle_rope_tree.argtypes = [_f32p, _u32p, _i64, _i32, _i32, _f32p, _f32p]
         L.oracle_attention_tree.argtypes = [_f32p, _f32p, _f32p, _f32p, _u32p, _u32p, _i64, _i64, _i32, _i32,
                                             _i32, _i32]
+        L.oracle_attention_generic.argtypes = [_f32p, _f32p, _f32p, _f32p, _u32p, _u32p, _i64, _i32, _i32, _i32,
+                                               _i32]
         L.oracle_default_tie_eps.restype = ctypes.c_float
         L.oracle_num_threads.restype = ctypes.c_int
         L.oracle_set_num_threads.argtypes = [ctypes.c_int]
@@ -407,6 +409,18 @@ def rope_tree(x: np.ndarray, row_pos, heads: int, head_dim: int, cos: np.ndarray
     pos = _c(row_pos, np.uint32)
     lib().oracle_rope_tree(y, pos, pos.shape[0], heads, head_dim, _c(cos, np.float32), _c(sin, np.float32))
     return y
+
+
+def attention_generic(q, k, v, seg_offset, seg_pos, q_heads: int, kv_heads: int, head_dim: int,
+                      window_max: int = SLIDING_WINDOW) -> np.ndarray:
+    """Packed-sequence attention for head layouts other than GQA-4 (reference
+    k_attention, src/tensor.cu:2209-2274); out [rows, q_heads * head_dim]."""
+    pos = _c(seg_pos, np.uint32)
+    rows = pos.shape[0]
+    out = np.empty((rows, q_heads * head_dim), np.float32)
+    lib().oracle_attention_generic(_c(q, np.float32), _c(k, np.float32), _c(v, np.float32), out,
+                                   _c(seg_offset, np.uint32), pos, rows, q_heads, kv_heads, head_dim, window_max)
+    return out
 
 
 def attention_tree(q, k, v, row_pos, anc, anc_stride: int, q_heads: int, kv_heads: int, head_dim: int,

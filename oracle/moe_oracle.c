@@ -580,6 +580,66 @@ ORACLE_API void oracle_attention_tree(const float* q, const float* k, const floa
     }
 }
 
+/* Packed-sequence attention for head layouts other than GQA-4 (reference
+ * k_attention, src/tensor.cu:2209-2274, launched by attention_gpu :3316-3340
+ * when q_heads != 4 kv_heads).  Row r sits at position seg_pos[r] of the
+ * sequence starting at row seg_offset[r]; its keys are rows seg_offset[r] +
+ * begin .. seg_offset[r] + pos, begin = max(0, pos + 1 - window_max).  Per
+ * (row, query head qh), kv head kh = qh / (q_heads / kv_heads):
+ *   s_w = (fma chain over d ascending of q[d] k_w[d], from +0) * scale,
+ *         scale = 1 / sqrtf(head_dim)
+ *   m = fmaxf over w from -FLT_MAX;  e_w = (float)exp((double)(s_w - m))
+ *   den = fp32 sum of e_w, w ascending;  p_w = e_w / den
+ *   out[d] = fma chain over w ascending of p_w v_w[d]
+ * (The GQA-4 kernel scores with four partial sums instead, see
+ * oracle_attention_tree.) */
+ORACLE_API void oracle_attention_generic(const float* q, const float* k, const float* v, float* out,
+                                         const uint32_t* seg_offset, const uint32_t* seg_pos, int64_t rows,
+                                         int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t window_max) {
+    volatile float root = sqrtf((float)head_dim);
+    const float scale = 1.0f / root;
+    const int32_t group = q_heads / kv_heads;
+#pragma omp parallel
+    {
+        float* e = (float*)malloc(sizeof(float) * (size_t)(window_max > 0 ? window_max : 1));
+#pragma omp for schedule(dynamic, 4)
+        for (int64_t row = 0; row < rows; ++row) {
+            const int64_t pos = seg_pos[row];
+            const int64_t begin = pos + 1 > window_max ? pos + 1 - window_max : 0;
+            const int64_t window = pos - begin + 1;
+            const int64_t first = (int64_t)seg_offset[row] + begin;
+            for (int32_t qh = 0; qh < q_heads; ++qh) {
+                const int32_t kh = qh / group;
+                const float* qv = q + (row * q_heads + qh) * (int64_t)head_dim;
+                float m = -3.402823466e+38F;
+                for (int64_t w = 0; w < window; ++w) {
+                    const float* kv = k + ((first + w) * kv_heads + kh) * (int64_t)head_dim;
+                    float a = 0.0f;
+                    for (int32_t d = 0; d < head_dim; ++d) a = fmaf(qv[d], kv[d], a);
+                    volatile float sw = a * scale;
+                    e[w] = sw;
+                    m = fmaxf(m, e[w]);
+                }
+                float den = 0.0f;
+                for (int64_t w = 0; w < window; ++w) {
+                    volatile float t = e[w] - m;
+                    e[w] = (float)exp((double)t);
+                    den += e[w];
+                }
+                for (int64_t w = 0; w < window; ++w) e[w] = e[w] / den;
+                float* o = out + (row * q_heads + qh) * (int64_t)head_dim;
+                for (int32_t d = 0; d < head_dim; ++d) {
+                    float val = 0.0f;
+                    for (int64_t w = 0; w < window; ++w)
+                        val = fmaf(e[w], v[((first + w) * kv_heads + kh) * (int64_t)head_dim + d], val);
+                    o[d] = val;
+                }
+            }
+        }
+        free(e);
+    }
+}
+
 /* Linear layer, GPU-path semantics: src/layer.cu:30-42 (Linear::forward) ->
  * src/tensor.cu:3120-3143 (matmul_transposed_bias_gpu) -> k_matmul_transposed_8x8
  * (src/tensor.cu:715-800): y[t][n] = (fp32 FMA chain over k ascending of

@@ -467,6 +467,19 @@ int main(int argc, char** argv) {
             }
         expect(worst < 3e-5 && worst0 < 3e-5, "split-bf16 Linear within 3e-5 of the fp32 chain");
         expect(differs, "the split-bf16 path ran (results differ from the fp32 chain in some bits)");
+        // the fp32 device copy was released after packing (as the reference);
+        // the host copy is intact and a device read uploads it again
+        bool host_same = true;
+        for (std::size_t j = 0; j < n; ++j)
+            for (std::size_t q = 0; q < k; ++q) host_same = host_same && lw_tc.at(j, q) == lw.at(j, q);
+        expect(host_same, "host fp32 copy intact after packing");
+        std::vector<float> back(n * k);
+        expect(hipMemcpy(back.data(), lw_tc.cuda_data(), n * k * sizeof(float), hipMemcpyDeviceToHost) == hipSuccess,
+               "hipMemcpy of the uploaded weight");
+        bool dev_same = true;
+        for (std::size_t j = 0; j < n; ++j)
+            for (std::size_t q = 0; q < k; ++q) dev_same = dev_same && back[j * k + q] == lw.at(j, q);
+        expect(dev_same, "fp32 device copy uploaded again after packing");
         Tensor moved = std::move(lw_tc);
         expect(moved.has_cuda_bf16_weight() && !lw_tc.has_cuda_bf16_weight(), "a move carries the bf16 copy");
         Tensor v3({4});

@@ -102,6 +102,90 @@ def test_attention_against_fp64(window):
     assert np.abs(out - want).max() < 1e-5 * max(1.0, np.abs(want).max())
 
 
+def packed_inputs(lens, q_heads, kv_heads, hd, seed):
+    """Packed sequences of the given lengths: q, k, v and each row's segment
+    start and position."""
+    rows = int(sum(lens))
+    seg_offset = np.concatenate([np.full(n, int(sum(lens[:i])), np.uint32) for i, n in enumerate(lens)])
+    seg_pos = np.concatenate([np.arange(n, dtype=np.uint32) for n in lens])
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((rows, q_heads * hd)).astype(np.float32)
+    k = rng.standard_normal((rows, kv_heads * hd)).astype(np.float32)
+    v = rng.standard_normal((rows, kv_heads * hd)).astype(np.float32)
+    return q, k, v, seg_offset, seg_pos
+
+
+@pytest.mark.parametrize("q_heads,kv_heads,hd,window", [(4, 4, 64, 2047), (8, 1, 128, 5), (6, 3, 80, 2047),
+                                                        (3, 1, 32, 2)])
+def test_attention_generic_against_fp64(q_heads, kv_heads, hd, window):
+    """The generic-layout attention oracle (reference k_attention) against a
+    float64 softmax attention over each row's own sequence prefix: pins the
+    head mapping kh = qh / (q_heads / kv_heads), the segment indexing and the
+    sliding window (a head or segment mix-up is far off)."""
+    lens = [7, 1, 12, 3]
+    q, k, v, off, pos = packed_inputs(lens, q_heads, kv_heads, hd, seed=q_heads + hd)
+    out = oracle.attention_generic(q, k, v, off, pos, q_heads, kv_heads, hd, window)
+    anc = np.zeros((q.shape[0], max(lens)), np.uint32)
+    for r in range(q.shape[0]):
+        anc[r, :pos[r] + 1] = off[r] + np.arange(pos[r] + 1)
+    want = fp64_attention(q, k, v, pos, anc, q_heads, kv_heads, hd, window)
+    assert np.abs(out - want).max() < 1e-5 * max(1.0, np.abs(want).max())
+    # a plausible mistake -- the keys of the whole packed batch instead of the
+    # row's own sequence -- is far off
+    anc_all = np.zeros_like(anc)
+    for r in range(q.shape[0]):
+        b = max(0, r + 1 - max(lens))
+        anc_all[r, :min(r + 1, max(lens))] = np.arange(b, r + 1)[-max(lens):]
+    wrong = fp64_attention(q, k, v, np.minimum(np.arange(q.shape[0]), max(lens) - 1).astype(np.uint32), anc_all,
+                           q_heads, kv_heads, hd, window)
+    assert np.abs(out - wrong).max() > 1e-2
+
+
+def test_attention_generic_closed_forms():
+    """Exact cases: a row's first position attends to itself alone (p = 1, out
+    = v); with q = 0 every score is 0, e = 1, den = n, so p = RN(1 / n) and
+    the output is the fma chain of RN(1 / n) v_w; a value outside the window
+    does not reach the row."""
+    hd = 48
+    q, k, v, off, pos = packed_inputs([5, 3], 2, 2, hd, seed=9)
+    out = oracle.attention_generic(q, k, v, off, pos, 2, 2, hd, 2047)
+    assert np.array_equal(out[0].view(np.uint32), v[0].view(np.uint32))       # row 0 of sequence 0
+    assert np.array_equal(out[5].view(np.uint32), v[5].view(np.uint32))       # row 0 of sequence 1
+    qz = np.zeros_like(q)
+    out = oracle.attention_generic(qz, k, v, off, pos, 2, 2, hd, 2047)
+    r = 4                                                                      # position 4: keys 0..4
+    p = np.float32(1.0) / np.float32(5.0)
+    want = np.zeros(2 * hd, np.float32)
+    for w in range(5):
+        want = (np.float64(p) * v[w].astype(np.float64) + want.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(out[r].view(np.uint32), want.view(np.uint32))
+    vb = v.copy()
+    vb[0] = 1e30                                                               # outside row 4's window of 2
+    a = oracle.attention_generic(q, k, v, off, pos, 2, 2, hd, 2)
+    b = oracle.attention_generic(q, k, vb, off, pos, 2, 2, hd, 2)
+    assert np.array_equal(a[2:5].view(np.uint32), b[2:5].view(np.uint32))
+
+
+def test_attention_generic_scores_are_one_chain_over_d():
+    """The generic kernel scores with ONE fma chain over d (reference
+    k_attention), not the GQA-4 kernel's four partial sums: with q . k terms
+    (1e8, 1, -1e8, 1) the chain gives 1 (1e8 + 1 rounds to 1e8, the
+    cancellation leaves the last 1) and the partial sums
+    (1e8 + 1) + (-1e8 + 1) give 0.  Row 1 attends to key 0 (that score) and
+    key 1 (score 0)."""
+    hd = 4
+    q = np.zeros((2, hd), np.float32)
+    k = np.zeros((2, hd), np.float32)
+    q[1] = [1e8, 1.0, -1e8, 1.0]
+    k[0] = [1.0, 1.0, 1.0, 1.0]
+    v = np.array([[1.0, 0.0, 0.0, 0.0], [0.0, 1.0, 0.0, 0.0]], np.float32)
+    out = oracle.attention_generic(q, k, v, np.zeros(2, np.uint32), np.array([0, 1], np.uint32), 1, 1, hd, 2047)
+    s0 = 1.0 / np.sqrt(hd)
+    p0 = np.exp(s0) / (np.exp(s0) + 1.0)
+    assert abs(out[1, 0] - p0) < 1e-6 and abs(out[1, 1] - (1 - p0)) < 1e-6
+    assert abs(out[1, 0] - 0.5) > 0.05           # the four-partial score (0) would give 1/2
+
+
 def test_attention_tree_equals_token_rows():
     """src/layer.cu:181-185: attention on the trie nodes equals attention on
     the packed token rows (each token its own row, its keys the rows of its

@@ -174,6 +174,41 @@ def test_attention_packed_long_sequences_bit_exact(gpu_device, window):
     np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("q_heads,kv_heads,hd,window", [(4, 4, 128, 2047), (8, 1, 64, 2047), (6, 3, 80, 5),
+                                                        (16, 2, 128, 300), (3, 1, 1, 2047)])
+def test_attention_packed_other_head_layouts_bit_exact(gpu_device, q_heads, kv_heads, hd, window):
+    """aps_attention_packed for head layouts other than GQA-4 (multi-head,
+    multi-query, 2:1 and 8:1 groups; head_dim 1 to 128), the reference's
+    generic k_attention: every row against the oracle bit for bit, on
+    sequences of 700, 64, 5 and 1 tokens, with infinities in some value rows
+    outside every window of 5 keys."""
+    from aps2026_amd import capi
+    from aps2026_amd.moe import _ptr, _stream
+    note(f"attention packed generic q_heads={q_heads} kv_heads={kv_heads} hd={hd} window={window}")
+    lens = [700, 64, 5, 1]
+    rows, stride = sum(lens), max(lens)
+    off = np.repeat(np.cumsum([0] + lens[:-1]), lens).astype(np.uint32)
+    pos = np.concatenate([np.arange(n) for n in lens]).astype(np.uint32)
+    rng = np.random.default_rng(q_heads * 100 + hd)
+    q = rng.standard_normal((rows, q_heads * hd)).astype(np.float32)
+    k = rng.standard_normal((rows, kv_heads * hd)).astype(np.float32)
+    v = rng.standard_normal((rows, kv_heads * hd)).astype(np.float32)
+    if window == 5:
+        v[10:20] = np.inf          # rows 10..19 of the first sequence: only rows up to 24 see them
+    qd, kd, vd = dev(q, gpu_device), dev(k, gpu_device), dev(v, gpu_device)
+    out = torch.full((rows, q_heads * hd), float("nan"), dtype=torch.float32, device=gpu_device)
+    od, pd = dev(off.view(np.int32), gpu_device), dev(pos.view(np.int32), gpu_device)
+    rc = capi.lib().aps_attention_packed(_ptr(qd), _ptr(kd), _ptr(vd), _ptr(out), _ptr(od), _ptr(pd), stride, rows,
+                                         q_heads, kv_heads, hd, window, _stream(qd.device))
+    assert rc == 0, capi.last_error()
+    torch.cuda.synchronize()
+    want = oracle.attention_generic(q, k, v, off, pos, q_heads, kv_heads, hd, window)
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    if window == 5:
+        assert np.isfinite(got[25:]).all()
+
+
 @pytest.mark.parametrize("window", [2047, 5])
 def test_attention_excluded_keys_take_no_part(gpu_device, window):
     """Precondition of the path-group kernel: value rows are finite.  A key
@@ -262,6 +297,41 @@ def test_linear_bit_exact(gpu_device, rows, k, n, bias):
     torch.cuda.synchronize()
     want = oracle.linear(x, w, b)
     np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,k,n,bias,offset", [(13, 37, 5, True, 0), (1, 1, 1, False, 0), (70, 17, 131, True, 0),
+                                                  (65, 4096, 6, True, 1), (200, 48, 20, True, 1),
+                                                  (3, 300, 65, False, 3), (130, 15, 64, True, 0)])
+def test_linear_general_shapes_bit_exact(gpu_device, rows, k, n, bias, offset):
+    """aps_linear on shapes the vector and matrix-core kernels do not take
+    (k % 16 != 0, n % 4 != 0, or arrays 4- but not 16-byte aligned: `offset`
+    floats into a buffer), the reference's tiled fallback: bit for bit
+    against the oracle's chain.  Row 0 of x is zero, so its products are
+    zeros of both signs: its sums must come out +0, as the chain gives,
+    through the zero-padded k steps too."""
+    note(f"linear general rows={rows} k={k} n={n} bias={bias} offset={offset}")
+    rng = np.random.default_rng(rows * 7 + k + n)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    w = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+    x[0] = 0.0
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32) if bias else None
+
+    def placed(a):
+        buf = torch.full((a.size + offset,), float("nan"), dtype=torch.float32, device=gpu_device)
+        buf[offset:] = torch.from_numpy(a.ravel()).to(gpu_device)
+        return buf[offset:]
+
+    from aps2026_amd import capi
+    from aps2026_amd.moe import _ptr, _stream
+    xd, wd = placed(x), placed(w)
+    bd = placed(b) if bias else None
+    y = placed(np.full((rows, n), np.nan, np.float32))
+    rc = capi.lib().aps_linear(_ptr(xd), _ptr(wd), _ptr(bd) if bias else None, rows, k, n, _ptr(y),
+                               _stream(xd.device))
+    assert rc == 0, capi.last_error()
+    torch.cuda.synchronize()
+    want = oracle.linear(x, w, b)
+    np.testing.assert_array_equal(y.cpu().numpy().reshape(rows, n).view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("rows,k,ns,bias", [(10240 // 20, 4096, (512, 512), (True, True)),
