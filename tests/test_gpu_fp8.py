@@ -280,19 +280,20 @@ def every_bf16_rows(exps, per=4095):
     return np.stack(rows)
 
 
-@pytest.mark.parametrize("T", [613, 8192])
-def test_router_x_quantisation_every_bf16_value(gpu_device, T):
+@pytest.mark.parametrize("T,E", [(613, 16), (8192, 16), (300, 3)])
+def test_router_x_quantisation_every_bf16_value(gpu_device, T, E):
     """The fused forward's router writes x's e4m3 codes and row scales (fp8
     weights, bf16 x, hidden 4096, 16 experts): on rows holding every finite
     bf16 value at 33 row scales (subnormal scales, the IEEE-division range
     below 2^-89, up to 2^127), plus an all-zero row, both must equal the
     oracle's quantiser bit for bit.  613 rows run 16-token workgroups, 8192
-    (the rows repeated) the 32-token ones."""
+    (the rows repeated) the 32-token ones; 3 experts leave 13 padding lanes
+    in every token's row."""
     exps = list(range(-133, -120, 3)) + list(range(-92, -76, 2)) + list(range(-60, 128, 7))
     x = np.concatenate([every_bf16_rows(exps), np.zeros((1, 4096), np.float32)])
     x = np.resize(x, (T, 4096))
-    note(f"router x quantisation: T={T} rows of every bf16 value at {len(exps)} scales")
-    inp = synth.make_moe_inputs(T=16, dtype="fp8", seed=5)
+    note(f"router x quantisation: T={T} E={E} rows of every bf16 value at {len(exps)} scales")
+    inp = synth.make_moe_inputs(T=16, E=E, dtype="fp8", seed=5)
     w = fp8_weights(inp, gpu_device)
     xd = to_dev_bf16(synth.f32_to_bf16_bits(x), gpu_device)
     gate = torch.from_numpy(inp.gate).to(gpu_device)
