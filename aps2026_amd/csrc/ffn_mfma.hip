@@ -1444,11 +1444,34 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
             wait_vm_lgkm0_n(g3 + 1 < nstages && g3 + 3 < nstages ? 4 : 0);
         }
         if (kOverlap) raw_barrier();  // every thread has read the previous tile out of the stage
+        // Column fragment by column fragment (32 columns, both row
+        // fragments): its LDS reads (fp8 column scales, FOLD 2's slot-0
+        // values) are issued before the previous fragment's stores, so that
+        // waiting for them does not wait for those stores (LDS operations
+        // complete in order: read, store, read, store would cost one LDS
+        // round trip per four columns).
+        float4 sc4[2][4];
+        u32x2_t ya4[2][2][4];
+        auto epi_reads = [&](int j, float4 (&sc)[4], u32x2_t (&ya)[2][4]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int row = aR + i * 32 + (lane & 31);
+            for (int q = 0; q < 4; ++q) {
+                const int col = 32 * j + 8 * q + 4 * (lane >> 5);
+                if constexpr (kFp8) sc[q] = *reinterpret_cast<const float4*>(lds.scl + ui * 128 + col);
+                if constexpr (FOLD == 2) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+                    for (int i = 0; i < 2; ++i)
+                        ya[i][q] = *reinterpret_cast<const u32x2_t*>(stage + (aR + i * 32 + (lane & 31)) * kArPitch + col);
+                }
+            }
+        };
+        epi_reads(0, sc4[0], ya4[0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j + 1 < 4) epi_reads(j + 1, sc4[(j + 1) & 1], ya4[(j + 1) & 1]);
+            const float4 (&sc)[4] = sc4[j & 1];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = aR + i * 32 + (lane & 31);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     float o[4];
@@ -1456,17 +1479,17 @@ k_ffn_down_ar(const uint8_t* __restrict__ act, int64_t act_row_bytes, const uint
                     for (int v = 0; v < 4; ++v) o[v] = acc[i][j][4 * q + v];
                     const int col = 32 * j + 8 * q + 4 * (lane >> 5);
                     if constexpr (kFp8) {
-                        const float4 a = *reinterpret_cast<const float4*>(lds.scl + ui * 128 + col);
-                        o[0] = o[0] * rs[i] * a.x; o[1] = o[1] * rs[i] * a.y;
-                        o[2] = o[2] * rs[i] * a.z; o[3] = o[3] * rs[i] * a.w;
+                        o[0] = o[0] * rs[i] * sc[q].x; o[1] = o[1] * rs[i] * sc[q].y;
+                        o[2] = o[2] * rs[i] * sc[q].z; o[3] = o[3] * rs[i] * sc[q].w;
                     }
                     u32x2_t* at = reinterpret_cast<u32x2_t*>(stage + row * kArPitch + col);
                     const u32x2_t v = {pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
                     // FOLD 2: this row's slot-1 output (bf16, as y would hold
                     // it) combined with the token's slot-0 row in the stage
-                    if constexpr (FOLD == 2) *at = combine4_bf16(*at, v);
+                    if constexpr (FOLD == 2) *at = combine4_bf16(ya4[j & 1][i][q], v);
                     else *at = v;
                 }
+            }
         }
         wait_lgkm0();
         raw_barrier();
