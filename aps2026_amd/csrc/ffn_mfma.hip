@@ -721,15 +721,42 @@ __device__ inline void up_piece(Ring3& ring, const uint8_t* __restrict__ x, int6
     const int gcol0 = (u.cb0 + (NJ == 4 ? wn : 0)) * 64 + (NJ == 4 ? 0 : 32 * hc);  // wave's first act column
     const int lcol0 = NJ == 4 ? wn * 64 : (Sh::WN == 2 ? wn * 32 : 0);             // ... within the piece
     const int c0 = u.expert * F + gcol0;      // its gate/up scale index (fp8)
+    // fp8: every scale the epilogue needs is loaded first (the x row scales,
+    // the w1 and w3 column scales), so that they cost one memory round
+    // trip, not one per 4-column group
+    typedef float ep_f32x4_t __attribute__((ext_vector_type(4)));
+    float rsv[MI];
+    ep_f32x4_t a1v[NJ / 2][4], a3v[NJ / 2][4];
+    if constexpr (kFp8) {
+        uint32_t ar[MI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            uint32_t p = u.m0 + aR + i * 32 + (lane & 31);
+            p = p < u.end ? p : u.end - 1;
+            ar[i] = assignment_rows[p];
+        }
+#pragma unroll
+        for (int j = 0; j < NJ / 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int sc_at = c0 + 32 * j + 8 * q + 4 * (lane >> 5);
+                a1v[j][q] = *reinterpret_cast<const ep_f32x4_t*>(s1 + sc_at);
+                a3v[j][q] = *reinterpret_cast<const ep_f32x4_t*>(s3 + sc_at);
+            }
+#pragma unroll
+        for (int i = 0; i < MI; ++i) rsv[i] = sx[ar[i]];
+        // the values pass through empty asm statements: the compiler then
+        // issues every load here (it had placed each pair of column-scale
+        // loads next to its use, each followed by a vmcnt(0) wait)
+#pragma unroll
+        for (int j = 0; j < NJ / 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(a1v[j][q]), "+v"(a3v[j][q]));
+    }
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
         const int row = aR + i * 32 + (lane & 31);
-        float rs = 1.0f;
-        if constexpr (kFp8) {
-            uint32_t p = u.m0 + row;
-            p = p < u.end ? p : u.end - 1;
-            rs = sx[assignment_rows[p]];
-        }
+        const float rs = kFp8 ? rsv[i] : 1.0f;
 #pragma unroll
         for (int j = 0; j < NJ / 2; ++j)
 #pragma unroll
@@ -741,7 +768,7 @@ __device__ inline void up_piece(Ring3& ring, const uint8_t* __restrict__ x, int6
                     up[v] = acc[i][j + NJ / 2][4 * q + v];
                 }
                 if constexpr (kFp8) {
-                    const float4 a1 = col_scales(s1, c0, j, q, lane), a3 = col_scales(s3, c0, j, q, lane);
+                    const ep_f32x4_t a1 = a1v[j][q], a3 = a3v[j][q];
                     g[0] = g[0] * rs * a1.x; g[1] = g[1] * rs * a1.y; g[2] = g[2] * rs * a1.z; g[3] = g[3] * rs * a1.w;
                     up[0] = up[0] * rs * a3.x; up[1] = up[1] * rs * a3.y; up[2] = up[2] * rs * a3.z; up[3] = up[3] * rs * a3.w;
                 }
