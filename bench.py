@@ -60,7 +60,7 @@ COPY_PROBE_BYTES = 256 << 20
 # the counter reads for the 256 MiB copy probe: FETCH_SIZE 131088.7 KiB
 # (x 1.9997), WRITE_SIZE 262144 KiB (x 1.0).  Summary and commands:
 # profiles/moe_forward_hbm_traffic.md.  Re-measure when a GEMM kernel changes.
-TRAFFIC_KIB = {"c2": (116967.1, 7168.0), "c5": (95136.2, 14336.0)}
+TRAFFIC_KIB = {"c2": (116972.0, 7168.0), "c5": (94700.5, 14336.0)}
 FETCH_SCALE, WRITE_SCALE = 262144.0 / 131088.7, 1.0
 
 
