@@ -1,7 +1,8 @@
 """The allocation-free forward (aps_moe_forward_noalloc) through the C ABI:
 its output equals aps_moe_forward's with a caller workspace bit for bit, on
 two calls in a row with the second batch smaller than the first (the static
-scratch keeps the first call's bytes), for a bf16 and an fp32 weight set;
+scratch keeps the first call's bytes), for a bf16, an fp32 and an fp8 weight
+set (the fp8 one runs the folded combine and the router's x quantisation);
 a batch past the scratch is refused with APS_ERR_WORKSPACE."""
 import ctypes
 import sys
@@ -21,6 +22,15 @@ def note(msg):
 
 
 def _weights(inp, dev):
+    if inp.dtype == "fp8":
+        codes, scales = [], []
+        for nm in ("w1", "w2", "w3"):
+            c = torch.from_numpy(inp.packed[nm + "_e4m3"]).to(dev)
+            sc = torch.from_numpy(inp.packed[nm + "_scale"]).to(dev)
+            codes.append([c[e].contiguous() for e in range(inp.E)])
+            scales.append([sc[e].contiguous() for e in range(inp.E)])
+        return moe.register_moe_weights_gpu(codes[0], codes[1], codes[2], compute_dtype=moe.FP8,
+                                            scales=(scales[0], scales[1], scales[2]))
     lists = []
     for nm in ("w1", "w2", "w3"):
         if inp.dtype == "bf16":
@@ -33,12 +43,12 @@ def _weights(inp, dev):
 
 
 def _x(inp, dev):
-    if inp.dtype == "bf16":
+    if inp.dtype in ("bf16", "fp8"):
         return torch.from_numpy(inp.packed["x_bf16"].view(np.int16)).to(dev).view(torch.bfloat16)
     return torch.from_numpy(inp.x).to(dev)
 
 
-@pytest.mark.parametrize("dtype,sizes", [("bf16", (4096, 300)), ("f32", (512, 77))])
+@pytest.mark.parametrize("dtype,sizes", [("bf16", (4096, 300)), ("f32", (512, 77)), ("fp8", (3000, 129))])
 def test_forward_noalloc_equals_workspace_forward(gpu_device, dtype, sizes):
     L = capi.lib()
     T0 = sizes[0]
@@ -47,8 +57,8 @@ def test_forward_noalloc_equals_workspace_forward(gpu_device, dtype, sizes):
     w = _weights(inp, gpu_device)
     x_all = _x(inp, gpu_device)
     gate = torch.from_numpy(inp.gate).to(gpu_device)
-    code = capi.DTYPE_BF16 if dtype == "bf16" else capi.DTYPE_F32
-    out_dt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    code = capi.DTYPE_F32 if dtype == "f32" else capi.DTYPE_BF16   # fp8 weights take bf16 x and output
+    out_dt = torch.float32 if dtype == "f32" else torch.bfloat16
     stream = ctypes.c_void_p(torch.cuda.current_stream(gpu_device).cuda_stream)
     for T in sizes:
         note(f"forward_noalloc {dtype} T={T}")
@@ -60,8 +70,8 @@ def test_forward_noalloc_equals_workspace_forward(gpu_device, dtype, sizes):
                                        code, stream)
         assert rc == capi.APS_OK, capi.last_error()
         torch.cuda.synchronize()
-        assert torch.equal(got.view(torch.int16 if dtype == "bf16" else torch.int32),
-                           want.view(torch.int16 if dtype == "bf16" else torch.int32))
+        assert torch.equal(got.view(torch.int32 if dtype == "f32" else torch.int16),
+                           want.view(torch.int32 if dtype == "f32" else torch.int16))
     # past the scratch: refused before any launch
     big = L.aps_moe_noalloc_scratch_bytes() // (2 * H) + 1
     rc = L.aps_moe_forward_noalloc(w.handle, ctypes.c_void_p(x_all.data_ptr()), code,
