@@ -440,6 +440,21 @@ int main(int argc, char** argv) {
             "attention_tree_gpu expects GQA-4", "GQA-4 check");
     }
 
+    // --- packed attention in another head layout (4 heads of 64, one KV
+    //     head each): the reference's generic kernel -----------------------
+    {
+        const std::vector<std::size_t> lens = {5, 3, 1};
+        const std::size_t rows = 9, heads = 4, hd = 64;
+        Tensor pq = random_tensor({rows, heads * hd}, rng, 1.0f), pk = random_tensor({rows, heads * hd}, rng, 1.0f),
+               pv = random_tensor({rows, heads * hd}, rng, 1.0f);
+        write_raw(dir, "mha_q", pq);
+        write_raw(dir, "mha_k", pk);
+        write_raw(dir, "mha_v", pv);
+        Tensor po({rows, heads * hd});
+        tensor_ops::attention_gpu(pq, pk, pv, po, lens, heads, heads, hd);
+        write_raw(dir, "mha_out", po);
+    }
+
     // --- the split-bf16 Linear (Tensor::prepare_cuda_bf16_weight) ------------
     {
         const std::size_t m = 70, k = 256, n = 132;

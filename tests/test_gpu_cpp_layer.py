@@ -168,6 +168,20 @@ def test_tree_attention_ops_bit_exact(run):
     assert np.array_equal(ld("attn_out", 2048).view(np.uint32), want.view(np.uint32))
 
 
+def test_packed_attention_other_head_layout_bit_exact(run):
+    """tensor_ops::attention_gpu through the C++ API with 4 query heads over
+    4 KV heads of 64 (not GQA-4: the reference's generic kernel) on packed
+    sequences of 5, 3 and 1 tokens: equal to the oracle bit for bit."""
+    d = run["dir"]
+    ld = lambda name: np.fromfile(d / f"{name}.f32", dtype=np.float32).reshape(9, 256)
+    q, k, v = ld("mha_q"), ld("mha_k"), ld("mha_v")
+    lens = [5, 3, 1]
+    off = np.repeat(np.cumsum([0] + lens[:-1]), lens).astype(np.uint32)
+    pos = np.concatenate([np.arange(n) for n in lens]).astype(np.uint32)
+    want = oracle.attention_generic(q, k, v, off, pos, 4, 4, 64)
+    assert np.array_equal(ld("mha_out").view(np.uint32), want.view(np.uint32))
+
+
 # The model mode of the check program: a two-layer model (hidden 512, 16
 # experts of 128, vocabulary 96, the reference's 16 query / 4 KV heads of
 # 128) written as a model.bin, built from PhiDecoderLayer(loader, i) parts.
