@@ -11,9 +11,10 @@
 // Here each wave owns one tile:
 //   1. lane e sums expert e's counts over all tiles (total) and over the
 //      tiles before its own (prefix) -- a handful of L2-resident loads;
-//   2. a wave scan over lanes turns totals into offsets;
-//   3. for each expert, one 64-bit ballot + mbcnt-style popcount gives every
-//      lane its stable rank inside the tile.
+//   2. one pass over the experts, each expert's figures read from its lane
+//      into scalar registers, scans the totals into offsets, and
+//   3. in the same pass one 64-bit ballot + mbcnt-style popcount per expert
+//      gives every lane its stable rank inside the tile.
 // Every (token, slot) is written exactly once, by the wave that owns the
 // token, so the scatter is O(T) work instead of the reference's O(E*T).
 //
@@ -156,28 +157,12 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
             }
         }
     }
-    // 2. exclusive scan of totals over lanes 0..E-1
-    uint32_t incl = total;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t v = __shfl_up(incl, d);
-        if (lane >= d) incl += v;
-    }
-    const uint32_t excl = incl - total;
-    const uint32_t base = excl + before;
-    if (tile == 0 && lane < E) {
-        counts[lane] = total;
-        offsets[lane] = excl;
-        if (lane == E - 1) offsets[E] = incl;
-        if constexpr (SLOTS) slot1[lane] = excl + total0;
-    }
-    // SLOTS: list index of this tile's first slot-0 / slot-1 route of each
-    // expert (lane e)
-    const uint32_t lbase0 = excl + before0;
-    const uint32_t lbase1 = excl + total0 + (before - before0);
-
-    // 3. stable rank of each lane's (token, slot) pairs inside this tile, per
-    //    expert: the pairs of lower lanes come first, slot 0 before slot 1
+    // 2./3. one pass over the experts, with expert e's figures read from
+    //    lane e into scalar registers (v_readlane: no LDS round trip, unlike
+    //    a shuffle): `run` is the exclusive scan of the totals, the offset
+    //    of expert e; a ballot per slot and a popcount below the lane give
+    //    each lane's stable rank inside the tile, the pairs of lower lanes
+    //    first and slot 0 before slot 1.
     int first = 255, second = 255;
     if (t < rows) {
         first = r0;
@@ -186,19 +171,35 @@ k_dispatch_scatter(const uint8_t* __restrict__ routes, const uint32_t* __restric
         if (status && bad) atomicAdd(status, static_cast<uint32_t>(bad));
     }
     const uint64_t below = (1ull << lane) - 1ull;
-    uint32_t p0 = 0, p1 = 0, i0 = 0, i1 = 0;
+    uint32_t p0 = 0, p1 = 0, i0 = 0, i1 = 0, excl = 0, run = 0;
     for (int e = 0; e < E; ++e) {
+        const uint32_t tot_e = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(total), e));
+        if (lane == e) excl = run;
         const uint64_t m0 = __ballot(first == e), m1 = __ballot(second == e);
-        if ((m0 | m1) == 0) continue;  // wave-uniform
-        const uint32_t b = __shfl(base, e);
-        const uint32_t r = static_cast<uint32_t>(__popcll(m0 & below) + __popcll(m1 & below));
-        if (first == e) p0 = b + r;
-        if (second == e) p1 = b + r + (first == e ? 1u : 0u);
-        if constexpr (SLOTS) {
-            const uint32_t l0 = __shfl(lbase0, e), l1 = __shfl(lbase1, e);
-            if (first == e) i0 = l0 + static_cast<uint32_t>(__popcll(m0 & below));
-            if (second == e) i1 = l1 + static_cast<uint32_t>(__popcll(m1 & below));
+        if ((m0 | m1) != 0) {  // wave-uniform
+            const uint32_t bef_e = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(before), e));
+            const uint32_t b = run + bef_e;
+            const uint32_t r = static_cast<uint32_t>(__popcll(m0 & below) + __popcll(m1 & below));
+            if (first == e) p0 = b + r;
+            if (second == e) p1 = b + r + (first == e ? 1u : 0u);
+            if constexpr (SLOTS) {
+                // list index of this tile's first slot-0 / slot-1 route of e
+                const uint32_t tot0_e =
+                    static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(total0), e));
+                const uint32_t bef0_e =
+                    static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(before0), e));
+                const uint32_t l0 = run + bef0_e, l1 = run + tot0_e + (bef_e - bef0_e);
+                if (first == e) i0 = l0 + static_cast<uint32_t>(__popcll(m0 & below));
+                if (second == e) i1 = l1 + static_cast<uint32_t>(__popcll(m1 & below));
+            }
         }
+        run += tot_e;
+    }
+    if (tile == 0 && lane < E) {
+        counts[lane] = total;
+        offsets[lane] = excl;
+        if (lane == E - 1) offsets[E] = run;
+        if constexpr (SLOTS) slot1[lane] = excl + total0;
     }
     if (t < rows) {
         assignment_rows[p0] = static_cast<uint32_t>(t);
