@@ -57,11 +57,11 @@ COPY_PROBE_BYTES = 256 << 20
 # HBM bytes per launch of the roofline kernel, from two rocprofv3 counter runs
 # (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch, of `bench.py --config C
 # --steps 3 --warmup 1 --cpu-baseline skip --copy-probe`), each scaled by what
-# the counter reads for the 256 MiB copy probe: FETCH_SIZE 131088.7 KiB
+# the counter reads for the 256 MiB copy probe: FETCH_SIZE 131089.0 KiB
 # (x 1.9997), WRITE_SIZE 262144 KiB (x 1.0).  Summary and commands:
 # profiles/moe_forward_hbm_traffic.md.  Re-measure when a GEMM kernel changes.
-TRAFFIC_KIB = {"c2": (116972.0, 7168.0), "c5": (94700.5, 14336.0)}
-FETCH_SCALE, WRITE_SCALE = 262144.0 / 131088.7, 1.0
+TRAFFIC_KIB = {"c2": (116953.7, 7168.0), "c5": (95038.3, 14336.0)}
+FETCH_SCALE, WRITE_SCALE = 262144.0 / 131089.0, 1.0
 
 
 def parse():
